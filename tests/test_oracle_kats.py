@@ -1,0 +1,353 @@
+"""The C oracle against the reference's own known-answer tests (crates/domain/src/*.rs
+#[cfg(test)] modules, crates/cuda-backend/src/matvec.rs:198-205) and against
+independent numpy restatements, closed forms and invariants.  CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import OracleError
+from adaforge_amd import synth
+from tests import numpy_ref as nr
+
+
+def q4_bytes(rows_blocks):
+    return np.concatenate([np.asarray(b, dtype=np.uint8) for b in rows_blocks])
+
+
+# ---- fp16 ---------------------------------------------------------------------------------------
+
+def test_half_edge_cases_q4_rs_120():
+    assert oracle.half_to_f32(1) == 2.0 ** -24
+    assert oracle.half_to_f32(0x8001) == -(2.0 ** -24)
+    assert oracle.half_to_f32(0xBC00) == -1.0
+    assert oracle.half_to_f32(0x7BFF) == 65504.0
+    assert math.isnan(oracle.half_to_f32(0x7E00))
+
+
+def test_every_half_bit_pattern_matches_numpy():
+    bits = np.arange(65536, dtype=np.uint32)
+    ours = np.array([oracle.half_to_f32(int(b)) for b in bits], dtype=np.float32)
+    ref = bits.astype(np.uint16).view(np.float16).astype(np.float32)
+    finite = np.isfinite(ref)
+    assert finite.sum() == 63488
+    assert np.array_equal(ours[finite].view(np.uint32), ref[finite].view(np.uint32))
+    assert np.array_equal(np.isnan(ours), np.isnan(ref))
+    assert np.array_equal(np.isinf(ours) & (ours > 0), np.isinf(ref) & (ref > 0))
+
+
+def test_f32_to_half_round_to_nearest_even_matches_numpy():
+    h = np.arange(0, 0x7C00, dtype=np.uint32)           # every finite positive half
+    v = h.astype(np.uint16).view(np.float16).astype(np.float32)
+    nxt = (h + 1).astype(np.uint16).view(np.float16).astype(np.float32)
+    mid = ((v.astype(np.float64) + nxt.astype(np.float64)) / 2).astype(np.float32)
+    ulp = np.float32(1) * 0
+    cand = np.concatenate([v, mid, np.nextafter(mid, np.float32(np.inf)), np.nextafter(mid, np.float32(0)),
+                           np.nextafter(v, np.float32(np.inf)), np.float32([65519.9, 65520, 70000, 1e-30, 2.0 ** -25,
+                                                                           3.0 * 2.0 ** -26])])
+    cand = cand[np.isfinite(cand)] + ulp
+    cand = np.concatenate([cand, -cand])
+    ours = np.array([oracle.f32_to_half(float(x)) for x in cand], dtype=np.uint16)
+    with np.errstate(over="ignore"):
+        ref = cand.astype(np.float16).view(np.uint16)
+    bad = np.nonzero(ours != ref)[0]
+    assert bad.size == 0, (cand[bad[:5]], ours[bad[:5]], ref[bad[:5]])
+    # the generator header's converter is the same function, pinned the same way
+    assert all(synth.half(float(x)) == r for x, r in zip(cand[::97], ref[::97]))
+
+
+# ---- Q4_0 ---------------------------------------------------------------------------------------
+
+def test_q4_known_nibbles_scale_sign_and_order_q4_rs_89():
+    b = np.zeros(18, dtype=np.uint8)
+    b[0], b[1] = 0x00, 0x38                              # 0x3800 = 0.5
+    for j in range(16):
+        b[2 + j] = j | ((15 - j) << 4)
+    for column in range(32):
+        x = np.zeros(32, dtype=np.float32)
+        x[column] = 1.0
+        q = column - 8 if column < 16 else 23 - column
+        assert oracle.q4_matvec(b, 32, 1, x).tolist() == [q * 0.5]
+
+
+def test_q4_validation_q4_rs_108():
+    assert not oracle.q4_validate(np.zeros(18, np.uint8), 31, 1)
+    assert not oracle.q4_validate(np.zeros(0, np.uint8), 32, 0)
+    assert not oracle.q4_validate(np.zeros(17, np.uint8), 32, 1)
+    b = np.zeros(18, np.uint8)
+    b[0], b[1] = 0x00, 0x7C
+    assert not oracle.q4_validate(b, 32, 1)
+    assert oracle.q4_validate(np.zeros(18, np.uint8), 32, 1)
+    with pytest.raises(OracleError):
+        oracle.q4_matvec(np.zeros(18, np.uint8), 32, 1, [0.0])
+    with pytest.raises(OracleError):
+        oracle.q4_matvec(np.zeros(18, np.uint8), 32, 1, np.full(32, np.nan, np.float32))
+
+
+@pytest.mark.parametrize("columns,rows", [(32, 1), (96, 5), (384, 7), (3840, 33)])
+def test_q4_matches_numpy_brute_force(columns, rows):
+    w = synth.q4(f"bf{columns}x{rows}", columns, rows)
+    x = synth.normal(f"x{columns}", columns)
+    dense = nr.q4_dequant(w, columns, rows).astype(np.float64)
+    ref = dense @ x.astype(np.float64)
+    got = oracle.q4_matvec(w, columns, rows, x)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+def test_q4_zero_input_linearity_one_hot_and_thread_invariance():
+    columns, rows = 256, 9
+    w = synth.q4("lin", columns, rows)
+    assert np.all(oracle.q4_matvec(w, columns, rows, np.zeros(columns, np.float32)) == 0.0)
+    dense = nr.q4_dequant(w, columns, rows)
+    for c in (0, 15, 16, 31, 200):
+        e = np.zeros(columns, np.float32)
+        e[c] = 1.0
+        assert np.array_equal(oracle.q4_matvec(w, columns, rows, e), dense[:, c].astype(np.float64))
+    a, b = synth.normal("la", columns), synth.normal("lb", columns)
+    s = oracle.q4_matvec(w, columns, rows, a) + oracle.q4_matvec(w, columns, rows, b)
+    np.testing.assert_allclose(oracle.q4_matvec(w, columns, rows, a + b), s, rtol=1e-6, atol=1e-6)
+    x = synth.normal("thr", columns)
+    assert np.array_equal(oracle.q4_matvec(w, columns, rows, x, threads=1), oracle.q4_matvec(w, columns, rows, x,
+                                                                                           threads=7))
+
+
+# ---- Q6_K ---------------------------------------------------------------------------------------
+
+def test_q6_known_constant_row_and_softcap_q6_rs_203():
+    b = np.zeros(210, np.uint8)
+    b[192:208] = 1
+    b[208], b[209] = 0x00, 0x38
+    assert oracle.q6_matvec(b, 256, 1, np.ones(256, np.float32)).tolist() == [-4096.0]
+    with pytest.raises(OracleError):
+        oracle.q6_matvec(b, 256, 1, [1.0])
+    assert not oracle.q6_validate(np.zeros(0, np.uint8), 32, 1)
+    assert oracle.softcap(0.0, 30.0) == 0.0
+    assert oracle.softcap(3000.0, 30.0) == 30.0
+    with pytest.raises(OracleError):
+        oracle.softcap(1.0, 0.0)
+    with pytest.raises(OracleError):
+        oracle.softcap(float("nan"), 30.0)
+
+
+def _known_q6_block():
+    """crates/domain/src/embedding.rs:261-277: code i % 64 packed, sub-scales i - 8, d = 0.5."""
+    b = np.zeros(210, np.uint8)
+    b[208], b[209] = 0x00, 0x38
+    for i in range(256):
+        code = i % 64
+        g, q, l = i // 128, (i % 128) // 32, i % 32
+        b[g * 64 + l + (q % 2) * 32] |= (code & 15) << (0 if q < 2 else 4)
+        b[128 + g * 32 + l] |= (code >> 4) << (q * 2)
+    for i in range(16):
+        b[192 + i] = np.uint8((i - 8) & 0xFF)
+    return b
+
+
+def test_embedding_all_codes_and_signed_subscales_embedding_rs_279():
+    b = _known_q6_block()
+    raw = oracle.embedding(b, 256, 1, [0], scaled=False)
+    for i, v in enumerate(raw):
+        assert v == 0.5 * (i // 16 - 8) * (i % 64 - 32), i
+    scaled = oracle.embedding(b, 256, 1, [0], scaled=True)
+    assert np.array_equal(scaled, raw * np.float32(16.0))
+    with pytest.raises(OracleError):
+        oracle.embedding(b, 255, 1, [0])
+    with pytest.raises(OracleError):
+        oracle.embedding(b, 256, 1, [1])
+    bad = b.copy()
+    bad[208], bad[209] = 0x00, 0x7C
+    with pytest.raises(OracleError):
+        oracle.embedding(bad, 256, 1, [0])
+
+
+def test_q6_matvec_matches_numpy_unpacker_and_embedding_rows():
+    columns, rows = 768, 11
+    w = synth.q6("q6bf", columns, rows)
+    x = synth.normal("q6x", columns)
+    dense = nr.q6_dequant(w, columns, rows)
+    np.testing.assert_allclose(oracle.q6_matvec(w, columns, rows, x), dense.astype(np.float64) @ x.astype(np.float64),
+                               rtol=1e-12, atol=1e-12)
+    rowsel = [0, 5, 10]
+    emb = oracle.embedding(w, columns, rows, rowsel, scaled=False).reshape(3, columns)
+    assert np.array_equal(emb, dense[rowsel])
+    # the known block decodes identically through both unpackers
+    kb = _known_q6_block()
+    assert np.array_equal(nr.q6_dequant(kb, 256, 1)[0], oracle.embedding(kb, 256, 1, [0], scaled=False))
+
+
+# ---- RMSNorm ------------------------------------------------------------------------------------
+
+def test_rmsnorm_known_result_rms_norm_rs_46():
+    y = oracle.rmsnorm([2.0, -3.0], 1.0, [1.0, 1.0, 0.0, 0.0])
+    assert abs(y[0] - 2.0 / math.sqrt(2.0)) < 1e-12
+    assert abs(y[1] + 3.0 / math.sqrt(2.0)) < 1e-12
+    assert y[2:].tolist() == [0.0, 0.0]
+    assert oracle.rmsnorm([0.0], 1e-6, [2.0]).tolist() == [0.0]
+
+
+def test_rmsnorm_rejects_rms_norm_rs_62():
+    for eps in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(OracleError):
+            oracle.rmsnorm([1.0], eps, [1.0])
+    with pytest.raises(OracleError):
+        oracle.rmsnorm(np.zeros(0, np.float32), 1e-6, [1.0])
+    with pytest.raises(OracleError):
+        oracle.rmsnorm([float("nan")], 1e-6, [1.0])
+    for x in ([], [0.0, 0.0], [float("inf")] * 3):
+        with pytest.raises(OracleError):
+            oracle.rmsnorm([1.0] * 3, 1e-6, np.asarray(x, np.float32))
+
+
+def test_rmsnorm_matches_closed_form():
+    w = synth.normal("rw", 3840, 1.0, 0.1)
+    x = synth.normal("rx", 3840 * 3)
+    np.testing.assert_allclose(oracle.rmsnorm(w, 1e-6, x), nr.rmsnorm(w, 1e-6, x), rtol=1e-13, atol=1e-15)
+
+
+# ---- RoPE ---------------------------------------------------------------------------------------
+
+def test_rope_identity_and_known_rotation_rope_rs_158():
+    f = np.ones(2, np.float32)
+    assert oracle.rope(4, 10000.0, f, 100, [1, 2, 3, 4], 0).tolist() == [1.0, 2.0, 3.0, 4.0]
+    y = oracle.rope(4, 10000.0, f, 100, [1, 0, 0, 0], 1)
+    assert abs(y[0] - math.cos(1.0)) < 1e-12 and abs(y[2] - math.sin(1.0)) < 1e-12
+    assert y[1] == 0.0 and y[3] == 0.0
+
+
+def test_rope_norm_and_suppressed_pairs_rope_rs_171():
+    f = np.array([1.0, 1e30], np.float32)
+    y = oracle.rope(4, 1e6, f, 262144, [1, 2, 3, 4], 262143)
+    assert abs((y * y).sum() - 30.0) < 1e-10
+    assert y[1] == 2.0 and y[3] == 4.0
+    with pytest.raises(OracleError):
+        oracle.rope(4, 1e6, f, 262144, [1, 2, 3, 4], 262144)
+
+
+def test_rope_rejects_rope_rs_181():
+    with pytest.raises(OracleError):
+        oracle.rope(3, 10000.0, [1.0], 10, [1, 2, 3], 0)
+    with pytest.raises(OracleError):
+        oracle.rope(4, 1.0, [1.0, 1.0], 10, [1, 2, 3, 4], 0)
+    for factor in (0.0, -1.0, float("nan"), float("inf")):
+        with pytest.raises(OracleError):
+            oracle.rope(4, 10000.0, [factor] * 2, 10, [1, 2, 3, 4], 0)
+    with pytest.raises(OracleError):
+        oracle.rope(4, 10000.0, [1.0] * 2, 10, [float("nan")] * 4, 0)
+    with pytest.raises(OracleError):
+        oracle.rope(4, 10000.0, [1.0] * 2, 10, [0.0] * 3, 0)
+
+
+@pytest.mark.parametrize("base,position", [(1e4, 1), (1e4, 1023), (1e6, 383), (1e6, 32767)])
+def test_rope_matches_complex_rotation(base, position):
+    x = synth.normal(f"rope{base}", 256 * 3)
+    np.testing.assert_allclose(oracle.rope(256, base, np.ones(128, np.float32), 131072, x, position),
+                               nr.rope(256, base, np.ones(128), x, position), rtol=1e-11, atol=1e-11)
+
+
+# ---- attention ----------------------------------------------------------------------------------
+
+def test_attention_masks_future_and_maps_grouped_heads_attention_rs_308():
+    v = [1.0, 10.0, 3.0, 30.0, 999.0, 999.0]
+    assert oracle.attention(4, 2, 1, None, 1.0, [0.0] * 4, [0.0] * 6, v, 3, 1).tolist() == [2.0, 2.0, 20.0, 20.0]
+    assert oracle.attention(4, 2, 1, 1, 1.0, [0.0] * 4, [0.0] * 6, v, 3, 1).tolist() == [3.0, 3.0, 30.0, 30.0]
+
+
+def test_attention_stable_softmax_and_scale_attention_rs_324():
+    assert oracle.attention(1, 1, 1, None, 1.0, [1000.0], [1000.0, 1001.0], [2.0, 3.0], 2, 1).tolist() == [3.0]
+    y = oracle.attention(1, 1, 1, None, 2.0, [1.0], [0.0, 1.0], [0.0, 1.0], 2, 1)[0]
+    assert abs(y - math.exp(2.0) / (1.0 + math.exp(2.0))) < 1e-12
+
+
+def test_attention_rejects_attention_rs_336():
+    assert not oracle.attention_validate(3, 2, 1, None, 1.0)
+    assert oracle.attention_validate(4, 2, 1, None, 1.0)
+    with pytest.raises(OracleError):
+        oracle.attention(1, 1, 1, None, 1.0, [1.0], [1.0], [1.0], 1, 1)
+    with pytest.raises(OracleError):
+        oracle.attention(1, 1, 1, None, 1.0, [float("nan")], [1.0], [1.0], 1, 0)
+
+
+@pytest.mark.parametrize("window,tokens,position", [(None, 40, 39), (16, 40, 39), (16, 40, 7), (None, 1, 0)])
+def test_attention_matches_numpy_softmax(window, tokens, position):
+    qh, kvh, w = 4, 2, 32
+    q = synth.normal("aq", qh * w)
+    k = synth.normal("ak", tokens * kvh * w)
+    v = synth.normal("av", tokens * kvh * w)
+    got = oracle.attention(qh, kvh, w, window, 0.25, q, k, v, tokens, position)
+    ref = nr.attention(qh, kvh, w, window, 0.25, q, k, v, tokens, position)
+    np.testing.assert_allclose(got, ref, rtol=1e-12, atol=1e-12)
+
+
+# ---- output branch, FFN ------------------------------------------------------------------------
+
+def test_attention_output_zero_branch_attention_output_rs_42():
+    out = oracle.attention_output(np.zeros(54, np.uint8), 32, 3, [2.0] * 3, 1e-6, [1.0] * 32, [1.0, -2.0, 3.0])
+    assert out.tolist() == [1.0, -2.0, 3.0]
+    with pytest.raises(OracleError):
+        oracle.attention_output(np.zeros(54, np.uint8), 32, 3, [2.0] * 3, 1e-6, [1.0] * 32, [1.0])
+
+
+def test_gelu_known_values_ffn_rs_159():
+    assert oracle.gelu_tanh(0.0) == 0.0
+    assert abs(oracle.gelu_tanh(1.0) - 0.8411919906082768) < 1e-12
+    assert abs(oracle.gelu_tanh(-1.0) + 0.15880800939172324) < 1e-12
+    xs = np.linspace(-6, 6, 97)
+    np.testing.assert_allclose([oracle.gelu_tanh(x) for x in xs], nr.gelu_tanh(xs), rtol=1e-14, atol=1e-15)
+
+
+def test_ffn_zero_branch_and_scale_ffn_rs_165():
+    z = np.zeros(576, np.uint8)
+    out = oracle.ffn([1.0] * 32, 1e-6, z, z, z, 32, 32, [1.0] * 32, 1e-6, 0.5, [2.0] * 32)
+    assert out.tolist() == [1.0] * 32
+    with pytest.raises(OracleError):
+        oracle.ffn([1.0] * 32, 1e-6, z, z, z, 32, 32, [1.0] * 32, 1e-6, 0.5, [0.0])
+
+
+def test_ffn_and_output_branch_match_numpy_composition():
+    H, I = 256, 512
+    pre, post = synth.normal("fpre", H, 1.0, 0.1), synth.normal("fpost", H, 1.0, 0.1)
+    g, u, d = synth.q4("fg", H, I), synth.q4("fu", H, I), synth.q4("fd", I, H)
+    x = synth.normal("fx", H)
+    n = nr.rmsnorm(pre, 1e-6, x).astype(np.float32)
+    G = (nr.q4_dequant(g, H, I).astype(np.float64) @ n.astype(np.float64)).astype(np.float32)
+    U = (nr.q4_dequant(u, H, I).astype(np.float64) @ n.astype(np.float64)).astype(np.float32)
+    act = nr.gelu_tanh(G.astype(np.float64)).astype(np.float32) * U
+    D = (nr.q4_dequant(d, I, H).astype(np.float64) @ act.astype(np.float64)).astype(np.float32)
+    P = nr.rmsnorm(post, 1e-6, D).astype(np.float32)
+    ref = ((P + x) * np.float32(0.75)).astype(np.float64)
+    got = oracle.ffn(pre, 1e-6, g, u, d, H, I, post, 1e-6, 0.75, x)
+    np.testing.assert_allclose(got, ref, rtol=2e-6, atol=2e-6)
+    got_nopost = oracle.ffn(pre, 1e-6, g, u, d, H, I, None, 1e-6, 1.0, x)
+    np.testing.assert_allclose(got_nopost, (D + x).astype(np.float64), rtol=2e-6, atol=2e-6)
+    o = synth.q4("fo", I, H)
+    a = synth.normal("fa", I)
+    br = oracle.attention_output(o, I, H, post, 1e-6, a, x)
+    proj = (nr.q4_dequant(o, I, H).astype(np.float64) @ a.astype(np.float64)).astype(np.float32)
+    np.testing.assert_allclose(br, nr.rmsnorm(post, 1e-6, proj).astype(np.float32).astype(np.float64) + x,
+                               rtol=2e-6, atol=2e-6)
+
+
+# ---- greedy, compare ---------------------------------------------------------------------------
+
+def test_greedy_sampling_rs_19():
+    assert oracle.greedy([-3.0, 2.0, 2.0, 1.0]) == 1
+    assert oracle.greedy([-3.0, -1.0]) == 1
+    with pytest.raises(OracleError):
+        oracle.greedy([])
+    with pytest.raises(OracleError):
+        oracle.greedy([0.0, float("nan")])
+    x = synth.normal("gr", 100000)
+    x[777] = x.max()
+    assert oracle.greedy(x) == int(np.argmax(x))
+
+
+def test_compare_matvec_rs_198():
+    assert oracle.compare([1.0], [1.0]) == (0.0, 0.0)
+    for v in (float("nan"), float("inf"), 2.0):
+        with pytest.raises(OracleError):
+            oracle.compare([1.0], [v])
+    with pytest.raises(OracleError):
+        oracle.compare([1.0], [])
+    e, r = oracle.compare([100.0], [100.005])
+    assert abs(r - abs(float(np.float32(100.005)) - 100.0) / (1e-4 + 1e-2)) < 1e-12
