@@ -1,0 +1,150 @@
+// Internal declarations shared by the HIP kernels (kernels.hip) and the host
+// library (api.hip).  Nothing here crosses the C-ABI boundary in include/af.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+namespace af {
+
+// ---- device-resident weight layouts ----------------------------------------------------------
+//
+// Q4_0 (GGUF: 18 B per 32 weights) is split at upload into two planes so every
+// lane issues one aligned 16-byte load per block:
+//   codes  [rows][blocks][16]  the block's nibble bytes, unchanged (byte j: low
+//                              nibble = weight j, high nibble = weight j + 16)
+//   scales [rows][blocks]      the block's fp16 d
+struct Q4View {
+    const uint8_t* codes;
+    const uint16_t* scales;
+    uint32_t rows;
+    uint32_t blocks;  // columns / 32
+};
+
+// Q6_K (GGUF: 210 B per 256 weights) is split into "units" of 64 weights.  Unit
+// u = 4 * superblock + 2 * g + hh (g: 128-element half, hh: 16-lane half of
+// the 32-lane quarter) covers elements 128 g + 32 q + 16 hh + j for q in 0..3,
+// j in 0..15, and stores:
+//   a [rows][units][16]  ql[64 g + 16 hh + j]        (q = 0 low nibble, q = 2 high)
+//   b [rows][units][16]  ql[64 g + 32 + 16 hh + j]   (q = 1 low nibble, q = 3 high)
+//   h [rows][units][16]  qh[32 g + 16 hh + j]        (bits 2q, 2q+1 = high code bits)
+//   s [rows][units]      4 int8 sub-scales sc[8 g + 2 q + hh], q = 0..3
+//   d [rows][superblocks] fp16 super-scale
+struct Q6View {
+    const uint8_t* a;
+    const uint8_t* b;
+    const uint8_t* h;
+    const uint32_t* s;
+    const uint16_t* d;
+    uint32_t rows;
+    uint32_t units;  // columns / 64
+};
+
+// ---- input stages (the GEMV prologue builds the fp32 input vector in LDS) -------------------
+enum InputKind : int {
+    IN_PLAIN = 0,  // x
+    IN_NORM = 1,   // f32(rms(x) * w_n)
+    IN_RESID = 2,  // v = (f32(rms(x) * w_a) + res) * scale  [w_a null: (x + res) * scale];
+                   // block 0 stores v to x_out; input = f32(rms(v) * w_n)
+    IN_EMBED = 3,  // v = Q6_K row ids[state[0]] * emb_scale; block 0 stores v; input = f32(rms(v) * w_n)
+};
+
+struct InputStage {
+    const float* x;
+    const float* res;
+    const float* w_a;
+    float eps_a;
+    float scale;
+    const float* w_n;
+    float eps_n;
+    float* x_out;
+    Q6View table;
+    const uint32_t* ids;
+    const uint32_t* state;
+    float emb_scale;
+};
+
+enum OutputKind : int {
+    OUT_PLAIN = 0,  // y[r] = row sum
+    OUT_GELU = 1,   // rows come in (gate, up) pairs: y[p] = f32(gelu_tanh(gate)) * up
+    OUT_ADD = 2,    // y[r] = row sum + add[r]
+};
+
+struct Q4Args {
+    Q4View w;      // the matrix (the gate matrix for OUT_GELU)
+    Q4View w2;     // the up matrix for OUT_GELU
+    InputStage in;
+    float* y;
+    const float* add;
+    const uint32_t* state;  // session state (null for standalone use): exit at once when stopped
+};
+
+// Session state words (device): position to consume next, sticky non-finite flag,
+// stop flag (set by the head when it selects a stop id or sees non-finite logits;
+// every kernel of a decode step returns immediately while it is set), and the
+// number of stop ids.
+enum { ST_POS = 0, ST_BAD = 1, ST_STOP = 2, ST_NSTOP = 3, ST_WORDS = 4 };
+constexpr uint32_t kMaxStopIds = 256;
+
+// Per-step record the head writes to mapped host memory: id, non-finite flag, stop flag.
+struct StepRecord {
+    uint32_t id;
+    uint32_t bad;
+    uint32_t stop;
+    uint32_t done;
+};
+
+struct HeadArgs {
+    Q6View w;
+    InputStage in;
+    float* logits;          // may be null
+    uint4* partial;         // one (value bits, id, bad, 0) per block
+    uint32_t* counter;      // blocks done (reset to 0 by the last block)
+    uint32_t* result;       // [id, bad] for the standalone head
+    uint32_t* state;        // step mode: state words
+    uint32_t* ids;          // step mode: ids[pos + 1] = argmax
+    const uint32_t* stop_ids;  // step mode: state[ST_NSTOP] ids
+    StepRecord* records;    // step mode: records[pos + 1] (mapped host memory)
+};
+
+struct AttnArgs {
+    const float* q_raw;
+    const float* k_raw;
+    const float* v_raw;
+    const float* q_norm;
+    const float* k_norm;
+    float q_eps, k_eps, v_eps;
+    int v_norm;
+    const double* inv_freq;  // head_width / 2
+    uint16_t* kcache;        // fp16 [kv_heads][ring][head_width]
+    uint16_t* vcache;
+    uint32_t ring;
+    uint32_t window;         // 0: global
+    float scale;
+    const uint32_t* state;   // non-null: position = state[ST_POS]
+    uint32_t position;
+    float* out;              // [q_heads][head_width]
+    float* part;             // [kv_heads][cmax][group][head_width + 2]
+    uint32_t* counters;      // [kv_heads]
+    uint32_t cmax;
+    uint32_t min_chunk;
+    uint32_t kv_heads;
+};
+
+// ---- launchers (kernels.hip) -----------------------------------------------------------------
+hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);
+hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s);
+hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s);
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t width, uint32_t vectors, float eps,
+                          hipStream_t s);
+hipError_t launch_resid(const InputStage& in, uint32_t width, float* y, hipStream_t s);
+hipError_t launch_advance(uint32_t* state, hipStream_t s);
+uint32_t head_grid(uint32_t rows);
+
+constexpr uint32_t kAttnMinChunk = 32;
+constexpr uint32_t kAttnMaxChunkLen = 2048;
+constexpr uint32_t kHeadRows = 4;  // rows per wave iteration in the head kernel
+
+}  // namespace af

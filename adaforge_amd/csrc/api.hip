@@ -1,0 +1,1195 @@
+// Host side of the C ABI (include/af.h): validation, weight repacking and
+// upload, standalone operators, and the generation session that captures the
+// whole decode step (48 layers + head + greedy) as one HIP graph.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/af.h"
+#include "af_internal.h"
+
+using namespace af;
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(int code, std::string msg) {
+    g_error = std::move(msg);
+    return code;
+}
+
+#define HIP_OK(expr, what)                                                                   \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess) return fail(AF_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+using Clock = std::chrono::steady_clock;
+double ms_since(Clock::time_point t) { return std::chrono::duration<double, std::milli>(Clock::now() - t).count(); }
+
+// ---- device ---------------------------------------------------------------------------------
+
+std::once_flag g_dev_once;
+int g_dev_status = AF_ERR_NO_DEVICE;
+std::string g_dev_msg;
+hipDeviceProp_t g_props;
+
+int ensure_device() {
+    std::call_once(g_dev_once, [] {
+        int n = 0;
+        if (hipGetDeviceCount(&n) != hipSuccess || n < 1) {
+            g_dev_msg = "no HIP device";
+            return;
+        }
+        if (hipGetDeviceProperties(&g_props, 0) != hipSuccess) {
+            g_dev_msg = "hipGetDeviceProperties failed";
+            return;
+        }
+        if (std::strncmp(g_props.gcnArchName, "gfx950", 6) != 0) {
+            g_dev_msg = std::string("gfx950 (MI355X) required, found ") + g_props.gcnArchName;
+            return;
+        }
+        g_dev_status = AF_OK;
+    });
+    if (g_dev_status != AF_OK) return fail(g_dev_status, g_dev_msg);
+    if (hipSetDevice(0) != hipSuccess) return fail(AF_ERR_DEVICE, "hipSetDevice(0) failed");
+    return AF_OK;
+}
+
+struct DevMem {
+    void* p = nullptr;
+    size_t bytes = 0;
+    DevMem() = default;
+    DevMem(const DevMem&) = delete;
+    DevMem& operator=(const DevMem&) = delete;
+    DevMem(DevMem&& o) noexcept : p(o.p), bytes(o.bytes) { o.p = nullptr; o.bytes = 0; }
+    DevMem& operator=(DevMem&& o) noexcept {
+        if (this != &o) {
+            reset();
+            p = o.p;
+            bytes = o.bytes;
+            o.p = nullptr;
+            o.bytes = 0;
+        }
+        return *this;
+    }
+    ~DevMem() { reset(); }
+    void reset() {
+        if (p) (void)hipFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    template <typename T>
+    T* as() const { return static_cast<T*>(p); }
+};
+
+int dev_alloc(DevMem& m, size_t bytes, const char* what) {
+    m.reset();
+    if (bytes == 0) bytes = 16;
+    HIP_OK(hipMalloc(&m.p, bytes), what);
+    m.bytes = bytes;
+    return AF_OK;
+}
+
+int dev_upload(DevMem& m, const void* src, size_t bytes, const char* what) {
+    int rc = dev_alloc(m, bytes, what);
+    if (rc) return rc;
+    HIP_OK(hipMemcpy(m.p, src, bytes, hipMemcpyHostToDevice), what);
+    return AF_OK;
+}
+
+unsigned host_threads() {
+    unsigned n = std::thread::hardware_concurrency();
+    return std::max(1u, std::min(16u, n ? n : 1u));
+}
+
+template <typename F>
+void parallel_rows(uint64_t n, F f) {
+    const unsigned t = (unsigned)std::min<uint64_t>(host_threads(), std::max<uint64_t>(1, n / 64));
+    if (t <= 1) {
+        f(0, n);
+        return;
+    }
+    std::vector<std::thread> pool;
+    const uint64_t per = (n + t - 1) / t;
+    for (unsigned i = 0; i < t; ++i) {
+        const uint64_t b = i * per, e = std::min(n, b + per);
+        if (b < e) pool.emplace_back(f, b, e);
+    }
+    for (auto& th : pool) th.join();
+}
+
+// ---- validation (mirrors the domain constructors) ---------------------------------------------
+
+bool half_finite(const uint8_t* p) { return ((p[1] << 8 | p[0]) & 0x7C00) != 0x7C00; }
+
+// Q4Matrix::new (crates/domain/src/q4.rs:9-28)
+int check_q4(const uint8_t* b, size_t len, uint32_t columns, uint32_t rows, const char* what) {
+    if (!b || columns == 0 || rows == 0 || columns % 32 != 0)
+        return fail(AF_ERR_INVALID, std::string(what) + ": invalid Q4_0 dimensions");
+    if ((uint64_t)(columns / 32) * rows * 18 != (uint64_t)len)
+        return fail(AF_ERR_INVALID, std::string(what) + ": inconsistent Q4_0 size");
+    for (size_t o = 0; o < len; o += 18)
+        if (!half_finite(b + o)) return fail(AF_ERR_INVALID, std::string(what) + ": non-finite Q4_0 scale");
+    return AF_OK;
+}
+
+// Q6Matrix::new (crates/domain/src/q6.rs:8-20)
+int check_q6(const uint8_t* b, size_t len, uint32_t columns, uint32_t rows, const char* what) {
+    if (!b || columns == 0 || columns > 65536 || columns % 256 != 0 || rows == 0 || rows > 1000000 ||
+        (uint64_t)(columns / 256) * rows * 210 != (uint64_t)len)
+        return fail(AF_ERR_INVALID, std::string(what) + ": invalid Q6_K matrix");
+    for (size_t o = 0; o < len; o += 210)
+        if (!half_finite(b + o + 208)) return fail(AF_ERR_INVALID, std::string(what) + ": invalid Q6_K matrix");
+    return AF_OK;
+}
+
+// RmsNorm::new (crates/domain/src/rms_norm.rs:8-16)
+int check_norm(const af_rms_norm& n, uint32_t expect, const char* what) {
+    if (!n.weights || n.len == 0 || n.len > 65536)
+        return fail(AF_ERR_INVALID, std::string(what) + ": invalid RMSNorm weights (1 to 65536 finite values required)");
+    for (uint32_t i = 0; i < n.len; ++i)
+        if (!std::isfinite(n.weights[i]))
+            return fail(AF_ERR_INVALID, std::string(what) + ": invalid RMSNorm weights (1 to 65536 finite values required)");
+    if (!std::isfinite(n.epsilon) || n.epsilon <= 0.0f)
+        return fail(AF_ERR_INVALID, std::string(what) + ": RMSNorm epsilon must be finite and positive");
+    if (expect && n.len != expect) return fail(AF_ERR_INVALID, std::string(what) + ": RMSNorm width mismatch");
+    return AF_OK;
+}
+
+// Rope::new (crates/domain/src/rope.rs:11-34)
+int check_rope(const af_rope_params& r) {
+    if (r.width == 0 || r.width > 65536 || r.width % 2 != 0 || !r.factors || !std::isfinite(r.base) ||
+        r.base <= 1.0 || r.context == 0)
+        return fail(AF_ERR_INVALID, "invalid RoPE parameters");
+    for (uint32_t i = 0; i < r.width / 2; ++i)
+        if (!std::isfinite(r.factors[i]) || r.factors[i] <= 0.0f) return fail(AF_ERR_INVALID, "invalid RoPE parameters");
+    return AF_OK;
+}
+
+// AttentionConfig::new (crates/domain/src/attention.rs:11-35)
+int check_attention(const af_attention_config& c) {
+    if (c.q_heads == 0 || c.kv_heads == 0 || c.width == 0 || c.q_heads % c.kv_heads != 0 || !std::isfinite(c.scale) ||
+        c.scale <= 0.0f || (uint64_t)c.q_heads * c.width > 0xFFFFFFFFull)
+        return fail(AF_ERR_INVALID, "invalid attention configuration");
+    return AF_OK;
+}
+
+// Kernel shape limits (in addition to the reference's own validation).
+int check_supported_q4(uint32_t columns, const char* what) {
+    if (columns > 16384) return fail(AF_ERR_INVALID, std::string(what) + ": Q4_0 columns above 16384 are not supported");
+    return AF_OK;
+}
+int check_supported_attention(const af_attention_config& c) {
+    const uint32_t g = c.q_heads / c.kv_heads;
+    if (c.width != 256) return fail(AF_ERR_INVALID, "attention head width must be 256");
+    if (g != 1 && g != 2 && g != 4) return fail(AF_ERR_INVALID, "query heads per KV head must be 1, 2 or 4");
+    return AF_OK;
+}
+
+std::vector<double> inverse_frequencies(const af_rope_params& r) {
+    // Rope::new (crates/domain/src/rope.rs:25-29): base^(-2 i / width) / factor_i in f64.
+    std::vector<double> f(r.width / 2);
+    for (uint32_t i = 0; i < r.width / 2; ++i)
+        f[i] = std::pow(r.base, -2.0 * (double)i / (double)r.width) / (double)r.factors[i];
+    return f;
+}
+
+// ---- repacking --------------------------------------------------------------------------------
+
+struct Q4Dev {
+    DevMem codes, scales;
+    uint32_t rows = 0, columns = 0;
+    Q4View view() const { return Q4View{codes.as<uint8_t>(), scales.as<uint16_t>(), rows, columns / 32}; }
+};
+
+// Concatenates the row blocks of several Q4_0 matrices (same columns) into one device matrix.
+int upload_q4(Q4Dev& d, const std::vector<af_matrix>& parts) {
+    const uint32_t columns = parts[0].columns, B = columns / 32;
+    uint64_t rows = 0;
+    for (auto& p : parts) rows += p.rows;
+    std::vector<uint8_t> codes(rows * B * 16);
+    std::vector<uint16_t> scales(rows * B);
+    uint64_t r0 = 0;
+    for (auto& p : parts) {
+        const uint8_t* src = p.bytes;
+        uint8_t* cd = codes.data() + r0 * B * 16;
+        uint16_t* sc = scales.data() + r0 * B;
+        parallel_rows((uint64_t)p.rows * B, [&](uint64_t b, uint64_t e) {
+            for (uint64_t i = b; i < e; ++i) {
+                const uint8_t* blk = src + i * 18;
+                sc[i] = (uint16_t)(blk[0] | (blk[1] << 8));
+                std::memcpy(cd + i * 16, blk + 2, 16);
+            }
+        });
+        r0 += p.rows;
+    }
+    int rc = dev_upload(d.codes, codes.data(), codes.size(), "Q4_0 codes upload");
+    if (rc) return rc;
+    rc = dev_upload(d.scales, scales.data(), scales.size() * 2, "Q4_0 scales upload");
+    if (rc) return rc;
+    d.rows = (uint32_t)rows;
+    d.columns = columns;
+    return AF_OK;
+}
+
+struct Q6Dev {
+    DevMem a, b, h, s, d;
+    uint32_t rows = 0, columns = 0;
+    Q6View view() const {
+        return Q6View{a.as<uint8_t>(), b.as<uint8_t>(), h.as<uint8_t>(), s.as<uint32_t>(), d.as<uint16_t>(), rows,
+                      columns / 64};
+    }
+};
+
+int upload_q6(Q6Dev& dv, const uint8_t* src, uint32_t columns, uint32_t rows) {
+    const uint64_t units = columns / 64, sblocks = columns / 256;
+    std::vector<uint8_t> A(rows * units * 16), B(rows * units * 16), H(rows * units * 16);
+    std::vector<uint32_t> S(rows * units);
+    std::vector<uint16_t> D(rows * sblocks);
+    parallel_rows((uint64_t)rows * sblocks, [&](uint64_t b0, uint64_t e0) {
+        for (uint64_t i = b0; i < e0; ++i) {
+            const uint8_t* blk = src + i * 210;
+            const uint8_t *ql = blk, *qh = blk + 128, *sc = blk + 192;
+            D[i] = (uint16_t)(blk[208] | (blk[209] << 8));
+            for (int g = 0; g < 2; ++g)
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint64_t u = i * 4 + g * 2 + hh;  // row * units + unit
+                    std::memcpy(&A[u * 16], ql + 64 * g + 16 * hh, 16);
+                    std::memcpy(&B[u * 16], ql + 64 * g + 32 + 16 * hh, 16);
+                    std::memcpy(&H[u * 16], qh + 32 * g + 16 * hh, 16);
+                    uint32_t w = 0;
+                    for (int q = 0; q < 4; ++q) w |= (uint32_t)sc[8 * g + 2 * q + hh] << (8 * q);
+                    S[u] = w;
+                }
+        }
+    });
+    int rc;
+    if ((rc = dev_upload(dv.a, A.data(), A.size(), "Q6_K upload"))) return rc;
+    if ((rc = dev_upload(dv.b, B.data(), B.size(), "Q6_K upload"))) return rc;
+    if ((rc = dev_upload(dv.h, H.data(), H.size(), "Q6_K upload"))) return rc;
+    if ((rc = dev_upload(dv.s, S.data(), S.size() * 4, "Q6_K upload"))) return rc;
+    if ((rc = dev_upload(dv.d, D.data(), D.size() * 2, "Q6_K upload"))) return rc;
+    dv.rows = rows;
+    dv.columns = columns;
+    return AF_OK;
+}
+
+float median_of(std::vector<float> t) {
+    if (t.empty()) return 0.0f;
+    std::sort(t.begin(), t.end());
+    const size_t n = t.size();
+    return n % 2 ? t[n / 2] : 0.5f * (t[n / 2 - 1] + t[n / 2]);
+}
+
+// Scratch for the standalone head / attention entry points (grown on demand, never shrunk).
+struct Scratch {
+    std::mutex mu;
+    DevMem head_partial, head_counter, attn_part, attn_counters;
+};
+Scratch g_scratch;
+
+int grow(DevMem& m, size_t bytes, bool zero, const char* what) {
+    if (m.bytes >= bytes) return AF_OK;
+    int rc = dev_alloc(m, bytes, what);
+    if (rc) return rc;
+    if (zero) HIP_OK(hipMemset(m.p, 0, bytes), what);
+    return AF_OK;
+}
+
+}  // namespace
+
+// ================================================================================================
+// C ABI
+// ================================================================================================
+
+struct af_q4 {
+    Q4Dev m;
+};
+struct af_q6 {
+    Q6Dev m;
+};
+
+extern "C" {
+
+const char* af_last_error(void) { return g_error.c_str(); }
+
+int af_device_query(af_device_info* out) {
+    if (!out) return fail(AF_ERR_INVALID, "null output");
+    int rc = ensure_device();
+    if (rc) return rc;
+    std::memset(out, 0, sizeof(*out));
+    std::snprintf(out->name, sizeof(out->name), "%s", g_props.name);
+    std::snprintf(out->arch, sizeof(out->arch), "%s", g_props.gcnArchName);
+    out->compute_units = g_props.multiProcessorCount;
+    size_t fr = 0, tot = 0;
+    HIP_OK(hipMemGetInfo(&fr, &tot), "hipMemGetInfo");
+    out->free_memory_bytes = fr;
+    out->total_memory_bytes = tot;
+    return AF_OK;
+}
+
+int af_q4_upload(const uint8_t* q4, size_t len, uint32_t columns, uint32_t rows, af_q4** out) {
+    if (!out) return fail(AF_ERR_INVALID, "null output");
+    *out = nullptr;
+    int rc = check_q4(q4, len, columns, rows, "Q4_0 matrix");
+    if (rc) return rc;
+    if ((rc = check_supported_q4(columns, "Q4_0 matrix"))) return rc;
+    if ((rc = ensure_device())) return rc;
+    auto m = std::make_unique<af_q4>();
+    if ((rc = upload_q4(m->m, {af_matrix{q4, len, columns, rows}}))) return rc;
+    *out = m.release();
+    return AF_OK;
+}
+
+void af_q4_free(af_q4* m) { delete m; }
+
+int af_q4_gemv(const af_q4* m, const float* x, float* y, void* stream) {
+    if (!m || !x || !y) return fail(AF_ERR_INVALID, "null argument");
+    Q4Args a{};
+    a.w = m->m.view();
+    a.in.x = x;
+    a.y = y;
+    HIP_OK(launch_q4_gemv(a, IN_PLAIN, OUT_PLAIN, m->m.rows, (hipStream_t)stream), "Q4_0 GEMV launch");
+    return AF_OK;
+}
+
+int af_q6_upload(const uint8_t* q6, size_t len, uint32_t columns, uint32_t rows, af_q6** out) {
+    if (!out) return fail(AF_ERR_INVALID, "null output");
+    *out = nullptr;
+    int rc = check_q6(q6, len, columns, rows, "Q6_K matrix");
+    if (rc) return rc;
+    if (columns > 4096) return fail(AF_ERR_INVALID, "Q6_K columns above 4096 are not supported");
+    if ((rc = ensure_device())) return rc;
+    auto m = std::make_unique<af_q6>();
+    if ((rc = upload_q6(m->m, q6, columns, rows))) return rc;
+    *out = m.release();
+    return AF_OK;
+}
+
+void af_q6_free(af_q6* m) { delete m; }
+
+int af_q6_gemv_argmax(const af_q6* m, const float* x, float* logits, uint32_t* result, void* stream) {
+    if (!m || !x || !result) return fail(AF_ERR_INVALID, "null argument");
+    std::lock_guard<std::mutex> lock(g_scratch.mu);
+    const uint32_t grid = head_grid(m->m.rows);
+    int rc;
+    if ((rc = grow(g_scratch.head_partial, (size_t)grid * sizeof(uint4), false, "head scratch"))) return rc;
+    if ((rc = grow(g_scratch.head_counter, 256, true, "head counter"))) return rc;
+    HeadArgs a{};
+    a.w = m->m.view();
+    a.in.x = x;
+    a.logits = logits;
+    a.partial = g_scratch.head_partial.as<uint4>();
+    a.counter = g_scratch.head_counter.as<uint32_t>();
+    a.result = result;
+    HIP_OK(launch_head(a, IN_PLAIN, grid, (hipStream_t)stream), "Q6_K head launch");
+    return AF_OK;
+}
+
+int af_rmsnorm(const float* x, const float* weights, float* y, uint32_t width, uint32_t vectors, float eps,
+               void* stream) {
+    if (!x || !weights || !y || width == 0 || vectors == 0) return fail(AF_ERR_INVALID, "invalid RMSNorm arguments");
+    if (!std::isfinite(eps) || eps <= 0.0f) return fail(AF_ERR_INVALID, "RMSNorm epsilon must be finite and positive");
+    HIP_OK(launch_rmsnorm(x, weights, y, width, vectors, eps, (hipStream_t)stream), "RMSNorm launch");
+    return AF_OK;
+}
+
+int af_matvec_run(const uint8_t* q4, size_t len, uint32_t columns, uint32_t rows, const float* inputs,
+                  uint32_t n_inputs, uint32_t timed_repetitions, float* outputs, float* median_ms) {
+    int rc = check_q4(q4, len, columns, rows, "Q4_0 matrix");
+    if (rc) return rc;
+    if ((rc = check_supported_q4(columns, "Q4_0 matrix"))) return rc;
+    if (!inputs || !outputs || n_inputs == 0) return fail(AF_ERR_INVALID, "invalid input vectors");
+    for (uint64_t i = 0; i < (uint64_t)n_inputs * columns; ++i)
+        if (!std::isfinite(inputs[i])) return fail(AF_ERR_INVALID, "invalid input vector");
+    if ((rc = ensure_device())) return rc;
+    Q4Dev m;
+    if ((rc = upload_q4(m, {af_matrix{q4, len, columns, rows}}))) return rc;
+    DevMem x, y;
+    if ((rc = dev_alloc(x, (size_t)columns * 4, "input"))) return rc;
+    if ((rc = dev_alloc(y, (size_t)rows * 4, "output"))) return rc;
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0), "event");
+    HIP_OK(hipEventCreate(&e1), "event");
+    std::vector<float> times;
+    Q4Args a{};
+    a.w = m.view();
+    a.in.x = x.as<float>();
+    a.y = y.as<float>();
+    int status = AF_OK;
+    for (uint32_t v = 0; v < n_inputs && !status; ++v) {
+        if (hipMemcpy(x.p, inputs + (size_t)v * columns, (size_t)columns * 4, hipMemcpyHostToDevice) != hipSuccess) {
+            status = fail(AF_ERR_DEVICE, "input upload");
+            break;
+        }
+        const uint32_t execs = v + 1 == n_inputs ? 1 + timed_repetitions : 1;
+        for (uint32_t r = 0; r < execs; ++r) {
+            hipError_t e = hipEventRecord(e0, 0);
+            if (e == hipSuccess) e = launch_q4_gemv(a, IN_PLAIN, OUT_PLAIN, rows, 0);
+            if (e == hipSuccess) e = hipEventRecord(e1, 0);
+            if (e == hipSuccess) e = hipEventSynchronize(e1);
+            if (e != hipSuccess) {
+                status = fail(AF_ERR_DEVICE, std::string("matvec launch: ") + hipGetErrorString(e));
+                break;
+            }
+            if (v + 1 == n_inputs && r > 0) {
+                float t = 0;
+                (void)hipEventElapsedTime(&t, e0, e1);
+                times.push_back(t);
+            }
+        }
+        if (!status && hipMemcpy(outputs + (size_t)v * rows, y.p, (size_t)rows * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            status = fail(AF_ERR_DEVICE, "output download");
+    }
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (median_ms) *median_ms = median_of(times);
+    return status;
+}
+
+int af_rmsnorm_run(const float* weights, uint32_t width, float eps, const float* inputs, uint32_t vectors,
+                   uint32_t timed_repetitions, float* outputs, float* median_ms) {
+    int rc = check_norm(af_rms_norm{weights, width, eps}, 0, "RMSNorm");
+    if (rc) return rc;
+    if (!inputs || !outputs || vectors == 0) return fail(AF_ERR_INVALID, "invalid RMSNorm input");
+    for (uint64_t i = 0; i < (uint64_t)vectors * width; ++i)
+        if (!std::isfinite(inputs[i])) return fail(AF_ERR_INVALID, "invalid RMSNorm input");
+    if ((rc = ensure_device())) return rc;
+    DevMem x, w, y;
+    const size_t n = (size_t)vectors * width * 4;
+    if ((rc = dev_upload(x, inputs, n, "RMSNorm input"))) return rc;
+    if ((rc = dev_upload(w, weights, (size_t)width * 4, "RMSNorm weights"))) return rc;
+    if ((rc = dev_alloc(y, n, "RMSNorm output"))) return rc;
+    hipEvent_t e0, e1;
+    HIP_OK(hipEventCreate(&e0), "event");
+    HIP_OK(hipEventCreate(&e1), "event");
+    std::vector<float> times;
+    int status = AF_OK;
+    for (uint32_t r = 0; r < 1 + timed_repetitions; ++r) {
+        hipError_t e = hipEventRecord(e0, 0);
+        if (e == hipSuccess) e = launch_rmsnorm(x.as<float>(), w.as<float>(), y.as<float>(), width, vectors, eps, 0);
+        if (e == hipSuccess) e = hipEventRecord(e1, 0);
+        if (e == hipSuccess) e = hipEventSynchronize(e1);
+        if (e != hipSuccess) {
+            status = fail(AF_ERR_DEVICE, std::string("RMSNorm launch: ") + hipGetErrorString(e));
+            break;
+        }
+        if (r > 0) {
+            float t = 0;
+            (void)hipEventElapsedTime(&t, e0, e1);
+            times.push_back(t);
+        }
+    }
+    if (!status && hipMemcpy(outputs, y.p, n, hipMemcpyDeviceToHost) != hipSuccess)
+        status = fail(AF_ERR_DEVICE, "RMSNorm download");
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    if (median_ms) *median_ms = median_of(times);
+    return status;
+}
+
+}  // extern "C"
+
+// ---- FFN ---------------------------------------------------------------------------------------
+
+struct af_ffn {
+    Q4Dev gate, up, down;
+    DevMem pre, post, act, mid;
+    float pre_eps = 0, post_eps = 0, scale = 1;
+    bool has_post = false;
+    uint32_t hidden = 0, intermediate = 0;
+};
+
+extern "C" {
+
+int af_ffn_create(const af_ffn_weights* w, af_ffn** out) {
+    if (!w || !out) return fail(AF_ERR_INVALID, "null argument");
+    *out = nullptr;
+    // Ffn::new (crates/domain/src/ffn.rs:70-98)
+    const uint32_t hidden = w->gate.columns, inter = w->gate.rows;
+    int rc;
+    if ((rc = check_q4(w->gate.bytes, w->gate.len, w->gate.columns, w->gate.rows, "FFN gate"))) return rc;
+    if ((rc = check_q4(w->up.bytes, w->up.len, w->up.columns, w->up.rows, "FFN up"))) return rc;
+    if ((rc = check_q4(w->down.bytes, w->down.len, w->down.columns, w->down.rows, "FFN down"))) return rc;
+    if (w->up.columns != hidden || w->up.rows != inter || w->down.columns != inter || w->down.rows != hidden ||
+        !std::isfinite(w->layer_scale))
+        return fail(AF_ERR_INVALID, "incompatible FFN dimensions or scale");
+    if ((rc = check_norm(w->pre, hidden, "FFN pre-norm"))) return rc;
+    const bool has_post = w->post.weights != nullptr;
+    if (has_post && (rc = check_norm(w->post, hidden, "FFN post-norm"))) return rc;
+    if ((rc = check_supported_q4(hidden, "FFN gate"))) return rc;
+    if ((rc = check_supported_q4(inter, "FFN down"))) return rc;
+    if ((rc = ensure_device())) return rc;
+    auto f = std::make_unique<af_ffn>();
+    if ((rc = upload_q4(f->gate, {w->gate}))) return rc;
+    if ((rc = upload_q4(f->up, {w->up}))) return rc;
+    if ((rc = upload_q4(f->down, {w->down}))) return rc;
+    if ((rc = dev_upload(f->pre, w->pre.weights, (size_t)hidden * 4, "FFN norm"))) return rc;
+    if (has_post && (rc = dev_upload(f->post, w->post.weights, (size_t)hidden * 4, "FFN norm"))) return rc;
+    if ((rc = dev_alloc(f->act, (size_t)inter * 4, "FFN activations"))) return rc;
+    if ((rc = dev_alloc(f->mid, (size_t)hidden * 4, "FFN down output"))) return rc;
+    f->pre_eps = w->pre.epsilon;
+    f->post_eps = w->post.epsilon;
+    f->scale = w->layer_scale;
+    f->has_post = has_post;
+    f->hidden = hidden;
+    f->intermediate = inter;
+    *out = f.release();
+    return AF_OK;
+}
+
+void af_ffn_free(af_ffn* f) { delete f; }
+
+int af_ffn_run(af_ffn* f, const float* x, float* y, void* stream) {
+    if (!f || !x || !y) return fail(AF_ERR_INVALID, "null argument");
+    hipStream_t s = (hipStream_t)stream;
+    Q4Args g{};
+    g.w = f->gate.view();
+    g.w2 = f->up.view();
+    g.in.x = x;
+    g.in.w_n = f->pre.as<float>();
+    g.in.eps_n = f->pre_eps;
+    g.y = f->act.as<float>();
+    HIP_OK(launch_q4_gemv(g, IN_NORM, OUT_GELU, f->intermediate, s), "FFN gate/up launch");
+    Q4Args d{};
+    d.w = f->down.view();
+    d.in.x = f->act.as<float>();
+    if (!f->has_post && f->scale == 1.0f) {  // down + residual in the GEMV epilogue
+        d.y = y;
+        d.add = x;
+        HIP_OK(launch_q4_gemv(d, IN_PLAIN, OUT_ADD, f->hidden, s), "FFN down launch");
+        return AF_OK;
+    }
+    d.y = f->mid.as<float>();
+    HIP_OK(launch_q4_gemv(d, IN_PLAIN, OUT_PLAIN, f->hidden, s), "FFN down launch");
+    InputStage r{};
+    r.x = f->mid.as<float>();
+    r.res = x;
+    r.w_a = f->has_post ? f->post.as<float>() : nullptr;
+    r.eps_a = f->post_eps;
+    r.scale = f->scale;
+    HIP_OK(launch_resid(r, f->hidden, y, s), "FFN tail launch");
+    return AF_OK;
+}
+
+int af_attention_decode(const af_attention_args* p, void* stream) {
+    if (!p || !p->q || !p->k || !p->v || !p->q_norm || !p->k_norm || !p->k_cache || !p->v_cache || !p->out)
+        return fail(AF_ERR_INVALID, "null attention argument");
+    int rc;
+    if ((rc = check_attention(p->config))) return rc;
+    if ((rc = check_rope(p->rope))) return rc;
+    if ((rc = check_supported_attention(p->config))) return rc;
+    if (p->rope.width != p->config.width) return fail(AF_ERR_INVALID, "RoPE width differs from head width");
+    if (p->position >= p->rope.context) return fail(AF_ERR_INVALID, "position outside the RoPE context");
+    const uint32_t nvis = p->config.window ? std::min(p->position + 1, p->config.window) : p->position + 1;
+    if (p->ring < nvis || p->ring == 0) return fail(AF_ERR_INVALID, "KV ring smaller than the visible range");
+    for (float e : {p->q_eps, p->k_eps, p->v_eps})
+        if (!std::isfinite(e) || e <= 0.0f) return fail(AF_ERR_INVALID, "epsilon must be finite and positive");
+    if ((rc = ensure_device())) return rc;
+    const uint32_t group = p->config.q_heads / p->config.kv_heads, D = p->config.width;
+    const uint32_t cmax = std::max<uint32_t>(64, (nvis + kAttnMaxChunkLen - 1) / kAttnMaxChunkLen);
+    std::lock_guard<std::mutex> lock(g_scratch.mu);
+    if ((rc = grow(g_scratch.attn_part, (size_t)p->config.kv_heads * cmax * group * (D + 2) * 4, false, "attention scratch")))
+        return rc;
+    if ((rc = grow(g_scratch.attn_counters, (size_t)std::max<uint32_t>(64, p->config.kv_heads) * 4, true,
+                   "attention counters")))
+        return rc;
+    // inverse frequencies: uploaded per call (the standalone entry point is a diagnostic)
+    std::vector<double> f = inverse_frequencies(p->rope);
+    DevMem freq;
+    if ((rc = dev_upload(freq, f.data(), f.size() * 8, "RoPE frequencies"))) return rc;
+    AttnArgs a{};
+    a.q_raw = p->q;
+    a.k_raw = p->k;
+    a.v_raw = p->v;
+    a.q_norm = p->q_norm;
+    a.k_norm = p->k_norm;
+    a.q_eps = p->q_eps;
+    a.k_eps = p->k_eps;
+    a.v_eps = p->v_eps;
+    a.v_norm = p->v_norm;
+    a.inv_freq = freq.as<double>();
+    a.kcache = p->k_cache;
+    a.vcache = p->v_cache;
+    a.ring = p->ring;
+    a.window = p->config.window;
+    a.scale = p->config.scale;
+    a.position = p->position;
+    a.out = p->out;
+    a.part = g_scratch.attn_part.as<float>();
+    a.counters = g_scratch.attn_counters.as<uint32_t>();
+    a.cmax = cmax;
+    a.min_chunk = kAttnMinChunk;
+    a.kv_heads = p->config.kv_heads;
+    HIP_OK(launch_attention(a, group, D, (hipStream_t)stream), "attention launch");
+    HIP_OK(hipStreamSynchronize((hipStream_t)stream), "attention");  // freq is freed on return
+    return AF_OK;
+}
+
+}  // extern "C"
+
+// ---- generation session --------------------------------------------------------------------------
+
+namespace {
+
+struct LayerDev {
+    Q4Dev qkv, o, gate, up, down;
+    DevMem input_norm, q_norm, k_norm, post_attn, ffn_norm, post_ffn, inv_freq, kcache, vcache;
+    float input_eps = 0, q_eps = 0, k_eps = 0, post_attn_eps = 0, ffn_eps = 0, post_ffn_eps = 0;
+    float layer_scale = 1, scale = 1;
+    uint32_t q_heads = 0, kv_heads = 0, width = 0, window = 0, ring = 0, qn = 0, kn = 0;
+    bool shared_v = false, v_norm = false;
+};
+
+int validate_layer(const af_layer_weights& w, uint32_t hidden, uint32_t capacity, uint32_t index) {
+    const std::string tag = "layer " + std::to_string(index);
+    int rc;
+    for (int i = 0; i < 3; ++i)
+        if ((rc = check_q4(w.matrices[i].bytes, w.matrices[i].len, w.matrices[i].columns, w.matrices[i].rows,
+                           (tag + " qkv").c_str())))
+            return rc;
+    if ((rc = check_q4(w.output.bytes, w.output.len, w.output.columns, w.output.rows, (tag + " output").c_str())))
+        return rc;
+    const af_ffn_weights& f = w.ffn;
+    if ((rc = check_q4(f.gate.bytes, f.gate.len, f.gate.columns, f.gate.rows, (tag + " gate").c_str()))) return rc;
+    if ((rc = check_q4(f.up.bytes, f.up.len, f.up.columns, f.up.rows, (tag + " up").c_str()))) return rc;
+    if ((rc = check_q4(f.down.bytes, f.down.len, f.down.columns, f.down.rows, (tag + " down").c_str()))) return rc;
+    if ((rc = check_rope(w.rope))) return rc;
+    if ((rc = check_attention(w.attention))) return rc;
+    const uint32_t hw = w.rope.width;
+    // stack.rs:60-84 (validate)
+    if (capacity == 0 || capacity > AF_MAX_CONTEXT || capacity > w.rope.context || w.input_norm.len != hidden ||
+        w.matrices[0].columns != hidden || w.matrices[1].columns != hidden || w.matrices[2].columns != hidden ||
+        w.head_norms[0].len != hw || w.head_norms[1].len != hw || w.matrices[0].rows % hw || w.matrices[1].rows % hw ||
+        w.matrices[2].rows % hw || w.matrices[0].rows != w.attention.q_heads * hw ||
+        w.matrices[1].rows != w.attention.kv_heads * hw || w.matrices[2].rows != w.matrices[1].rows ||
+        w.attention.width != hw || w.output.columns != w.matrices[0].rows || w.output.rows != hidden ||
+        f.gate.columns != hidden || f.up.columns != hidden || f.up.rows != f.gate.rows ||
+        f.down.columns != f.gate.rows || f.down.rows != hidden || !std::isfinite(f.layer_scale))
+        return fail(AF_ERR_INVALID, tag + ": incompatible consecutive-block dimensions or insufficient context");
+    if ((rc = check_norm(w.input_norm, hidden, (tag + " input norm").c_str()))) return rc;
+    if ((rc = check_norm(w.head_norms[0], hw, (tag + " q norm").c_str()))) return rc;
+    if ((rc = check_norm(w.head_norms[1], hw, (tag + " k norm").c_str()))) return rc;
+    if ((rc = check_norm(w.output_norm, hidden, (tag + " post-attention norm").c_str()))) return rc;
+    if ((rc = check_norm(f.pre, hidden, (tag + " FFN norm").c_str()))) return rc;
+    if ((rc = check_norm(f.post, hidden, (tag + " post-FFN norm").c_str()))) return rc;
+    if ((rc = check_supported_attention(w.attention))) return rc;
+    if ((rc = check_supported_q4(hidden, tag.c_str()))) return rc;
+    if ((rc = check_supported_q4(f.gate.rows, tag.c_str()))) return rc;
+    if ((rc = check_supported_q4(w.output.columns, tag.c_str()))) return rc;
+    return AF_OK;
+}
+
+}  // namespace
+
+struct af_session {
+    std::vector<LayerDev> layers;
+    Q6Dev head;
+    DevMem final_norm;
+    float final_eps = 0, emb_scale = 1, cap = 0;
+    uint32_t hidden = 0, intermediate = 0, vocabulary = 0, capacity = 0;
+    uint32_t max_qkv = 0, max_q = 0, cmax = 0, head_blocks = 0;
+    DevMem X, H, QKV, ATT, PROJ, ACT, D, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
+    uint32_t max_kv_rows = 0;
+    StepRecord* records = nullptr;      // mapped host memory, capacity + 2 entries (host view)
+    StepRecord* records_dev = nullptr;  // the same memory as the device addresses it
+    hipStream_t stream = nullptr;
+    hipGraphExec_t decode_exec = nullptr, prefill_exec = nullptr;
+    hipGraph_t decode_graph = nullptr, prefill_graph = nullptr;
+    std::vector<hipEvent_t> events;
+    hipEvent_t ev_start = nullptr;
+    std::vector<uint32_t> cached;  // tokens of the conversation (GenerationSession prefix)
+    uint32_t consumed = 0;         // positions with K/V in the caches
+    bool poisoned = false;
+    bool use_graphs = true;
+
+    ~af_session() {
+        if (stream) (void)hipStreamSynchronize(stream);
+        if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
+        if (prefill_exec) (void)hipGraphExecDestroy(prefill_exec);
+        if (decode_graph) (void)hipGraphDestroy(decode_graph);
+        if (prefill_graph) (void)hipGraphDestroy(prefill_graph);
+        for (auto e : events) (void)hipEventDestroy(e);
+        if (ev_start) (void)hipEventDestroy(ev_start);
+        if (records) (void)hipHostFree(records);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+
+    // One layer's five kernels.  Layer 0 embeds ids[pos]; later layers finish the
+    // previous layer's FFN tail (post-norm, residual, scale) in their prologue.
+    hipError_t enqueue_layer(uint32_t l, bool step) {
+        LayerDev& L = layers[l];
+        const uint32_t* st = step ? STATE.as<uint32_t>() : nullptr;
+        Q4Args qa{};
+        qa.w = L.qkv.view();
+        qa.y = QKV.as<float>();
+        qa.state = st;
+        qa.in.w_n = L.input_norm.as<float>();
+        qa.in.eps_n = L.input_eps;
+        qa.in.x_out = X.as<float>();
+        int kind;
+        if (l == 0) {
+            qa.in.table = head.view();
+            qa.in.ids = IDS.as<uint32_t>();
+            qa.in.state = STATE.as<uint32_t>();
+            qa.in.emb_scale = emb_scale;
+            kind = IN_EMBED;
+        } else {
+            const LayerDev& P = layers[l - 1];
+            qa.in.x = D.as<float>();
+            qa.in.res = H.as<float>();
+            qa.in.w_a = P.post_ffn.as<float>();
+            qa.in.eps_a = P.post_ffn_eps;
+            qa.in.scale = P.layer_scale;
+            kind = IN_RESID;
+        }
+        hipError_t e = launch_q4_gemv(qa, kind, OUT_PLAIN, L.qkv.rows, stream);
+        if (e != hipSuccess) return e;
+
+        AttnArgs aa{};
+        const float* qkv = QKV.as<float>();
+        aa.q_raw = qkv;
+        aa.k_raw = qkv + L.qn;
+        aa.v_raw = L.shared_v ? qkv + L.qn : qkv + L.qn + L.kn;
+        aa.q_norm = L.q_norm.as<float>();
+        aa.k_norm = L.k_norm.as<float>();
+        aa.q_eps = L.q_eps;
+        aa.k_eps = L.k_eps;
+        aa.v_eps = L.input_eps;
+        aa.v_norm = L.v_norm;
+        aa.inv_freq = L.inv_freq.as<double>();
+        aa.kcache = L.kcache.as<uint16_t>();
+        aa.vcache = L.vcache.as<uint16_t>();
+        aa.ring = L.ring;
+        aa.window = L.window;
+        aa.scale = L.scale;
+        aa.state = STATE.as<uint32_t>();
+        aa.out = ATT.as<float>();
+        aa.part = PART.as<float>();
+        aa.counters = COUNTERS.as<uint32_t>();
+        aa.cmax = cmax;
+        aa.min_chunk = kAttnMinChunk;
+        aa.kv_heads = L.kv_heads;
+        if ((e = launch_attention(aa, L.q_heads / L.kv_heads, L.width, stream)) != hipSuccess) return e;
+
+        Q4Args oa{};
+        oa.w = L.o.view();
+        oa.in.x = ATT.as<float>();
+        oa.y = PROJ.as<float>();
+        oa.state = st;
+        if ((e = launch_q4_gemv(oa, IN_PLAIN, OUT_PLAIN, L.o.rows, stream)) != hipSuccess) return e;
+
+        Q4Args ga{};
+        ga.w = L.gate.view();
+        ga.w2 = L.up.view();
+        ga.in.x = PROJ.as<float>();
+        ga.in.res = X.as<float>();
+        ga.in.w_a = L.post_attn.as<float>();
+        ga.in.eps_a = L.post_attn_eps;
+        ga.in.scale = 1.0f;
+        ga.in.w_n = L.ffn_norm.as<float>();
+        ga.in.eps_n = L.ffn_eps;
+        ga.in.x_out = H.as<float>();
+        ga.y = ACT.as<float>();
+        ga.state = st;
+        if ((e = launch_q4_gemv(ga, IN_RESID, OUT_GELU, intermediate, stream)) != hipSuccess) return e;
+
+        Q4Args da{};
+        da.w = L.down.view();
+        da.in.x = ACT.as<float>();
+        da.y = D.as<float>();
+        da.state = st;
+        return launch_q4_gemv(da, IN_PLAIN, OUT_PLAIN, hidden, stream);
+    }
+
+    HeadArgs head_args(bool step, bool with_logits) {
+        const LayerDev& P = layers.back();
+        HeadArgs h{};
+        h.w = head.view();
+        h.in.x = D.as<float>();
+        h.in.res = H.as<float>();
+        h.in.w_a = P.post_ffn.as<float>();
+        h.in.eps_a = P.post_ffn_eps;
+        h.in.scale = P.layer_scale;
+        h.in.w_n = final_norm.as<float>();
+        h.in.eps_n = final_eps;
+        h.in.x_out = X.as<float>();
+        h.logits = with_logits ? LOGITS.as<float>() : nullptr;
+        h.partial = HPART.as<uint4>();
+        h.counter = HCOUNT.as<uint32_t>();
+        h.result = RESULT.as<uint32_t>();
+        if (step) {
+            h.state = STATE.as<uint32_t>();
+            h.ids = IDS.as<uint32_t>();
+            h.stop_ids = STOPS.as<uint32_t>();
+            h.records = records_dev;
+        }
+        return h;
+    }
+
+    hipError_t enqueue_step(bool with_head) {
+        for (uint32_t l = 0; l < layers.size(); ++l) {
+            hipError_t e = enqueue_layer(l, true);
+            if (e != hipSuccess) return e;
+        }
+        if (with_head) return launch_head(head_args(true, false), IN_RESID, head_blocks, stream);
+        return launch_advance(STATE.as<uint32_t>(), stream);
+    }
+
+    int capture(bool with_head, hipGraph_t& g, hipGraphExec_t& x) {
+        HIP_OK(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "graph capture begin");
+        hipError_t e = enqueue_step(with_head);
+        hipError_t e2 = hipStreamEndCapture(stream, &g);
+        HIP_OK(e, "graph capture");
+        HIP_OK(e2, "graph capture end");
+        HIP_OK(hipGraphInstantiate(&x, g, nullptr, nullptr, 0), "graph instantiate");
+        HIP_OK(hipGraphUpload(x, stream), "graph upload");
+        return AF_OK;
+    }
+
+    hipError_t run_step(bool with_head) {
+        if (use_graphs) return hipGraphLaunch(with_head ? decode_exec : prefill_exec, stream);
+        return enqueue_step(with_head);
+    }
+
+    int set_state(uint32_t pos, uint32_t nstop) {
+        uint32_t st[ST_WORDS] = {pos, 0u, 0u, nstop};
+        HIP_OK(hipMemcpyAsync(STATE.p, st, sizeof(st), hipMemcpyHostToDevice, stream), "state upload");
+        return AF_OK;
+    }
+};
+
+namespace {
+
+int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head, uint32_t capacity,
+                 af_session** out) {
+    if (!out) return fail(AF_ERR_INVALID, "null output");
+    *out = nullptr;
+    if (!layers || !head || n_layers == 0 || n_layers > 256 || capacity == 0 || capacity > AF_MAX_CONTEXT)
+        return fail(AF_ERR_INVALID, "session limited to 1..256 blocks and " + std::to_string(AF_MAX_CONTEXT) +
+                                        " tokens of context");
+    int rc;
+    const af_matrix& hm = head->matrix;
+    if ((rc = check_q6(hm.bytes, hm.len, hm.columns, hm.rows, "output head"))) return rc;
+    const uint32_t hidden = hm.columns;
+    if (hidden > 4096) return fail(AF_ERR_INVALID, "hidden width above 4096 is not supported by the head");
+    if ((rc = check_norm(head->norm, hidden, "output norm"))) return rc;
+    if (!std::isfinite(head->cap) || head->cap <= 0.0f) return fail(AF_ERR_INVALID, "incompatible output head");
+    const uint32_t inter = layers[0].ffn.gate.rows;
+    for (uint32_t i = 0; i < n_layers; ++i) {
+        if ((rc = validate_layer(layers[i], hidden, capacity, i))) return rc;
+        if (layers[i].ffn.gate.rows != inter) return fail(AF_ERR_INVALID, "FFN width differs across layers");
+    }
+    if ((rc = ensure_device())) return rc;
+
+    auto s = std::make_unique<af_session>();
+    s->hidden = hidden;
+    s->intermediate = inter;
+    s->vocabulary = hm.rows;
+    s->capacity = capacity;
+    s->final_eps = head->norm.epsilon;
+    s->cap = head->cap;
+    s->emb_scale = std::sqrt((float)hidden);  // EmbeddingBatch::scale (crates/domain/src/embedding.rs:49-51)
+    const char* env = std::getenv("AF_DISABLE_GRAPHS");
+    s->use_graphs = !(env && *env && std::strcmp(env, "0") != 0);
+    HIP_OK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "session stream");
+
+    uint32_t max_kv = 0, max_q = 0, max_group = 1;
+    s->layers.resize(n_layers);
+    for (uint32_t i = 0; i < n_layers; ++i) {
+        const af_layer_weights& w = layers[i];
+        LayerDev& L = s->layers[i];
+        L.q_heads = w.attention.q_heads;
+        L.kv_heads = w.attention.kv_heads;
+        L.width = w.attention.width;
+        L.window = w.attention.window;
+        L.scale = w.attention.scale;
+        L.qn = w.matrices[0].rows;
+        L.kn = w.matrices[1].rows;
+        L.shared_v = w.matrices[2].bytes == w.matrices[1].bytes;
+        L.v_norm = (w.flags & AF_LAYER_V_NORM) != 0;
+        L.input_eps = w.input_norm.epsilon;
+        L.q_eps = w.head_norms[0].epsilon;
+        L.k_eps = w.head_norms[1].epsilon;
+        L.post_attn_eps = w.output_norm.epsilon;
+        L.ffn_eps = w.ffn.pre.epsilon;
+        L.post_ffn_eps = w.ffn.post.epsilon;
+        L.layer_scale = w.ffn.layer_scale;
+        std::vector<af_matrix> qkv = {w.matrices[0], w.matrices[1]};
+        if (!L.shared_v) qkv.push_back(w.matrices[2]);
+        if ((rc = upload_q4(L.qkv, qkv))) return rc;
+        if ((rc = upload_q4(L.o, {w.output}))) return rc;
+        if ((rc = upload_q4(L.gate, {w.ffn.gate}))) return rc;
+        if ((rc = upload_q4(L.up, {w.ffn.up}))) return rc;
+        if ((rc = upload_q4(L.down, {w.ffn.down}))) return rc;
+        if ((rc = dev_upload(L.input_norm, w.input_norm.weights, (size_t)hidden * 4, "norm upload"))) return rc;
+        if ((rc = dev_upload(L.q_norm, w.head_norms[0].weights, (size_t)L.width * 4, "norm upload"))) return rc;
+        if ((rc = dev_upload(L.k_norm, w.head_norms[1].weights, (size_t)L.width * 4, "norm upload"))) return rc;
+        if ((rc = dev_upload(L.post_attn, w.output_norm.weights, (size_t)hidden * 4, "norm upload"))) return rc;
+        if ((rc = dev_upload(L.ffn_norm, w.ffn.pre.weights, (size_t)hidden * 4, "norm upload"))) return rc;
+        if ((rc = dev_upload(L.post_ffn, w.ffn.post.weights, (size_t)hidden * 4, "norm upload"))) return rc;
+        std::vector<double> f = inverse_frequencies(w.rope);
+        if ((rc = dev_upload(L.inv_freq, f.data(), f.size() * 8, "RoPE upload"))) return rc;
+        // Sliding-window layers keep a ring of `window` slots: a decode step never
+        // writes past the token it consumes, so no visible slot is overwritten.
+        L.ring = L.window ? std::min(L.window, capacity) : capacity;
+        const size_t kv = (size_t)L.kv_heads * L.ring * L.width * 2;
+        if ((rc = dev_alloc(L.kcache, kv, "K cache"))) return rc;
+        if ((rc = dev_alloc(L.vcache, kv, "V cache"))) return rc;
+        HIP_OK(hipMemset(L.kcache.p, 0, kv), "K cache clear");
+        HIP_OK(hipMemset(L.vcache.p, 0, kv), "V cache clear");
+        max_kv = std::max(max_kv, L.kv_heads);
+        max_q = std::max(max_q, L.qn);
+        max_group = std::max(max_group, L.q_heads / L.kv_heads);
+        s->max_qkv = std::max(s->max_qkv, L.qkv.rows);
+        s->max_kv_rows = std::max(s->max_kv_rows, L.kn);
+    }
+    s->max_q = max_q;
+    if ((rc = upload_q6(s->head, hm.bytes, hm.columns, hm.rows))) return rc;
+    if ((rc = dev_upload(s->final_norm, head->norm.weights, (size_t)hidden * 4, "final norm"))) return rc;
+
+    s->cmax = std::max<uint32_t>(64, (capacity + kAttnMaxChunkLen - 1) / kAttnMaxChunkLen);
+    s->head_blocks = head_grid(hm.rows);
+    struct {
+        DevMem* m;
+        size_t bytes;
+        bool zero;
+    } bufs[] = {
+        {&s->X, (size_t)hidden * 4, true},
+        {&s->H, (size_t)hidden * 4, true},
+        {&s->QKV, (size_t)s->max_qkv * 4, true},
+        {&s->ATT, (size_t)max_q * 4, true},
+        {&s->PROJ, (size_t)hidden * 4, true},
+        {&s->ACT, (size_t)inter * 4, true},
+        {&s->D, (size_t)hidden * 4, true},
+        {&s->LOGITS, (size_t)hm.rows * 4, false},
+        {&s->PART, (size_t)max_kv * s->cmax * max_group * (256 + 2) * 4, false},
+        {&s->COUNTERS, (size_t)std::max<uint32_t>(max_kv, 64) * 4, true},
+        {&s->HPART, (size_t)s->head_blocks * 16, false},
+        {&s->HCOUNT, 256, true},
+        {&s->STATE, ST_WORDS * 4, true},
+        {&s->IDS, ((size_t)capacity + 2) * 4, true},
+        {&s->STOPS, kMaxStopIds * 4, true},
+        {&s->RESULT, 256, true},
+    };
+    for (auto& b : bufs) {
+        if ((rc = dev_alloc(*b.m, b.bytes, "session buffer"))) return rc;
+        if (b.zero) HIP_OK(hipMemset(b.m->p, 0, b.bytes), "session buffer clear");
+    }
+    HIP_OK(hipHostMalloc((void**)&s->records, ((size_t)capacity + 2) * sizeof(StepRecord), hipHostMallocMapped),
+           "step records");
+    std::memset(s->records, 0, ((size_t)capacity + 2) * sizeof(StepRecord));
+    HIP_OK(hipHostGetDevicePointer((void**)&s->records_dev, s->records, 0), "step records mapping");
+    s->events.resize(AF_MAX_NEW_TOKENS);
+    for (auto& e : s->events) HIP_OK(hipEventCreate(&e), "event");
+    HIP_OK(hipEventCreate(&s->ev_start), "event");
+    HIP_OK(hipDeviceSynchronize(), "session upload");
+    if (s->use_graphs) {
+        if ((rc = s->capture(true, s->decode_graph, s->decode_exec))) return rc;
+        if ((rc = s->capture(false, s->prefill_graph, s->prefill_exec))) return rc;
+    }
+    HIP_OK(hipStreamSynchronize(s->stream), "session ready");
+    *out = s.release();
+    return AF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int af_session_open(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head,
+                    uint32_t capacity, af_session** out) {
+    return open_session(layers, n_layers, head, capacity, out);
+}
+
+void af_session_close(af_session* s) { delete s; }
+
+int af_session_reset(af_session* s) {
+    if (!s) return fail(AF_ERR_INVALID, "null session");
+    if (s->poisoned) return fail(AF_ERR_POISONED, "invalid HIP session; restart the chat");
+    s->cached.clear();
+    s->consumed = 0;
+    return AF_OK;
+}
+
+int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop,
+                        size_t n_stop, uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out,
+                        size_t* n_out, int32_t* stopped_out, af_generation_stats* stats) {
+    if (!s) return fail(AF_ERR_INVALID, "null session");
+    if (n_out) *n_out = 0;
+    if (stopped_out) *stopped_out = 0;
+    if (s->poisoned) return fail(AF_ERR_POISONED, "invalid HIP session; restart the chat");
+    // stack.rs:1184-1194
+    bool ok = prompt && n_prompt > 0 && max_new >= 1 && max_new <= AF_MAX_NEW_TOKENS &&
+              n_prompt + max_new <= s->capacity && stop && n_stop > 0 && n_stop <= kMaxStopIds && ids_out &&
+              n_prompt >= s->cached.size();
+    for (size_t i = 0; ok && i < n_prompt; ++i) ok = prompt[i] < s->vocabulary;
+    for (size_t i = 0; ok && i < n_stop; ++i) ok = stop[i] < s->vocabulary;
+    for (size_t i = 0; ok && i < s->cached.size(); ++i) ok = prompt[i] == s->cached[i];
+    if (!ok) return fail(AF_ERR_INVALID, "prompt, KV prefix or session capacity incompatible");
+
+    const auto started = Clock::now();
+    const size_t cached_tokens = s->cached.size();
+    s->poisoned = true;
+    const uint32_t P = (uint32_t)n_prompt, pend = P - s->consumed;
+    hipStream_t st = s->stream;
+    HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, prompt + s->consumed, (size_t)pend * 4,
+                          hipMemcpyHostToDevice, st),
+           "prompt upload");
+    HIP_OK(hipMemcpyAsync(s->STOPS.p, stop, n_stop * 4, hipMemcpyHostToDevice, st), "stop ids upload");
+    std::memset(s->records + P, 0, (size_t)(s->capacity + 2 - P) * sizeof(StepRecord));
+    int rc = s->set_state(pend == 0 ? s->consumed - 1 : s->consumed, (uint32_t)n_stop);
+    if (rc) return rc;
+    for (uint32_t i = 0; i + 1 < pend; ++i) HIP_OK(s->run_step(false), "prefill step");
+    HIP_OK(hipStreamSynchronize(st), "prefill");
+    const double prefill_ms = ms_since(started);
+    const double start_offset = ms_since(started);
+    HIP_OK(hipEventRecord(s->ev_start, st), "event");
+    // Enqueue all decode steps; each step's head writes its id and flags to mapped host
+    // memory, and a stop id makes the remaining steps return at once.
+    for (uint32_t k = 0; k < max_new; ++k) {
+        if (k == 0 && pend == 0) {
+            HIP_OK(launch_head(s->head_args(true, false), IN_RESID, s->head_blocks, st), "head launch");
+        } else {
+            HIP_OK(s->run_step(true), "decode step");
+        }
+        HIP_OK(hipEventRecord(s->events[k], st), "event");
+    }
+    std::vector<uint32_t> ids;
+    bool stopped = false, bad = false;
+    double first_ms = 0, last_ms = 0;
+    for (uint32_t k = 0; k < max_new; ++k) {
+        HIP_OK(hipEventSynchronize(s->events[k]), "decode step");
+        const volatile StepRecord* vr = s->records + P + k;
+        StepRecord r;
+        r.id = vr->id;
+        r.bad = vr->bad;
+        r.stop = vr->stop;
+        r.done = vr->done;
+        float t = 0;
+        (void)hipEventElapsedTime(&t, s->ev_start, s->events[k]);
+        if (!r.done || r.bad) {
+            bad = true;
+            break;
+        }
+        if (r.stop) {
+            stopped = true;
+            break;
+        }
+        if (k == 0) first_ms = start_offset + t;
+        last_ms = start_offset + t;
+        ids.push_back(r.id);
+        if (on_token) on_token(user, r.id);
+    }
+    HIP_OK(hipStreamSynchronize(st), "generation");
+    if (bad) return fail(AF_ERR_NONFINITE, "non-finite logits or invalid greedy id");
+    for (size_t i = 0; i < ids.size(); ++i) ids_out[i] = ids[i];
+    s->cached.assign(prompt, prompt + n_prompt);
+    s->cached.insert(s->cached.end(), ids.begin(), ids.end());
+    // The last generated token is consumed by the next call's first step.
+    s->consumed = stopped ? (uint32_t)s->cached.size() : (uint32_t)s->cached.size() - 1;
+    s->poisoned = false;
+    if (n_out) *n_out = ids.size();
+    if (stopped_out) *stopped_out = stopped;
+    if (stats) {
+        stats->prompt_tokens = n_prompt - cached_tokens;
+        stats->cached_tokens = cached_tokens;
+        stats->prefill_ms = prefill_ms;
+        stats->has_first_token = !ids.empty();
+        stats->first_token_ms = ids.empty() ? 0.0 : first_ms;
+        stats->decode_tokens = ids.empty() ? 0 : ids.size() - 1;
+        stats->decode_ms = ids.empty() ? 0.0 : last_ms - first_ms;
+        stats->total_ms = ms_since(started);
+    }
+    return AF_OK;
+}
+
+int af_generate(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head,
+                const uint32_t* prompt, size_t n_prompt, const uint32_t* stop, size_t n_stop, uint32_t max_new,
+                uint32_t* ids_out, size_t* n_out, int32_t* stopped, af_generation_stats* stats) {
+    // stack.rs:820-833
+    if (n_prompt > 256 || max_new < 1 || max_new > AF_MAX_NEW_TOKENS)
+        return fail(AF_ERR_INVALID, "invalid generation configuration");
+    af_session* s = nullptr;
+    int rc = open_session(layers, n_layers, head, (uint32_t)n_prompt + max_new, &s);
+    if (rc) return rc;
+    rc = af_session_generate(s, prompt, n_prompt, stop, n_stop, max_new, nullptr, nullptr, ids_out, n_out, stopped,
+                             stats);
+    delete s;
+    return rc;
+}
+
+int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_outputs, uint16_t* kv_appended,
+                     float* logits, float* hidden) {
+    if (!s) return fail(AF_ERR_INVALID, "null session");
+    if (s->poisoned) return fail(AF_ERR_POISONED, "invalid HIP session; restart the chat");
+    if (!ids || n == 0 || s->cached.size() + n > s->capacity || s->consumed != s->cached.size())
+        return fail(AF_ERR_INVALID, "trace ids exceed the session capacity or follow an unconsumed token");
+    for (size_t i = 0; i < n; ++i)
+        if (ids[i] >= s->vocabulary) return fail(AF_ERR_INVALID, "token id outside the vocabulary");
+    s->poisoned = true;
+    hipStream_t st = s->stream;
+    const size_t nl = s->layers.size(), H = s->hidden;
+    int rc;
+    if (layer_outputs && (rc = grow(s->SNAP, nl * H * 4, false, "trace buffer"))) return rc;
+    const size_t kvr = s->max_kv_rows, kv_bytes = nl * 2 * kvr * 2;
+    if (kv_appended && (rc = grow(s->KVSNAP, kv_bytes, true, "trace buffer"))) return rc;
+    HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, ids, n * 4, hipMemcpyHostToDevice, st), "ids upload");
+    if ((rc = s->set_state(s->consumed, 0))) return rc;
+    for (size_t t = 0; t < n; ++t) {
+        for (uint32_t l = 0; l < nl; ++l) {
+            HIP_OK(s->enqueue_layer(l, true), "trace layer");
+            if (kv_appended) {
+                const LayerDev& L = s->layers[l];
+                const size_t slot = (s->consumed + t) % L.ring, row = (size_t)L.width * 2;
+                uint8_t* dst = s->KVSNAP.as<uint8_t>() + (size_t)l * 2 * kvr * 2;
+                HIP_OK(hipMemcpy2DAsync(dst, row, L.kcache.as<uint8_t>() + slot * row, (size_t)L.ring * row, row,
+                                        L.kv_heads, hipMemcpyDeviceToDevice, st),
+                       "trace K copy");
+                HIP_OK(hipMemcpy2DAsync(dst + kvr * 2, row, L.vcache.as<uint8_t>() + slot * row, (size_t)L.ring * row,
+                                        row, L.kv_heads, hipMemcpyDeviceToDevice, st),
+                       "trace V copy");
+            }
+            if (layer_outputs) {
+                InputStage r{};
+                r.x = s->D.as<float>();
+                r.res = s->H.as<float>();
+                r.w_a = s->layers[l].post_ffn.as<float>();
+                r.eps_a = s->layers[l].post_ffn_eps;
+                r.scale = s->layers[l].layer_scale;
+                HIP_OK(launch_resid(r, s->hidden, s->SNAP.as<float>() + l * H, st), "trace snapshot");
+            }
+        }
+        if (layer_outputs)
+            HIP_OK(hipMemcpyAsync(layer_outputs + t * nl * H, s->SNAP.p, nl * H * 4, hipMemcpyDeviceToHost, st),
+                   "trace download");
+        if (kv_appended)
+            HIP_OK(hipMemcpyAsync(kv_appended + t * nl * 2 * kvr, s->KVSNAP.p, kv_bytes, hipMemcpyDeviceToHost, st),
+                   "trace download");
+        if (t + 1 < n) HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+    }
+    // head on the last token: raw logits, no state change; then advance past it
+    HeadArgs h = s->head_args(false, true);
+    HIP_OK(launch_head(h, IN_RESID, s->head_blocks, st), "trace head");
+    HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+    if (logits) HIP_OK(hipMemcpyAsync(logits, s->LOGITS.p, (size_t)s->vocabulary * 4, hipMemcpyDeviceToHost, st), "logits");
+    if (hidden) HIP_OK(hipMemcpyAsync(hidden, s->X.p, H * 4, hipMemcpyDeviceToHost, st), "hidden");
+    HIP_OK(hipStreamSynchronize(st), "trace");
+    s->cached.insert(s->cached.end(), ids, ids + n);
+    s->consumed = (uint32_t)s->cached.size();
+    s->poisoned = false;
+    return AF_OK;
+}
+
+}  // extern "C"

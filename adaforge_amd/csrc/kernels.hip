@@ -1,0 +1,795 @@
+// HIP kernels for gfx950 (MI355X): the batch-1 decode step of a Q4_0 / Q6_K
+// transformer.  Every kernel is bandwidth-bound GEMV or streaming work; none
+// uses MFMA.  Cross-workgroup results (attention chunks, argmax partials) are
+// combined by the last workgroup to finish, found with a device-scope counter
+// that the last workgroup resets, so the kernels can be replayed in a graph.
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "af_internal.h"
+
+namespace af {
+
+// ---- helpers ----------------------------------------------------------------------------------
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over the block of one double per thread (blockDim a multiple of 64, <= 512).
+__device__ double block_sum_d(double v, double* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    return t;
+}
+
+__device__ float block_sum_f(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    return t;
+}
+
+__device__ float block_max_f(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int w = 1; w < nw; ++w) t = fmaxf(t, red[w]);
+    return t;
+}
+
+// f32(x * r * w) with the products in double, as the FP64 RMSNorm oracle rounds its output.
+__device__ __forceinline__ float norm_apply(float x, double r, float w) {
+    return (float)__dmul_rn(__dmul_rn((double)x, r), (double)w);
+}
+
+__device__ __forceinline__ double inv_rms(double sumsq, uint32_t n, float eps) {
+    return 1.0 / sqrt(__dadd_rn(sumsq / (double)n, (double)eps));
+}
+
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in double, rounded to f32, times up in f32.
+__device__ __forceinline__ float gelu_mul(float g, float u) {
+    const double x = (double)g;
+    const double c = sqrt(2.0 / 3.14159265358979323846);
+    const double inner = __dadd_rn(x, __dmul_rn(__dmul_rn(__dmul_rn(0.044715, x), x), x));
+    const double t = tanh(__dmul_rn(c, inner));
+    const float gl = (float)__dmul_rn(__dmul_rn(0.5, x), __dadd_rn(1.0, t));
+    return __fmul_rn(gl, u);
+}
+
+// One 64-weight Q6_K unit's code bytes for quarter q from its ql/ql/qh dwords.
+__device__ __forceinline__ uint32_t q6_codes(uint32_t a, uint32_t b, uint32_t h, int q) {
+    switch (q) {
+        case 0: return (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+        case 1: return (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+        case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+        default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+    }
+}
+
+// ---- input stage: builds the fp32 GEMV input vector in LDS ------------------------------------
+
+// Embedding row (Q6_K, repacked) times emb_scale into xs; one thread per unit dword (16 elements).
+__device__ void embed_row(const InputStage& in, float* xs, uint32_t K) {
+    const Q6View& t = in.table;
+    const uint32_t row = min(in.ids[in.state[ST_POS]], t.rows - 1);  // ids are validated; never read past the table
+    const uint32_t units = t.units, sblocks = units / 4;
+    const uint32_t* A = reinterpret_cast<const uint32_t*>(t.a + (size_t)row * units * 16);
+    const uint32_t* B = reinterpret_cast<const uint32_t*>(t.b + (size_t)row * units * 16);
+    const uint32_t* H = reinterpret_cast<const uint32_t*>(t.h + (size_t)row * units * 16);
+    for (uint32_t w = threadIdx.x; w < units * 4; w += blockDim.x) {
+        const uint32_t u = w >> 2, k = w & 3;
+        const uint32_t sb = u >> 2, g = (u >> 1) & 1, hh = u & 1;
+        const uint32_t a = A[w], b = B[w], h = H[w];
+        const uint32_t sc = t.s[(size_t)row * units + u];
+        const float d = h2f(t.d[(size_t)row * sblocks + sb]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t c = q6_codes(a, b, h, q);
+            const float ds = __fmul_rn(d, (float)(int8_t)(sc >> (8 * q)));
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const int code = (int)((c >> (8 * n)) & 0xFF) - 32;
+                const uint32_t e = sb * 256 + g * 128 + q * 32 + hh * 16 + 4 * k + n;
+                xs[e] = __fmul_rn(__fmul_rn(ds, (float)code), in.emb_scale);
+            }
+        }
+    }
+    (void)K;
+}
+
+template <int IN>
+__device__ void input_stage(const InputStage& in, float* xs, uint32_t K, double* red) {
+    const uint32_t tid = threadIdx.x, nt = blockDim.x;
+    if constexpr (IN == IN_PLAIN) {
+        for (uint32_t i = tid; i < K; i += nt) xs[i] = in.x[i];
+        __syncthreads();
+        return;
+    } else {
+        double ss = 0.0;
+        if constexpr (IN == IN_NORM) {
+            for (uint32_t i = tid; i < K; i += nt) {
+                const float v = in.x[i];
+                xs[i] = v;
+                ss += (double)v * (double)v;
+            }
+        } else if constexpr (IN == IN_RESID) {
+            double ra = 1.0;
+            if (in.w_a) {
+                double sa = 0.0;
+                for (uint32_t i = tid; i < K; i += nt) {
+                    const double v = (double)in.x[i];
+                    sa += v * v;
+                }
+                ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
+            }
+            for (uint32_t i = tid; i < K; i += nt) {
+                const float t = in.w_a ? norm_apply(in.x[i], ra, in.w_a[i]) : in.x[i];
+                const float v = __fmul_rn(__fadd_rn(t, in.res[i]), in.scale);
+                xs[i] = v;
+                if (blockIdx.x == 0 && in.x_out) in.x_out[i] = v;
+                ss += (double)v * (double)v;
+            }
+        } else {  // IN_EMBED
+            embed_row(in, xs, K);
+            __syncthreads();
+            for (uint32_t i = tid; i < K; i += nt) {
+                const float v = xs[i];
+                if (blockIdx.x == 0 && in.x_out) in.x_out[i] = v;
+                ss += (double)v * (double)v;
+            }
+        }
+        const double r = inv_rms(block_sum_d(ss, red), K, in.eps_n);
+        for (uint32_t i = tid; i < K; i += nt) xs[i] = norm_apply(xs[i], r, in.w_n[i]);
+        __syncthreads();
+    }
+}
+
+// ---- Q4_0 GEMV --------------------------------------------------------------------------------
+//
+// A workgroup has S * G waves.  The S waves of a wave-group split the columns
+// into S slices of at most 128 blocks; lane l owns blocks l and l + 64 of its
+// slice for the whole kernel, so its 64 input values stay in registers and
+// each weight row costs it two 16-byte code loads and two scale loads.  A
+// wave-group computes R rows per iteration (R / 2 gate/up pairs for OUT_GELU);
+// lanes reduce over the wave, slices over LDS in slice order.
+//
+// Per 32-weight block: sum (q - 8) x = sum q x - 8 sum x.  Low nibbles are
+// converted directly; high nibbles are converted in place (16 q) against
+// x / 16, which is exact.
+
+__device__ __forceinline__ float q4_block_dot(uint4 c, const float* xl, const float* xh) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = w[k] & 0xF0F0F0F0u;
+        s0 = fmaf((float)(lo & 0xFFu), xl[4 * k + 0], s0);
+        s0 = fmaf((float)((lo >> 8) & 0xFFu), xl[4 * k + 1], s0);
+        s0 = fmaf((float)((lo >> 16) & 0xFFu), xl[4 * k + 2], s0);
+        s0 = fmaf((float)(lo >> 24), xl[4 * k + 3], s0);
+        s1 = fmaf((float)(hi & 0xFFu), xh[4 * k + 0], s1);
+        s1 = fmaf((float)((hi >> 8) & 0xFFu), xh[4 * k + 1], s1);
+        s1 = fmaf((float)((hi >> 16) & 0xFFu), xh[4 * k + 2], s1);
+        s1 = fmaf((float)(hi >> 24), xh[4 * k + 3], s1);
+    }
+    return s0 + s1;
+}
+
+template <int R, int S, int IN, int OUT>
+__global__ __launch_bounds__(256) void q4_gemv_kernel(Q4Args a, uint32_t out_rows) {
+    constexpr int G = S >= 4 ? 1 : 4 / S;
+    constexpr int RP = OUT == OUT_GELU ? R / 2 : R;
+    extern __shared__ float xs[];
+    __shared__ double red[8];
+    __shared__ float part[G][S][R];
+
+    if (a.state && a.state[ST_STOP]) return;
+    const uint32_t B = a.w.blocks, K = B * 32;
+    input_stage<IN>(a.in, xs, K, red);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int s = wave % S, g = wave / S;
+    const uint32_t P = (B + S - 1) / S, sb = s * P, se = min(B, sb + P);
+    const uint32_t b0 = sb + lane, b1 = sb + 64 + lane;
+    const bool v0 = b0 < se, v1 = b1 < se;
+
+    float xl0[16], xh0[16], xl1[16], xh1[16];
+    float sx0 = 0.0f, sx1 = 0.0f;
+    {
+        const uint32_t i0 = (v0 ? b0 : 0) * 32, i1 = (v1 ? b1 : 0) * 32;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            const float l0 = v0 ? xs[i0 + j] : 0.0f, h0 = v0 ? xs[i0 + 16 + j] : 0.0f;
+            const float l1 = v1 ? xs[i1 + j] : 0.0f, h1 = v1 ? xs[i1 + 16 + j] : 0.0f;
+            xl0[j] = l0;
+            xh0[j] = h0 * 0.0625f;
+            xl1[j] = l1;
+            xh1[j] = h1 * 0.0625f;
+            sx0 += l0 + h0;
+            sx1 += l1 + h1;
+        }
+    }
+    const float bias0 = 8.0f * sx0, bias1 = 8.0f * sx1;
+
+    const uint32_t ngroups = (out_rows + RP - 1) / RP;
+    for (uint32_t base = blockIdx.x; base * G < ngroups; base += gridDim.x) {
+        const uint32_t grp = base * G + g;
+        const bool gactive = grp < ngroups;
+        uint4 c0[R], c1[R];
+        uint16_t d0[R], d1[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const Q4View& m = (OUT == OUT_GELU && i >= RP) ? a.w2 : a.w;
+            const uint32_t row = OUT == OUT_GELU ? grp * RP + (i % RP) : grp * R + i;
+            const bool ok = gactive && row < m.rows;
+            const size_t rb = (size_t)row * B;
+            c0[i] = (ok && v0) ? *reinterpret_cast<const uint4*>(m.codes + (rb + b0) * 16) : make_uint4(0, 0, 0, 0);
+            c1[i] = (ok && v1) ? *reinterpret_cast<const uint4*>(m.codes + (rb + b1) * 16) : make_uint4(0, 0, 0, 0);
+            d0[i] = (ok && v0) ? m.scales[rb + b0] : (uint16_t)0;
+            d1[i] = (ok && v1) ? m.scales[rb + b1] : (uint16_t)0;
+        }
+        float acc[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            float t = h2f(d0[i]) * (q4_block_dot(c0[i], xl0, xh0) - bias0);
+            t = fmaf(h2f(d1[i]), q4_block_dot(c1[i], xl1, xh1) - bias1, t);
+            acc[i] = wave_sum(t);
+        }
+        if constexpr (S > 1) {
+            if (lane == 0) {
+#pragma unroll
+                for (int i = 0; i < R; ++i) part[g][s][i] = acc[i];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                float t = part[g][0][i];
+#pragma unroll
+                for (int q = 1; q < S; ++q) t += part[g][q][i];
+                acc[i] = t;
+            }
+            __syncthreads();
+        }
+        if (s == 0 && gactive) {
+            if constexpr (OUT == OUT_GELU) {
+                float gv = acc[0], uv = acc[RP];
+#pragma unroll
+                for (int i = 1; i < RP; ++i)
+                    if (lane == i) {
+                        gv = acc[i];
+                        uv = acc[RP + i];
+                    }
+                const uint32_t row = grp * RP + lane;
+                if (lane < RP && row < out_rows) a.y[row] = gelu_mul(gv, uv);
+            } else {
+                float v = acc[0];
+#pragma unroll
+                for (int i = 1; i < R; ++i)
+                    if (lane == i) v = acc[i];
+                const uint32_t row = grp * R + lane;
+                if (lane < R && row < out_rows) a.y[row] = OUT == OUT_ADD ? __fadd_rn(v, a.add[row]) : v;
+            }
+        }
+    }
+}
+
+template <int R, int S, int IN, int OUT>
+static hipError_t q4_launch3(const Q4Args& a, uint32_t out_rows, hipStream_t st) {
+    constexpr int G = S >= 4 ? 1 : 4 / S;
+    constexpr int RP = OUT == OUT_GELU ? R / 2 : R;
+    const uint32_t ngroups = (out_rows + RP - 1) / RP;
+    uint32_t grid = (ngroups + G - 1) / G;
+    if (grid > 8192) grid = 8192;
+    const size_t lds = (size_t)a.w.blocks * 32 * sizeof(float);
+    hipLaunchKernelGGL((q4_gemv_kernel<R, S, IN, OUT>), dim3(grid), dim3(64 * S * G), lds, st, a, out_rows);
+    return hipGetLastError();
+}
+
+template <int IN, int OUT>
+static hipError_t q4_launch2(const Q4Args& a, uint32_t out_rows, hipStream_t st) {
+    const uint32_t B = a.w.blocks;
+    if (B <= 128) return q4_launch3<OUT == OUT_GELU ? 8 : 4, 1, IN, OUT>(a, out_rows, st);
+    if (B <= 256) return q4_launch3<OUT == OUT_GELU ? 8 : 4, 2, IN, OUT>(a, out_rows, st);
+    if (B <= 512) return q4_launch3<OUT == OUT_GELU ? 8 : 4, 4, IN, OUT>(a, out_rows, st);
+    return hipErrorInvalidValue;
+}
+
+template <int IN>
+static hipError_t q4_launch1(const Q4Args& a, int out_kind, uint32_t out_rows, hipStream_t st) {
+    switch (out_kind) {
+        case OUT_PLAIN: return q4_launch2<IN, OUT_PLAIN>(a, out_rows, st);
+        case OUT_GELU: return q4_launch2<IN, OUT_GELU>(a, out_rows, st);
+        case OUT_ADD: return q4_launch2<IN, OUT_ADD>(a, out_rows, st);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s) {
+    switch (in_kind) {
+        case IN_PLAIN: return q4_launch1<IN_PLAIN>(a, out_kind, out_rows, s);
+        case IN_NORM: return q4_launch1<IN_NORM>(a, out_kind, out_rows, s);
+        case IN_RESID: return q4_launch1<IN_RESID>(a, out_kind, out_rows, s);
+        case IN_EMBED: return q4_launch1<IN_EMBED>(a, out_kind, out_rows, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+// ---- Q6_K head GEMV with fused greedy argmax --------------------------------------------------
+//
+// Lane u of every wave owns 64-weight unit u of each row (units <= 64, i.e.
+// columns <= 4096), with its 64 inputs in registers.  Waves stride over rows
+// R at a time; each keeps the best (value, smallest id) and a non-finite flag.
+// The last block to finish reduces the per-block partials and, in step mode,
+// appends the id to the session's token array and advances the position.
+
+__device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t bi) {
+    return v > bv || (v == bv && i < bi);
+}
+
+template <int IN>
+__global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
+    constexpr int R = kHeadRows;
+    extern __shared__ float xs[];
+    __shared__ double red[8];
+    __shared__ float wv[256];
+    __shared__ uint32_t wi[256], wb[256];
+    __shared__ bool last;
+
+    if (a.state && a.state[ST_STOP]) return;
+    const uint32_t units = a.w.units, K = units * 64, sblocks = units / 4;
+    input_stage<IN>(a.in, xs, K, red);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const bool act = (uint32_t)lane < units;
+    const uint32_t u = act ? (uint32_t)lane : 0;
+    const uint32_t sbk = u >> 2, base = sbk * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16;
+    float x[4][16], bias[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        float t = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            x[q][j] = act ? xs[base + q * 32 + j] : 0.0f;
+            t += x[q][j];
+        }
+        bias[q] = 32.0f * t;
+    }
+
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu, bad = 0;
+    const uint32_t rows = a.w.rows;
+    const uint32_t stride = gridDim.x * 4 * R;
+    for (uint32_t r0 = (blockIdx.x * 4 + wave) * R; r0 < rows; r0 += stride) {
+        uint4 A[R], Bq[R], H[R];
+        uint32_t S4[R];
+        uint16_t D[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const uint32_t row = r0 + i;
+            const bool ok = act && row < rows;
+            const size_t o = ((size_t)row * units + u) * 16;
+            A[i] = ok ? *reinterpret_cast<const uint4*>(a.w.a + o) : make_uint4(0, 0, 0, 0);
+            Bq[i] = ok ? *reinterpret_cast<const uint4*>(a.w.b + o) : make_uint4(0, 0, 0, 0);
+            H[i] = ok ? *reinterpret_cast<const uint4*>(a.w.h + o) : make_uint4(0, 0, 0, 0);
+            S4[i] = ok ? a.w.s[(size_t)row * units + u] : 0u;
+            D[i] = ok ? a.w.d[(size_t)row * sblocks + sbk] : (uint16_t)0;
+        }
+        float acc[R];
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            const uint32_t av[4] = {A[i].x, A[i].y, A[i].z, A[i].w};
+            const uint32_t bw[4] = {Bq[i].x, Bq[i].y, Bq[i].z, Bq[i].w};
+            const uint32_t hv[4] = {H[i].x, H[i].y, H[i].z, H[i].w};
+            const float d = h2f(D[i]);
+            float t = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                float sq = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    const uint32_t c = q6_codes(av[k], bw[k], hv[k], q);
+                    sq = fmaf((float)(c & 0xFFu), x[q][4 * k + 0], sq);
+                    sq = fmaf((float)((c >> 8) & 0xFFu), x[q][4 * k + 1], sq);
+                    sq = fmaf((float)((c >> 16) & 0xFFu), x[q][4 * k + 2], sq);
+                    sq = fmaf((float)(c >> 24), x[q][4 * k + 3], sq);
+                }
+                const float ds = d * (float)(int8_t)(S4[i] >> (8 * q));
+                t = fmaf(ds, sq - bias[q], t);
+            }
+            acc[i] = wave_sum(t);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const uint32_t row = r0 + i;
+                if (row < rows) {
+                    const float v = acc[i];
+                    if (!isfinite(v)) bad = 1;
+                    else if (better(v, row, bv, bi)) {
+                        bv = v;
+                        bi = row;
+                    }
+                }
+            }
+        }
+        if (a.logits) {
+            float v = acc[0];
+#pragma unroll
+            for (int i = 1; i < R; ++i)
+                if (lane == i) v = acc[i];
+            if (lane < R && r0 + lane < rows) a.logits[r0 + lane] = v;
+        }
+    }
+    if (lane == 0) {
+        wv[wave] = bv;
+        wi[wave] = bi;
+        wb[wave] = bad;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) {
+            if (better(wv[w], wi[w], bv, bi)) {
+                bv = wv[w];
+                bi = wi[w];
+            }
+            bad |= wb[w];
+        }
+        a.partial[blockIdx.x] = make_uint4(__float_as_uint(bv), bi, bad, 0u);
+        __threadfence();
+        const uint32_t ticket = atomicAdd(a.counter, 1u);
+        last = ticket == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    float v = -INFINITY;
+    uint32_t id = 0xFFFFFFFFu, flag = 0;
+    for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
+        const uint4 p = a.partial[b];
+        const float pv = __uint_as_float(p.x);
+        if (better(pv, p.y, v, id)) {
+            v = pv;
+            id = p.y;
+        }
+        flag |= p.z;
+    }
+    wv[threadIdx.x] = v;
+    wi[threadIdx.x] = id;
+    wb[threadIdx.x] = flag;
+    __syncthreads();
+    for (uint32_t h = blockDim.x / 2; h > 0; h >>= 1) {
+        if (threadIdx.x < h) {
+            const uint32_t o = threadIdx.x + h;
+            if (better(wv[o], wi[o], wv[threadIdx.x], wi[threadIdx.x])) {
+                wv[threadIdx.x] = wv[o];
+                wi[threadIdx.x] = wi[o];
+            }
+            wb[threadIdx.x] |= wb[o];
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        const uint32_t best = wi[0], flagged = wb[0] || best >= rows;
+        if (a.result) {
+            a.result[0] = best;
+            a.result[1] = flagged;
+        }
+        if (a.state) {
+            const uint32_t pos = a.state[ST_POS];
+            uint32_t stop = flagged;
+            for (uint32_t i = 0; i < a.state[ST_NSTOP]; ++i)
+                if (a.stop_ids[i] == best) stop = 1u;
+            a.ids[pos + 1] = best;
+            if (flagged) a.state[ST_BAD] = 1u;
+            if (stop) a.state[ST_STOP] = 1u;
+            a.state[ST_POS] = pos + 1;
+            if (a.records) {
+                StepRecord r;
+                r.id = best;
+                r.bad = flagged;
+                r.stop = stop;
+                r.done = 1u;
+                a.records[pos + 1] = r;
+            }
+        }
+        *a.counter = 0u;
+    }
+}
+
+uint32_t head_grid(uint32_t rows) {
+    uint32_t per_block = 4 * kHeadRows;
+    uint32_t g = (rows + per_block - 1) / per_block;
+    return g > 2048 ? 2048 : g;
+}
+
+hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s) {
+    const size_t lds = (size_t)a.w.units * 64 * sizeof(float);
+    switch (in_kind) {
+        case IN_PLAIN: hipLaunchKernelGGL(q6_head_kernel<IN_PLAIN>, dim3(grid), dim3(256), lds, s, a); break;
+        case IN_NORM: hipLaunchKernelGGL(q6_head_kernel<IN_NORM>, dim3(grid), dim3(256), lds, s, a); break;
+        case IN_RESID: hipLaunchKernelGGL(q6_head_kernel<IN_RESID>, dim3(grid), dim3(256), lds, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---- GQA decode attention ---------------------------------------------------------------------
+//
+// Grid (cmax, kv_heads), 256 threads.  Each block takes one chunk of the
+// visible range [max(0, pos + 1 - window), pos] for one KV head and its GQ
+// query heads.  Prologue: q-norm + NeoX RoPE of the query heads (double angle,
+// double rotation, f32 result); the block whose chunk ends at pos also
+// normalises and rotates the new key, optionally normalises the value, rounds
+// both to fp16 and appends them at slot pos % ring.  Then scores (16 lanes per
+// token), chunk softmax, and p-weighted values; chunk partials (acc, max, sum)
+// are merged by the last block of the KV head.
+
+template <int D, int GQ>
+__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+    static_assert(D == 256, "one thread per channel");
+    __shared__ float qs[GQ][D];
+    __shared__ float tmp[D];
+    __shared__ float scores[GQ][kAttnMaxChunkLen];
+    __shared__ float vred[8][GQ][D];
+    __shared__ double red[8];
+    __shared__ float fred[8];
+    __shared__ bool last;
+
+    const uint32_t tid = threadIdx.x;
+    if (a.state && a.state[ST_STOP]) return;
+    const uint32_t pos = a.state ? a.state[ST_POS] : a.position;
+    const uint32_t nvis = a.window ? min(pos + 1, a.window) : pos + 1;
+    const uint32_t start = pos + 1 - nvis;
+    uint32_t chunks = min(a.cmax, (nvis + a.min_chunk - 1) / a.min_chunk);
+    const uint32_t clen = (nvis + chunks - 1) / chunks;
+    chunks = (nvis + clen - 1) / clen;
+    const uint32_t c = blockIdx.x, kvh = blockIdx.y;
+    if (c >= chunks) return;
+    const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
+    const uint32_t n = t1 - t0;
+    const uint32_t ring = a.ring;
+
+    double sn = 0.0, cs = 1.0;
+    if (tid < D / 2) sincos((double)pos * a.inv_freq[tid], &sn, &cs);
+
+    auto norm_rope = [&](const float* src, const float* w, float eps, float* dst) {
+        const float v = src[tid];
+        const double r = inv_rms(block_sum_d((double)v * (double)v, red), D, eps);
+        tmp[tid] = norm_apply(v, r, w[tid]);
+        __syncthreads();
+        if (tid < D / 2) {
+            const double x = (double)tmp[tid], y = (double)tmp[tid + D / 2];
+            dst[tid] = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
+            dst[tid + D / 2] = (float)__dadd_rn(__dmul_rn(x, sn), __dmul_rn(y, cs));
+        }
+        __syncthreads();
+    };
+
+#pragma unroll
+    for (int gi = 0; gi < GQ; ++gi) norm_rope(a.q_raw + (size_t)(kvh * GQ + gi) * D, a.q_norm, a.q_eps, qs[gi]);
+
+    if (t1 == pos + 1) {  // this chunk holds the new token: append K and V
+        norm_rope(a.k_raw + (size_t)kvh * D, a.k_norm, a.k_eps, vred[0][0]);
+        float v = a.v_raw[(size_t)kvh * D + tid];
+        if (a.v_norm) {
+            const double r = inv_rms(block_sum_d((double)v * (double)v, red), D, a.v_eps);
+            v = (float)__dmul_rn((double)v, r);
+        }
+        const size_t slot = ((size_t)kvh * ring + pos % ring) * D + tid;
+        a.kcache[slot] = f2h(vred[0][0][tid]);
+        a.vcache[slot] = f2h(v);
+        __syncthreads();
+    }
+
+    // scores: 16 lanes per token, 16 channels per lane
+    {
+        const uint32_t grp = tid >> 4, j = tid & 15;
+        float qr[GQ][16];
+#pragma unroll
+        for (int gi = 0; gi < GQ; ++gi)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) qr[gi][e] = qs[gi][16 * j + e];
+        for (uint32_t t = t0 + grp; t < t1; t += 16) {
+            const uint16_t* kp = a.kcache + ((size_t)kvh * ring + t % ring) * D + 16 * j;
+            const uint4 k0 = *reinterpret_cast<const uint4*>(kp);
+            const uint4 k1 = *reinterpret_cast<const uint4*>(kp + 8);
+            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+            float kf[16];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
+                kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
+            }
+#pragma unroll
+            for (int gi = 0; gi < GQ; ++gi) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
+#pragma unroll
+                for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+                if (j == 0) scores[gi][t - t0] = d * a.scale;
+            }
+        }
+    }
+    __syncthreads();
+
+    float m[GQ], l[GQ];
+#pragma unroll
+    for (int gi = 0; gi < GQ; ++gi) {
+        float mx = -INFINITY;
+        for (uint32_t i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, scores[gi][i]);
+        m[gi] = block_max_f(mx, fred);
+        float sum = 0.0f;
+        for (uint32_t i = tid; i < n; i += blockDim.x) {
+            const float p = expf(scores[gi][i] - m[gi]);
+            scores[gi][i] = p;
+            sum += p;
+        }
+        l[gi] = block_sum_f(sum, fred);
+    }
+    __syncthreads();
+
+    // values: 32 lanes per token row, 8 channels per lane, 8 token groups
+    {
+        const uint32_t tg = tid >> 5, dl = tid & 31;
+        float acc[GQ][8];
+#pragma unroll
+        for (int gi = 0; gi < GQ; ++gi)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[gi][e] = 0.0f;
+        for (uint32_t t = t0 + tg; t < t1; t += 8) {
+            const uint4 vv = *reinterpret_cast<const uint4*>(a.vcache + ((size_t)kvh * ring + t % ring) * D + 8 * dl);
+            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+            float vf[8];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
+                vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
+            }
+#pragma unroll
+            for (int gi = 0; gi < GQ; ++gi) {
+                const float p = scores[gi][t - t0];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[gi][e] = fmaf(p, vf[e], acc[gi][e]);
+            }
+        }
+#pragma unroll
+        for (int gi = 0; gi < GQ; ++gi)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vred[tg][gi][8 * dl + e] = acc[gi][e];
+    }
+    __syncthreads();
+    float o[GQ];
+#pragma unroll
+    for (int gi = 0; gi < GQ; ++gi) {
+        float t = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 8; ++g) t += vred[g][gi][tid];
+        o[gi] = t;
+    }
+    if (chunks == 1) {
+#pragma unroll
+        for (int gi = 0; gi < GQ; ++gi) a.out[(size_t)(kvh * GQ + gi) * D + tid] = o[gi] / l[gi];
+        return;
+    }
+    const size_t stride = (size_t)GQ * (D + 2);
+    float* mine = a.part + ((size_t)kvh * a.cmax + c) * stride;
+#pragma unroll
+    for (int gi = 0; gi < GQ; ++gi) {
+        mine[gi * (D + 2) + tid] = o[gi];
+        if (tid == 0) {
+            mine[gi * (D + 2) + D] = m[gi];
+            mine[gi * (D + 2) + D + 1] = l[gi];
+        }
+    }
+    __syncthreads();
+    if (tid == 0) {
+        __threadfence();
+        const uint32_t ticket = atomicAdd(a.counters + kvh, 1u);
+        last = ticket == chunks - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    __threadfence();
+    const float* all = a.part + (size_t)kvh * a.cmax * stride;
+#pragma unroll
+    for (int gi = 0; gi < GQ; ++gi) {
+        float M = -INFINITY;
+        for (uint32_t k = 0; k < chunks; ++k) M = fmaxf(M, all[k * stride + gi * (D + 2) + D]);
+        float L = 0.0f, acc = 0.0f;
+        for (uint32_t k = 0; k < chunks; ++k) {
+            const float* p = all + k * stride + gi * (D + 2);
+            const float w = expf(p[D] - M);
+            L = fmaf(w, p[D + 1], L);
+            acc = fmaf(w, p[tid], acc);
+        }
+        a.out[(size_t)(kvh * GQ + gi) * D + tid] = acc / L;
+    }
+    if (tid == 0) a.counters[kvh] = 0u;
+}
+
+hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s) {
+    if (head_width != 256) return hipErrorInvalidValue;
+    const dim3 grid(a.cmax, a.kv_heads);
+    switch (group) {
+        case 1: hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((attention_kernel<256, 2>), grid, dim3(256), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((attention_kernel<256, 4>), grid, dim3(256), 0, s, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+// ---- small kernels ----------------------------------------------------------------------------
+
+// One block per vector: y = f32(x * rsqrt(mean(x^2) + eps) * w), reduction in double.
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* x, const float* w, float* y, uint32_t width,
+                                                      float eps) {
+    __shared__ double red[8];
+    const float* xv = x + (size_t)blockIdx.x * width;
+    float* yv = y + (size_t)blockIdx.x * width;
+    double ss = 0.0;
+    for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) ss += (double)xv[i] * (double)xv[i];
+    const double r = inv_rms(block_sum_d(ss, red), width, eps);
+    for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) yv[i] = norm_apply(xv[i], r, w[i]);
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t width, uint32_t vectors, float eps,
+                          hipStream_t s) {
+    hipLaunchKernelGGL(rmsnorm_kernel, dim3(vectors), dim3(256), 0, s, x, w, y, width, eps);
+    return hipGetLastError();
+}
+
+// One block: y = (f32(rms(x) * w_a) + res) * scale (w_a null: (x + res) * scale).
+__global__ __launch_bounds__(256) void resid_kernel(InputStage in, uint32_t width, float* y) {
+    __shared__ double red[8];
+    double ra = 1.0;
+    if (in.w_a) {
+        double sa = 0.0;
+        for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) sa += (double)in.x[i] * (double)in.x[i];
+        ra = inv_rms(block_sum_d(sa, red), width, in.eps_a);
+    }
+    for (uint32_t i = threadIdx.x; i < width; i += blockDim.x) {
+        const float t = in.w_a ? norm_apply(in.x[i], ra, in.w_a[i]) : in.x[i];
+        y[i] = __fmul_rn(__fadd_rn(t, in.res[i]), in.scale);
+    }
+}
+
+hipError_t launch_resid(const InputStage& in, uint32_t width, float* y, hipStream_t s) {
+    hipLaunchKernelGGL(resid_kernel, dim3(1), dim3(256), 0, s, in, width, y);
+    return hipGetLastError();
+}
+
+__global__ void advance_kernel(uint32_t* state) { state[ST_POS] += 1u; }
+
+hipError_t launch_advance(uint32_t* state, hipStream_t s) {
+    hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, state);
+    return hipGetLastError();
+}
+
+}  // namespace af

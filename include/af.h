@@ -1,0 +1,244 @@
+/*
+ * af.h - C ABI of the MI355X (gfx950) batch-1 decode backend.
+ *
+ * Drop-in boundary for AdaForge's GPU adapter: a Rust FFI crate binds these
+ * entry points to implement the application ports `GpuDiagnostics` and
+ * `GenerationSession` (crates/application/src/lib.rs:28-187, 1092-1126) in
+ * place of crates/cuda-backend (cudarc + NVRTC).  No HIP, CUDA or torch type
+ * crosses it: host buffers are plain pointers and sizes, device buffers are
+ * `void*`/typed pointers the caller obtained from HIP, streams are `void*`
+ * (a hipStream_t; NULL = the null stream).
+ *
+ * Errors: every entry point returns AF_OK or an AF_ERR_* code and leaves a
+ * message for af_last_error() (thread-local), mapping onto the reference's
+ * DiagnosticError(String) (crates/application/src/lib.rs:17-25).  Invalid
+ * arguments are rejected before any GPU work, as the reference validates
+ * before any CUDA call (crates/cuda-backend/src/stack.rs:60-84).
+ *
+ * Threading: a handle is used by one thread at a time; sessions own one
+ * private stream (crates/cuda-backend/src/stack.rs:863-866).
+ *
+ * Weight formats are GGUF's, as the reference's GGUF reader hands them over:
+ * Q4_0 (18 bytes per 32 weights: fp16 d, 16 nibble bytes), Q6_K (210 bytes
+ * per 256 weights), row-major [rows][blocks]; `columns` is the contiguous
+ * dimension (crates/model-formats/src/gguf.rs, README.md:76).
+ */
+#ifndef ADAFORGE_AF_H
+#define ADAFORGE_AF_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AF_OK 0
+#define AF_ERR_INVALID 1    /* rejected before any GPU work */
+#define AF_ERR_DEVICE 2     /* HIP runtime or launch failure */
+#define AF_ERR_NONFINITE 3  /* non-finite logits reached greedy selection */
+#define AF_ERR_POISONED 4   /* the session failed earlier and must be closed */
+#define AF_ERR_NO_DEVICE 5  /* no gfx950 device */
+
+#define AF_MAX_CONTEXT 32768u  /* crates/cuda-backend/src/stack.rs:18 (MAX_CONTEXT) */
+#define AF_MAX_NEW_TOKENS 128u /* crates/cuda-backend/src/stack.rs:1183 (1..=128 per generate) */
+#define AF_MAX_PROMPT 32768u
+
+/* Message of the last failure on this thread ("" if none). */
+const char* af_last_error(void);
+
+/* ---- device query: GpuDiagnostics::check (crates/application/src/lib.rs:178,
+ *      crates/cuda-backend/src/lib.rs:208-300, device-identity part) ---------------------------- */
+typedef struct {
+    char name[256];
+    char arch[64];             /* "gfx950..." */
+    int32_t compute_units;
+    uint64_t free_memory_bytes;
+    uint64_t total_memory_bytes;
+} af_device_info;
+int af_device_query(af_device_info* out);
+
+/* ---- host-level diagnostics ----------------------------------------------------------------- */
+
+/* GPU half of GpuDiagnostics::check_matvec (crates/application/src/lib.rs:179-186 ->
+ * crates/cuda-backend/src/matvec.rs:9-122).  Uploads the Q4_0 matrix (validated as
+ * Q4Matrix::new, crates/domain/src/q4.rs:9-28), runs y = W x once for each of the
+ * n_inputs vectors (inputs: [n_inputs][columns]), then 1 warm-up and
+ * `timed_repetitions` timed launches on the last vector; outputs: [n_inputs][rows];
+ * *median_ms: median kernel time (0 if timed_repetitions == 0).  The caller compares
+ * against Q4Matrix::reference_matvec with compare() (matvec.rs:175-193). */
+int af_matvec_run(const uint8_t* q4, size_t len, uint32_t columns, uint32_t rows, const float* inputs,
+                  uint32_t n_inputs, uint32_t timed_repetitions, float* outputs, float* median_ms);
+
+/* GPU half of GpuDiagnostics::check_rms_norm (crates/application/src/lib.rs:172-177 ->
+ * crates/cuda-backend/src/rms_norm.rs:9-130): `vectors` rows of `width` normalised with
+ * the weights (validated as RmsNorm::new, crates/domain/src/rms_norm.rs:8-16), 1 warm-up
+ * and `timed_repetitions` timed launches; outputs: [vectors][width]. */
+int af_rmsnorm_run(const float* weights, uint32_t width, float eps, const float* inputs, uint32_t vectors,
+                   uint32_t timed_repetitions, float* outputs, float* median_ms);
+
+/* ---- device-resident operators (device pointers, caller's stream) ---------------------------- */
+
+typedef struct af_q4 af_q4; /* a Q4_0 matrix resident on the device */
+typedef struct af_q6 af_q6; /* a Q6_K matrix resident on the device */
+
+/* Q4Matrix upload (crates/domain/src/q4.rs:9-28 validation; crates/cuda-backend/src/matvec.rs:36-38). */
+int af_q4_upload(const uint8_t* q4, size_t len, uint32_t columns, uint32_t rows, af_q4** out);
+void af_q4_free(af_q4* m);
+/* y[rows] = W x[columns] (kernels/ada/q4_matvec.cu q4_matvec, launched by matvec.rs:72-101). */
+int af_q4_gemv(const af_q4* m, const float* x, float* y, void* stream);
+
+/* Q6Matrix upload (crates/domain/src/q6.rs:8-20; crates/cuda-backend/src/logits.rs:292-316). */
+int af_q6_upload(const uint8_t* q6, size_t len, uint32_t columns, uint32_t rows, af_q6** out);
+void af_q6_free(af_q6* m);
+/* Raw logits = W x and greedy selection (ResidentHead::project_gpu + GpuGreedy::select,
+ * crates/cuda-backend/src/logits.rs:424-467, greedy.rs:135-184): result (device, 2 words)
+ * receives [argmax id (largest value, smallest id on ties), non-finite flag]; logits
+ * (device, rows floats) may be NULL. */
+int af_q6_gemv_argmax(const af_q6* m, const float* x, float* logits, uint32_t* result, void* stream);
+
+/* RMSNorm of `vectors` contiguous rows (kernels/ada/rms_norm.cu rms_norm, rms_norm.rs:72-108). */
+int af_rmsnorm(const float* x, const float* weights, float* y, uint32_t width, uint32_t vectors, float eps,
+               void* stream);
+
+/* Host-side weight descriptors, mirroring the domain types the ports borrow
+ * (crates/application/src/lib.rs:919-927, 1049-1053). */
+typedef struct {
+    const float* weights; /* host, len floats */
+    uint32_t len;
+    float epsilon;
+} af_rms_norm;
+
+typedef struct {
+    const uint8_t* bytes; /* host GGUF Q4_0 / Q6_K blocks */
+    size_t len;
+    uint32_t columns;
+    uint32_t rows;
+} af_matrix;
+
+typedef struct {
+    uint32_t width;       /* head width (pairs i, i + width/2) */
+    double base;          /* theta */
+    const float* factors; /* host, width/2 frequency divisors (crates/domain/src/rope.rs:11-34) */
+    uint32_t context;
+} af_rope_params;
+
+typedef struct {
+    uint32_t q_heads;
+    uint32_t kv_heads;
+    uint32_t width;
+    uint32_t window; /* 0: global (None) */
+    float scale;     /* score scale (crates/domain/src/attention.rs:11-35) */
+} af_attention_config;
+
+/* Ffn (crates/domain/src/ffn.rs:60-94): pre-norm, gate/up (tanh-GELU(gate) * up), down,
+ * optional post-norm (post.weights NULL: none), then (post + x) * layer_scale. */
+typedef struct {
+    af_rms_norm pre;
+    af_matrix gate, up, down;
+    af_rms_norm post;
+    float layer_scale;
+} af_ffn_weights;
+
+typedef struct af_ffn af_ffn;
+int af_ffn_create(const af_ffn_weights* w, af_ffn** out);
+void af_ffn_free(af_ffn* f);
+/* FfnKernel::run (crates/cuda-backend/src/ffn.rs:290-516): y = Ffn(x); x, y device [hidden]. */
+int af_ffn_run(af_ffn* f, const float* x, float* y, void* stream);
+
+/* Decode attention for one token (AttentionKernel + prepare_qkv + cache append,
+ * crates/cuda-backend/src/attention.rs:107-170, stack.rs:332-497): per-head RMSNorm and
+ * NeoX RoPE of q and k at `position`, optional unit-weight RMSNorm of v, K/V rounded to
+ * fp16 and appended at slot position % ring of the caches ([kv_heads][ring][width] fp16,
+ * device), then softmax(scale q.k) v over [max(0, position + 1 - window), position]. */
+typedef struct {
+    const float* q;      /* device [q_heads][width], raw projection outputs */
+    const float* k;      /* device [kv_heads][width] */
+    const float* v;      /* device [kv_heads][width] */
+    const float* q_norm; /* device [width] */
+    const float* k_norm; /* device [width] */
+    float q_eps, k_eps, v_eps;
+    int32_t v_norm;
+    af_rope_params rope; /* factors on the host */
+    af_attention_config config;
+    uint16_t* k_cache;   /* device fp16 */
+    uint16_t* v_cache;
+    uint32_t ring;       /* cache slots; >= window for local layers, >= position + 1 otherwise */
+    uint32_t position;
+    float* out;          /* device [q_heads][width] */
+} af_attention_args;
+int af_attention_decode(const af_attention_args* args, void* stream);
+
+/* ---- generation session: GpuDiagnostics::open_session / generate and GenerationSession
+ *      (crates/application/src/lib.rs:29-47, 1092-1126; crates/cuda-backend/src/stack.rs:820-966,
+ *      1146-1480) -------------------------------------------------------------------------- */
+
+#define AF_LAYER_V_NORM 1u /* unit-weight RMSNorm of V with the input-norm epsilon (stack.rs:687-688) */
+
+typedef struct {
+    af_rms_norm input_norm;
+    af_matrix matrices[3];   /* q, k, v; v.bytes == k.bytes: V shares K's weights (stack.rs:172) */
+    af_rms_norm head_norms[2];
+    af_rope_params rope;
+    af_attention_config attention;
+    af_matrix output;        /* AttentionOutput (crates/domain/src/attention_output.rs) */
+    af_rms_norm output_norm;
+    af_ffn_weights ffn;
+    uint32_t flags;
+} af_layer_weights;
+
+typedef struct {
+    af_rms_norm norm;
+    af_matrix matrix; /* tied Q6_K embedding / lm-head */
+    float cap;        /* final softcap (selection uses raw logits, logits.rs:267-276) */
+} af_output_head;
+
+typedef struct {
+    uint64_t prompt_tokens;
+    uint64_t cached_tokens;
+    double prefill_ms;
+    double first_token_ms;
+    int32_t has_first_token;
+    uint64_t decode_tokens;
+    double decode_ms;
+    double total_ms;
+} af_generation_stats; /* GenerationStats (crates/application/src/lib.rs:1067-1076) */
+
+typedef void (*af_token_fn)(void* user, uint32_t id);
+typedef struct af_session af_session;
+
+/* open_session: uploads every layer and the head, allocates KV caches for `capacity`
+ * tokens (1..AF_MAX_CONTEXT) and captures the decode step as a graph. */
+int af_session_open(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head,
+                    uint32_t capacity, af_session** out);
+/* GenerationSession::generate / generate_stream (stack.rs:1171-1386): prompt must extend the
+ * session's cached tokens; at most max_new (1..AF_MAX_NEW_TOKENS) greedy ids, stopping before
+ * any id in `stop` (non-empty).  on_token may be NULL.  ids_out holds >= max_new ids. */
+int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop,
+                        size_t n_stop, uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out,
+                        size_t* n_out, int32_t* stopped, af_generation_stats* stats);
+/* GenerationSession::reset (stack.rs:1469-1480). */
+int af_session_reset(af_session* s);
+void af_session_close(af_session* s);
+
+/* GpuDiagnostics::generate (crates/application/src/lib.rs:38-47, stack.rs:820-833): a session
+ * sized prompt + max_new, one generation, closed. */
+int af_generate(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head,
+                const uint32_t* prompt, size_t n_prompt, const uint32_t* stop, size_t n_stop, uint32_t max_new,
+                uint32_t* ids_out, size_t* n_out, int32_t* stopped, af_generation_stats* stats);
+
+/* GPU half of GpuDiagnostics::check_layer_stack / check_logits (crates/application/src/lib.rs:49-66,
+ * crates/cuda-backend/src/stack.rs:707-817): consumes `ids` at the session's next positions
+ * with direct launches and returns every layer's output per token (layer_outputs:
+ * [n][layers][hidden], may be NULL), the fp16 K and V each layer appended per token
+ * (kv_appended: [n][layers][2][kv_rows] fp16 bits, kv_rows = the largest kv_heads * width, may be
+ * NULL), the raw logits after the last token (logits: [vocabulary], may be NULL) and the final
+ * RMSNorm input after the last token (hidden: [hidden], may be NULL).  The ids join the
+ * session's cached tokens. */
+int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_outputs, uint16_t* kv_appended,
+                     float* logits, float* hidden);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -47,6 +47,7 @@ def _load():
         "or_embedding": (i32, [P, u32, u32, P, sz, i32, P]),
         "or_greedy": (i32, [P, sz, P]),
         "or_compare": (i32, [P, P, sz, f64, f64, P, P, P]),
+        "or_layer_forward": (i32, [P, u32, u32, P, P, P, u32, i32, P, P, P, i32]),
         "or_model_new": (P, [u32, u32, u32, P, P, u32, P, f32, u32, i32]),
         "or_model_free": (None, [P]),
         "or_model_reset": (None, [P]),
@@ -249,6 +250,53 @@ class Layer(ctypes.Structure):
     ]
 
 
+def layer_table(model):
+    """or_layer descriptors for a synthetic model (adaforge_amd.synth.SynthModel)."""
+    n = len(model.layers)
+    table = (Layer * n)()
+    for i, L in enumerate(model.layers):
+        t = table[i]
+        t.input_norm, t.input_eps = _p(L.input_norm), L.eps
+        t.q, t.k = _p(L.q), _p(L.k)
+        t.v = _p(L.k) if L.v is None else _p(L.v)
+        t.q_norm, t.q_eps = _p(L.q_norm), L.eps
+        t.k_norm, t.k_eps = _p(L.k_norm), L.eps
+        t.rope_base, t.rope_factors, t.rope_context = L.rope_base, _p(L.rope_factors), L.rope_context
+        t.q_heads, t.kv_heads, t.head_width = L.q_heads, L.kv_heads, L.head_width
+        t.window, t.scale = L.window or 0, L.scale
+        t.o, t.post_attn_norm, t.post_attn_eps = _p(L.o), _p(L.post_attn_norm), L.eps
+        t.ffn_norm, t.ffn_eps = _p(L.ffn_norm), L.eps
+        t.gate, t.up, t.down = _p(L.gate), _p(L.up), _p(L.down)
+        t.post_ffn_norm, t.post_ffn_eps, t.layer_scale = _p(L.post_ffn_norm), L.eps, L.layer_scale
+        t.v_norm, t.kv_fp16 = int(L.v_norm), 1
+    return table
+
+
+def layer_forward(model, table, index, x, keys, values, position, given_kv=False, threads=None):
+    """One layer (stack.rs:670-700) on input x with the K/V history `keys`/`values`
+    ([position + 1][kv_rows] float32, modified in place unless given_kv).  Returns
+    (output float32[hidden], the layer's own new k, new v)."""
+    L = model.layers[index]
+    kn = L.kv_heads * L.head_width
+    x = _f32(x)
+    assert keys.dtype == np.float32 and keys.flags.c_contiguous and keys.size >= (position + 1) * kn
+    y = np.empty(model.hidden, np.float32)
+    kn_, vn_ = np.empty(kn, np.float32), np.empty(kn, np.float32)
+    _check(_lib.or_layer_forward(ctypes.byref(table[index]), model.hidden, model.intermediate, _p(x), _p(keys),
+                                 _p(values), position, 1 if given_kv else 0, _p(kn_), _p(vn_), _p(y),
+                                 threads or THREADS), "layer rejected")
+    return y, kn_, vn_
+
+
+def f16_ulps(a, b):
+    """Distance in fp16 units in the last place between two arrays of fp16-representable floats."""
+    ia = np.asarray(a, np.float32).astype(np.float16).view(np.int16).astype(np.int32)
+    ib = np.asarray(b, np.float32).astype(np.float16).view(np.int16).astype(np.int32)
+    ia = np.where(ia < 0, -32768 - ia, ia)
+    ib = np.where(ib < 0, -32768 - ib, ib)
+    return np.abs(ia - ib)
+
+
 class Model:
     """Whole-model CPU chain (stack.rs:670-700) over a synthetic model description.
 
@@ -258,22 +306,7 @@ class Model:
     def __init__(self, model, capacity, threads=None):
         self._keep = model
         n = len(model.layers)
-        table = (Layer * n)()
-        for i, L in enumerate(model.layers):
-            t = table[i]
-            t.input_norm, t.input_eps = _p(L.input_norm), L.eps
-            t.q, t.k = _p(L.q), _p(L.k)
-            t.v = _p(L.k) if L.v is None else _p(L.v)
-            t.q_norm, t.q_eps = _p(L.q_norm), L.eps
-            t.k_norm, t.k_eps = _p(L.k_norm), L.eps
-            t.rope_base, t.rope_factors, t.rope_context = L.rope_base, _p(L.rope_factors), L.rope_context
-            t.q_heads, t.kv_heads, t.head_width = L.q_heads, L.kv_heads, L.head_width
-            t.window, t.scale = L.window or 0, L.scale
-            t.o, t.post_attn_norm, t.post_attn_eps = _p(L.o), _p(L.post_attn_norm), L.eps
-            t.ffn_norm, t.ffn_eps = _p(L.ffn_norm), L.eps
-            t.gate, t.up, t.down = _p(L.gate), _p(L.up), _p(L.down)
-            t.post_ffn_norm, t.post_ffn_eps, t.layer_scale = _p(L.post_ffn_norm), L.eps, L.layer_scale
-            t.v_norm, t.kv_fp16 = int(L.v_norm), 1
+        table = layer_table(model)
         self._table = table
         self.hidden, self.vocabulary = model.hidden, model.vocabulary
         self.layers = n
@@ -315,3 +348,53 @@ class Model:
                                       ctypes.byref(n), ctypes.byref(stopped), _p(margins)), "generation rejected")
         k = n.value
         return ids[:k].tolist(), bool(stopped.value), margins[:k + int(stopped.value)]
+
+
+def check_layer_stack(model, ids, outputs, kv, atol=1e-4, rtol=1e-4, kv_slack=1e-5, threads=None):
+    """Teacher-forced check of a GPU trace (crates/cuda-backend/src/stack.rs:707-817 contract).
+
+    For each token t (positions 0..n-1 from an empty cache) and layer l the oracle runs layer l
+    on the GPU's own layer input (the embedding for l = 0, else the GPU's output of layer l - 1)
+    with the GPU's own fp16 K/V history, including the K/V the GPU appended at t, and the GPU's
+    layer output must lie within atol + rtol |ref| on every element.
+
+    The appended K/V themselves are checked against the oracle's own values for the same input
+    before the fp16 boundary: each GPU fp16 value must be within one fp16 ulp of the oracle's
+    value plus kv_slack times the largest magnitude in that head (the two sides agree to about
+    1e-7 of the head's scale before rounding, which near zero spans several fp16 ulps).
+
+    outputs: [n][layers][hidden]; kv: [n][layers][2][kv_rows] float32 (fp16 values).
+    Returns (max layer tolerance ratio, max K/V ratio (<= 1 passes), number of K/V values whose
+    fp16 rounding differs from the oracle's)."""
+    H, V = model.hidden, model.vocabulary
+    n = len(ids)
+    table = layer_table(model)
+    emb = embedding(model.table, H, V, ids, scaled=True).reshape(n, H)
+    hist = []
+    for L in model.layers:
+        kn = L.kv_heads * L.head_width
+        hist.append((np.zeros(n * kn, np.float32), np.zeros(n * kn, np.float32), kn, L.head_width))
+    worst, kv_worst, differ = 0.0, 0.0, 0
+    for t in range(n):
+        for l in range(len(model.layers)):
+            keys, values, kn, hw = hist[l]
+            keys[t * kn:(t + 1) * kn] = kv[t, l, 0, :kn]
+            values[t * kn:(t + 1) * kn] = kv[t, l, 1, :kn]
+            x = emb[t] if l == 0 else outputs[t, l - 1]
+            y, k_own, v_own = layer_forward(model, table, l, x, keys, values, t, given_kv=True, threads=threads)
+            try:
+                _, r = compare(y.astype(np.float64), outputs[t, l], atol, rtol)
+            except OracleError as e:
+                raise OracleError(f"token {t}, layer {l}: {e}") from None
+            worst = max(worst, r)
+            for gpu, own in ((kv[t, l, 0, :kn], k_own), (kv[t, l, 1, :kn], v_own)):
+                own16 = own.astype(np.float16)
+                spacing = np.abs(np.spacing(own16)).astype(np.float64)
+                head_max = np.repeat(np.abs(own).reshape(-1, hw).max(axis=1), hw).astype(np.float64)
+                bound = spacing + kv_slack * head_max
+                ratio = np.abs(gpu.astype(np.float64) - own.astype(np.float64)) / bound
+                kv_worst = max(kv_worst, float(ratio.max()))
+                differ += int((gpu != own16.astype(np.float32)).sum())
+    if kv_worst > 1.0:
+        raise OracleError(f"appended K/V outside one fp16 ulp (+{kv_slack} x head max): ratio {kv_worst:.3g}")
+    return worst, kv_worst, differ

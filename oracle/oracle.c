@@ -563,31 +563,37 @@ static void to_f32(const double* a, float* b, size_t n) {
     for (size_t i = 0; i < n; ++i) b[i] = (float)a[i];
 }
 
-/* One layer at `position` on input x (hidden), output written to y. stack.rs:670-700 */
-static int layer_reference(or_model* m, uint32_t l, const float* x, float* y, uint32_t position) {
-    const or_layer* w = &m->layer[l];
-    uint32_t H = m->hidden, hw = w->head_width;
+/* One layer at `position` (crates/cuda-backend/src/stack.rs:670-700) on input x.  keys/values
+ * hold (position + 1) * kv_rows floats; entries < position are the cache.  If use_given_kv,
+ * entry `position` is taken as given; otherwise the layer's new K/V (normed, rotated, rounded
+ * to fp16 when kv_fp16) are stored there.  k_new/v_new (may be NULL) receive the layer's own
+ * new K/V before the fp16 rounding, either way, so a caller can compare a GPU's with them. */
+int or_layer_forward(const or_layer* w, uint32_t hidden, uint32_t intermediate, const float* x, float* keys,
+                     float* values, uint32_t position, int use_given_kv, float* k_new, float* v_new, float* y,
+                     int threads) {
+    uint32_t H = hidden, hw = w->head_width;
     uint32_t qn = w->q_heads * hw, kn = w->kv_heads * hw;
     uint32_t big = qn > H ? qn : H;
-    double* t = (double*)malloc(sizeof(double) * (big > m->intermediate ? big : m->intermediate));
+    double* t = (double*)malloc(sizeof(double) * (big > intermediate ? big : intermediate));
     float* normalized = (float*)malloc(sizeof(float) * H);
     float* q = (float*)malloc(sizeof(float) * qn);
     float* k = (float*)malloc(sizeof(float) * kn);
     float* v = (float*)malloc(sizeof(float) * kn);
+    float* ones = (float*)malloc(sizeof(float) * hw);
     double* a64 = (double*)malloc(sizeof(double) * qn);
     float* a = (float*)malloc(sizeof(float) * qn);
     double* branch = (double*)malloc(sizeof(double) * H);
     float* branch32 = (float*)malloc(sizeof(float) * H);
     int rc = OR_ERR;
-    if (!t || !normalized || !q || !k || !v || !a64 || !a || !branch || !branch32) goto done;
-    if (position >= m->capacity) goto done;
+    if (!t || !normalized || !q || !k || !v || !ones || !a64 || !a || !branch || !branch32) goto done;
+    for (uint32_t i = 0; i < hw; ++i) ones[i] = 1.0f;
     if (or_rmsnorm(w->input_norm, H, w->input_eps, x, H, t) != OR_OK) goto done;
     to_f32(t, normalized, H);
-    if (or_q4_matvec(w->q, H, qn, normalized, t, m->threads) != OR_OK) goto done;
+    if (or_q4_matvec(w->q, H, qn, normalized, t, threads) != OR_OK) goto done;
     to_f32(t, q, qn);
-    if (or_q4_matvec(w->k, H, kn, normalized, t, m->threads) != OR_OK) goto done;
+    if (or_q4_matvec(w->k, H, kn, normalized, t, threads) != OR_OK) goto done;
     to_f32(t, k, kn);
-    if (or_q4_matvec(w->v, H, kn, normalized, t, m->threads) != OR_OK) goto done;
+    if (or_q4_matvec(w->v, H, kn, normalized, t, threads) != OR_OK) goto done;
     to_f32(t, v, kn);
     if (or_rmsnorm(w->q_norm, hw, w->q_eps, q, qn, t) != OR_OK) goto done;
     to_f32(t, q, qn);
@@ -598,26 +604,30 @@ static int layer_reference(or_model* m, uint32_t l, const float* x, float* y, ui
     if (or_rope(hw, w->rope_base, w->rope_factors, w->rope_context, k, kn, position, t) != OR_OK) goto done;
     to_f32(t, k, kn);
     if (w->v_norm) {
-        if (or_rmsnorm(m->ones, hw, w->input_eps, v, kn, t) != OR_OK) goto done;
+        if (or_rmsnorm(ones, hw, w->input_eps, v, kn, t) != OR_OK) goto done;
         to_f32(t, v, kn);
     }
+    if (k_new) memcpy(k_new, k, sizeof(float) * kn); /* before the fp16 boundary */
+    if (v_new) memcpy(v_new, v, sizeof(float) * kn);
     if (w->kv_fp16) {
         for (uint32_t i = 0; i < kn; ++i) {
             k[i] = or_f16_round(k[i]);
             v[i] = or_f16_round(v[i]);
         }
     }
-    memcpy(m->keys[l] + (size_t)position * kn, k, sizeof(float) * kn);
-    memcpy(m->values[l] + (size_t)position * kn, v, sizeof(float) * kn);
-    if (or_attention(w->q_heads, w->kv_heads, hw, w->window, w->scale, q, m->keys[l], m->values[l], position + 1,
-                     position, a64) != OR_OK)
+    if (!use_given_kv) {
+        memcpy(keys + (size_t)position * kn, k, sizeof(float) * kn);
+        memcpy(values + (size_t)position * kn, v, sizeof(float) * kn);
+    }
+    if (or_attention(w->q_heads, w->kv_heads, hw, w->window, w->scale, q, keys, values, position + 1, position,
+                     a64) != OR_OK)
         goto done;
     to_f32(a64, a, qn);
-    if (or_attention_output(w->o, qn, H, w->post_attn_norm, w->post_attn_eps, a, x, branch, m->threads) != OR_OK)
+    if (or_attention_output(w->o, qn, H, w->post_attn_norm, w->post_attn_eps, a, x, branch, threads) != OR_OK)
         goto done;
     to_f32(branch, branch32, H);
-    if (or_ffn(w->ffn_norm, w->ffn_eps, w->gate, w->up, w->down, H, m->intermediate, w->post_ffn_norm,
-               w->post_ffn_eps, w->layer_scale, branch32, t, m->threads) != OR_OK)
+    if (or_ffn(w->ffn_norm, w->ffn_eps, w->gate, w->up, w->down, H, intermediate, w->post_ffn_norm,
+               w->post_ffn_eps, w->layer_scale, branch32, t, threads) != OR_OK)
         goto done;
     to_f32(t, y, H);
     rc = OR_OK;
@@ -627,11 +637,18 @@ done:
     free(q);
     free(k);
     free(v);
+    free(ones);
     free(a64);
     free(a);
     free(branch);
     free(branch32);
     return rc;
+}
+
+static int layer_reference(or_model* m, uint32_t l, const float* x, float* y, uint32_t position) {
+    if (position >= m->capacity) return OR_ERR;
+    return or_layer_forward(&m->layer[l], m->hidden, m->intermediate, x, m->keys[l], m->values[l], position, 0, NULL,
+                            NULL, y, m->threads);
 }
 
 int or_model_step(or_model* m, uint32_t token, float* hidden_out, float* per_layer) {

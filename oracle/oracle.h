@@ -83,6 +83,11 @@ typedef struct {
     int kv_fp16;     /* round K and V to fp16 at the cache boundary */
 } or_layer;
 
+/* One layer (stack.rs:670-700) on input x with a caller-owned K/V history; see oracle.c. */
+int or_layer_forward(const or_layer* w, uint32_t hidden, uint32_t intermediate, const float* x, float* keys,
+                     float* values, uint32_t position, int use_given_kv, float* k_new, float* v_new, float* y,
+                     int threads);
+
 typedef struct or_model or_model;
 
 or_model* or_model_new(uint32_t hidden, uint32_t intermediate, uint32_t layers, const or_layer* layer_table,
