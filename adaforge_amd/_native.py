@@ -83,6 +83,10 @@ class GenerationStats(ctypes.Structure):
                 ("has_first_token", i32), ("decode_tokens", u64), ("decode_ms", f64), ("total_ms", f64)]
 
 
+class KernelTiming(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 32), ("launches", u64), ("total_ms", f64), ("bytes_per_launch", f64)]
+
+
 TOKEN_FN = ctypes.CFUNCTYPE(None, P, u32)
 
 # name -> (restype, argtypes): every function include/af.h declares.
@@ -110,6 +114,8 @@ SIGNATURES = {
     "af_generate": (i32, [ctypes.POINTER(LayerDesc), u32, ctypes.POINTER(HeadDesc), u32p, sz, u32p, sz, u32, u32p,
                           ctypes.POINTER(sz), ctypes.POINTER(i32), ctypes.POINTER(GenerationStats)]),
     "af_session_trace": (i32, [P, u32p, sz, f32p, u16p, f32p, f32p]),
+    "af_session_profile": (i32, [P, u32p, sz, u32, u32p, ctypes.POINTER(sz), ctypes.POINTER(KernelTiming), sz,
+                                 ctypes.POINTER(sz)]),
 }
 
 _lib = None

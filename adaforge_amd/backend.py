@@ -180,6 +180,19 @@ class HipGenerationSession:
     def reset(self):
         check(N.lib().af_session_reset(self._h))
 
+    def profile(self, prompt, max_new):
+        """Decode with per-kernel event timing (ADAFORGE_TIMING_DECODE, stack.rs:1245-1251):
+        returns (ids, {kind: (launches, total_ms, bytes_per_launch)})."""
+        pa, pp = _ids(prompt)
+        out = np.zeros(max(int(max_new), 1), np.uint32)
+        n = N.sz()
+        t = (N.KernelTiming * 16)()
+        nt = N.sz()
+        check(N.lib().af_session_profile(self._h, pp, pa.size, int(max_new), out.ctypes.data_as(N.u32p),
+                                         ctypes.byref(n), t, 16, ctypes.byref(nt)))
+        return out[:n.value].tolist(), {t[i].name.decode(): (t[i].launches, t[i].total_ms, t[i].bytes_per_launch)
+                                        for i in range(nt.value)}
+
     def trace(self, ids, kv_rows=None, layer_outputs=True, logits=True, hidden=True):
         """GPU half of check_layer_stack / check_logits (stack.rs:707-817).
 

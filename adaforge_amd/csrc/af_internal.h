@@ -145,6 +145,7 @@ uint32_t head_grid(uint32_t rows);
 
 constexpr uint32_t kAttnMinChunk = 32;
 constexpr uint32_t kAttnMaxChunkLen = 2048;
+constexpr uint32_t kAttnMaxChunks = 64;  // cmax bound: capacity <= 64 * kAttnMaxChunkLen
 constexpr uint32_t kHeadRows = 4;  // rows per wave iteration in the head kernel
 
 }  // namespace af

@@ -598,7 +598,8 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
         if (!std::isfinite(e) || e <= 0.0f) return fail(AF_ERR_INVALID, "epsilon must be finite and positive");
     if ((rc = ensure_device())) return rc;
     const uint32_t group = p->config.q_heads / p->config.kv_heads, D = p->config.width;
-    const uint32_t cmax = std::max<uint32_t>(64, (nvis + kAttnMaxChunkLen - 1) / kAttnMaxChunkLen);
+    if (nvis > kAttnMaxChunks * kAttnMaxChunkLen) return fail(AF_ERR_INVALID, "visible range above 131072 tokens");
+    const uint32_t cmax = kAttnMaxChunks;
     std::lock_guard<std::mutex> lock(g_scratch.mu);
     if ((rc = grow(g_scratch.attn_part, (size_t)p->config.kv_heads * cmax * group * (D + 2) * 4, false, "attention scratch")))
         return rc;
@@ -691,6 +692,34 @@ int validate_layer(const af_layer_weights& w, uint32_t hidden, uint32_t capacity
     return AF_OK;
 }
 
+enum KernelKind { K_QKV = 0, K_ATTN, K_OPROJ, K_GATEUP, K_DOWN, K_HEAD, K_KINDS };
+const char* const kKindNames[K_KINDS] = {"qkv", "attention", "o_proj", "gate_up", "down", "head"};
+
+// Event pairs around individual launches (direct-launch profiling only).
+struct KernelTimer {
+    struct Rec {
+        hipEvent_t a, b;
+        int kind;
+        double bytes;
+    };
+    std::vector<Rec> recs;
+    size_t used = 0;
+    ~KernelTimer() {
+        for (auto& r : recs) {
+            (void)hipEventDestroy(r.a);
+            (void)hipEventDestroy(r.b);
+        }
+    }
+    Rec* next() {
+        if (used == recs.size()) {
+            Rec r{};
+            if (hipEventCreate(&r.a) != hipSuccess || hipEventCreate(&r.b) != hipSuccess) return nullptr;
+            recs.push_back(r);
+        }
+        return &recs[used++];
+    }
+};
+
 }  // namespace
 
 struct af_session {
@@ -713,6 +742,24 @@ struct af_session {
     uint32_t consumed = 0;         // positions with K/V in the caches
     bool poisoned = false;
     bool use_graphs = true;
+    KernelTimer* timer = nullptr;  // set during af_session_profile
+
+    // Launches f(); when profiling, brackets it with an event pair tagged with its kind and bytes.
+    template <typename F>
+    hipError_t timed(int kind, double bytes, F f) {
+        KernelTimer::Rec* r = timer ? timer->next() : nullptr;
+        if (r) {
+            r->kind = kind;
+            r->bytes = bytes;
+            hipError_t e = hipEventRecord(r->a, stream);
+            if (e != hipSuccess) return e;
+        }
+        hipError_t e = f();
+        if (e == hipSuccess && r) e = hipEventRecord(r->b, stream);
+        return e;
+    }
+    static double q4_bytes(const Q4Dev& m) { return (double)m.rows * (m.columns / 32) * 18.0; }
+    uint32_t host_pos = 0;  // position being consumed (profiling: attention bytes)
 
     ~af_session() {
         if (stream) (void)hipStreamSynchronize(stream);
@@ -754,7 +801,8 @@ struct af_session {
             qa.in.scale = P.layer_scale;
             kind = IN_RESID;
         }
-        hipError_t e = launch_q4_gemv(qa, kind, OUT_PLAIN, L.qkv.rows, stream);
+        hipError_t e = timed(K_QKV, q4_bytes(L.qkv) + 4.0 * (3.0 * hidden + L.qkv.rows),
+                             [&] { return launch_q4_gemv(qa, kind, OUT_PLAIN, L.qkv.rows, stream); });
         if (e != hipSuccess) return e;
 
         AttnArgs aa{};
@@ -781,14 +829,20 @@ struct af_session {
         aa.cmax = cmax;
         aa.min_chunk = kAttnMinChunk;
         aa.kv_heads = L.kv_heads;
-        if ((e = launch_attention(aa, L.q_heads / L.kv_heads, L.width, stream)) != hipSuccess) return e;
+        const double nvis = L.window ? std::min<double>(host_pos + 1, L.window) : host_pos + 1.0;
+        const double attn_bytes = nvis * 2.0 * L.kn * 2.0 + 4.0 * (2.0 * L.qn + 2.0 * L.kn) + 4.0 * L.kn;
+        if ((e = timed(K_ATTN, attn_bytes, [&] { return launch_attention(aa, L.q_heads / L.kv_heads, L.width, stream); })) !=
+            hipSuccess)
+            return e;
 
         Q4Args oa{};
         oa.w = L.o.view();
         oa.in.x = ATT.as<float>();
         oa.y = PROJ.as<float>();
         oa.state = st;
-        if ((e = launch_q4_gemv(oa, IN_PLAIN, OUT_PLAIN, L.o.rows, stream)) != hipSuccess) return e;
+        if ((e = timed(K_OPROJ, q4_bytes(L.o) + 4.0 * (L.qn + L.o.rows),
+                       [&] { return launch_q4_gemv(oa, IN_PLAIN, OUT_PLAIN, L.o.rows, stream); })) != hipSuccess)
+            return e;
 
         Q4Args ga{};
         ga.w = L.gate.view();
@@ -803,14 +857,17 @@ struct af_session {
         ga.in.x_out = H.as<float>();
         ga.y = ACT.as<float>();
         ga.state = st;
-        if ((e = launch_q4_gemv(ga, IN_RESID, OUT_GELU, intermediate, stream)) != hipSuccess) return e;
+        if ((e = timed(K_GATEUP, q4_bytes(L.gate) + q4_bytes(L.up) + 4.0 * (3.0 * hidden + intermediate),
+                       [&] { return launch_q4_gemv(ga, IN_RESID, OUT_GELU, intermediate, stream); })) != hipSuccess)
+            return e;
 
         Q4Args da{};
         da.w = L.down.view();
         da.in.x = ACT.as<float>();
         da.y = D.as<float>();
         da.state = st;
-        return launch_q4_gemv(da, IN_PLAIN, OUT_PLAIN, hidden, stream);
+        return timed(K_DOWN, q4_bytes(L.down) + 4.0 * (intermediate + hidden),
+                     [&] { return launch_q4_gemv(da, IN_PLAIN, OUT_PLAIN, hidden, stream); });
     }
 
     HeadArgs head_args(bool step, bool with_logits) {
@@ -843,7 +900,9 @@ struct af_session {
             hipError_t e = enqueue_layer(l, true);
             if (e != hipSuccess) return e;
         }
-        if (with_head) return launch_head(head_args(true, false), IN_RESID, head_blocks, stream);
+        if (with_head)
+            return timed(K_HEAD, (double)head.rows * (head.columns / 256) * 210.0 + 4.0 * 3.0 * hidden,
+                         [&] { return launch_head(head_args(true, false), IN_RESID, head_blocks, stream); });
         return launch_advance(STATE.as<uint32_t>(), stream);
     }
 
@@ -959,7 +1018,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     if ((rc = upload_q6(s->head, hm.bytes, hm.columns, hm.rows))) return rc;
     if ((rc = dev_upload(s->final_norm, head->norm.weights, (size_t)hidden * 4, "final norm"))) return rc;
 
-    s->cmax = std::max<uint32_t>(64, (capacity + kAttnMaxChunkLen - 1) / kAttnMaxChunkLen);
+    s->cmax = kAttnMaxChunks;  // capacity <= AF_MAX_CONTEXT <= kAttnMaxChunks * kAttnMaxChunkLen
     s->head_blocks = head_grid(hm.rows);
     struct {
         DevMem* m;
@@ -1023,17 +1082,23 @@ int af_session_reset(af_session* s) {
     return AF_OK;
 }
 
-int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop,
-                        size_t n_stop, uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out,
-                        size_t* n_out, int32_t* stopped_out, af_generation_stats* stats) {
+}  // extern "C"
+
+namespace {
+
+// GenerationSession::generate (crates/cuda-backend/src/stack.rs:1171-1386).  With a timer the
+// decode steps are launched directly with an event pair around every kernel (no stop ids).
+int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop, size_t n_stop,
+                  uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out, size_t* n_out,
+                  int32_t* stopped_out, af_generation_stats* stats, KernelTimer* timer) {
     if (!s) return fail(AF_ERR_INVALID, "null session");
     if (n_out) *n_out = 0;
     if (stopped_out) *stopped_out = 0;
     if (s->poisoned) return fail(AF_ERR_POISONED, "invalid HIP session; restart the chat");
     // stack.rs:1184-1194
     bool ok = prompt && n_prompt > 0 && max_new >= 1 && max_new <= AF_MAX_NEW_TOKENS &&
-              n_prompt + max_new <= s->capacity && stop && n_stop > 0 && n_stop <= kMaxStopIds && ids_out &&
-              n_prompt >= s->cached.size();
+              n_prompt + max_new <= s->capacity && (timer || (stop && n_stop > 0)) && n_stop <= kMaxStopIds &&
+              ids_out && n_prompt >= s->cached.size();
     for (size_t i = 0; ok && i < n_prompt; ++i) ok = prompt[i] < s->vocabulary;
     for (size_t i = 0; ok && i < n_stop; ++i) ok = stop[i] < s->vocabulary;
     for (size_t i = 0; ok && i < s->cached.size(); ++i) ok = prompt[i] == s->cached[i];
@@ -1047,7 +1112,7 @@ int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, 
     HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, prompt + s->consumed, (size_t)pend * 4,
                           hipMemcpyHostToDevice, st),
            "prompt upload");
-    HIP_OK(hipMemcpyAsync(s->STOPS.p, stop, n_stop * 4, hipMemcpyHostToDevice, st), "stop ids upload");
+    if (n_stop) HIP_OK(hipMemcpyAsync(s->STOPS.p, stop, n_stop * 4, hipMemcpyHostToDevice, st), "stop ids upload");
     std::memset(s->records + P, 0, (size_t)(s->capacity + 2 - P) * sizeof(StepRecord));
     int rc = s->set_state(pend == 0 ? s->consumed - 1 : s->consumed, (uint32_t)n_stop);
     if (rc) return rc;
@@ -1058,14 +1123,23 @@ int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, 
     HIP_OK(hipEventRecord(s->ev_start, st), "event");
     // Enqueue all decode steps; each step's head writes its id and flags to mapped host
     // memory, and a stop id makes the remaining steps return at once.
+    s->timer = timer;
     for (uint32_t k = 0; k < max_new; ++k) {
-        if (k == 0 && pend == 0) {
-            HIP_OK(launch_head(s->head_args(true, false), IN_RESID, s->head_blocks, st), "head launch");
-        } else {
-            HIP_OK(s->run_step(true), "decode step");
+        s->host_pos = P - 1 + k;
+        hipError_t e;
+        if (k == 0 && pend == 0)
+            e = s->timed(K_HEAD, (double)s->head.rows * (s->head.columns / 256) * 210.0 + 12.0 * s->hidden, [&] {
+                return launch_head(s->head_args(true, false), IN_RESID, s->head_blocks, st);
+            });
+        else
+            e = timer ? s->enqueue_step(true) : s->run_step(true);
+        if (e == hipSuccess) e = hipEventRecord(s->events[k], st);
+        if (e != hipSuccess) {
+            s->timer = nullptr;
+            return fail(AF_ERR_DEVICE, std::string("decode step: ") + hipGetErrorString(e));
         }
-        HIP_OK(hipEventRecord(s->events[k], st), "event");
     }
+    s->timer = nullptr;
     std::vector<uint32_t> ids;
     bool stopped = false, bad = false;
     double first_ms = 0, last_ms = 0;
@@ -1112,6 +1186,43 @@ int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, 
         stats->decode_ms = ids.empty() ? 0.0 : last_ms - first_ms;
         stats->total_ms = ms_since(started);
     }
+    return AF_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop,
+                        size_t n_stop, uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out,
+                        size_t* n_out, int32_t* stopped_out, af_generation_stats* stats) {
+    return generate_core(s, prompt, n_prompt, stop, n_stop, max_new, on_token, user, ids_out, n_out, stopped_out,
+                         stats, nullptr);
+}
+
+int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, uint32_t max_new, uint32_t* ids_out,
+                       size_t* n_out, af_kernel_timing* timings, size_t capacity, size_t* n_timings) {
+    if (!timings || !n_timings || capacity < K_KINDS) return fail(AF_ERR_INVALID, "timing output too small");
+    KernelTimer timer;
+    int rc = generate_core(s, prompt, n_prompt, nullptr, 0, max_new, nullptr, nullptr, ids_out, n_out, nullptr,
+                           nullptr, &timer);
+    if (rc) return rc;
+    for (int k = 0; k < K_KINDS; ++k) {
+        std::memset(&timings[k], 0, sizeof(timings[k]));
+        std::snprintf(timings[k].name, sizeof(timings[k].name), "%s", kKindNames[k]);
+    }
+    for (size_t i = 0; i < timer.used; ++i) {
+        const auto& r = timer.recs[i];
+        float ms = 0;
+        HIP_OK(hipEventElapsedTime(&ms, r.a, r.b), "kernel timing");
+        af_kernel_timing& t = timings[r.kind];
+        t.launches += 1;
+        t.total_ms += ms;
+        t.bytes_per_launch += r.bytes;
+    }
+    for (int k = 0; k < K_KINDS; ++k)
+        if (timings[k].launches) timings[k].bytes_per_launch /= (double)timings[k].launches;
+    *n_timings = K_KINDS;
     return AF_OK;
 }
 

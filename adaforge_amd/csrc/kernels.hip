@@ -122,51 +122,103 @@ __device__ void embed_row(const InputStage& in, float* xs, uint32_t K) {
     (void)K;
 }
 
+// Loads N float4 per thread from p at float4 indices base + j * blockDim + thread (zero past n4).
+// All loads are issued before any is used, so one memory latency covers the whole batch.
+template <int N>
+__device__ __forceinline__ void load_f4(const float* __restrict__ p, uint32_t base, uint32_t n4, float4 (&o)[N]) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const uint32_t i = base + j * blockDim.x + threadIdx.x;
+        o[j] = i < n4 ? reinterpret_cast<const float4*>(p)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+__device__ __forceinline__ double sq4(float4 v) {
+    return (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+}
+
+__device__ __forceinline__ float4 norm4(float4 x, double r, float4 w) {
+    return make_float4(norm_apply(x.x, r, w.x), norm_apply(x.y, r, w.y), norm_apply(x.z, r, w.z),
+                       norm_apply(x.w, r, w.w));
+}
+
+__device__ __forceinline__ float4 resid4(float4 t, float4 res, float scale) {
+    return make_float4(__fmul_rn(__fadd_rn(t.x, res.x), scale), __fmul_rn(__fadd_rn(t.y, res.y), scale),
+                       __fmul_rn(__fadd_rn(t.z, res.z), scale), __fmul_rn(__fadd_rn(t.w, res.w), scale));
+}
+
+// Builds the normalised fp32 input vector in LDS (IN_NORM, IN_RESID, IN_EMBED).  K % 4 == 0 and
+// every vector is 16-byte aligned.  Passes cover 4 float4 per thread (4096 floats at 256
+// threads), so for the model widths each loop body runs once with its loads batched.
 template <int IN>
 __device__ void input_stage(const InputStage& in, float* xs, uint32_t K, double* red) {
-    const uint32_t tid = threadIdx.x, nt = blockDim.x;
-    if constexpr (IN == IN_PLAIN) {
-        for (uint32_t i = tid; i < K; i += nt) xs[i] = in.x[i];
-        __syncthreads();
-        return;
-    } else {
-        double ss = 0.0;
-        if constexpr (IN == IN_NORM) {
-            for (uint32_t i = tid; i < K; i += nt) {
-                const float v = in.x[i];
-                xs[i] = v;
-                ss += (double)v * (double)v;
-            }
-        } else if constexpr (IN == IN_RESID) {
-            double ra = 1.0;
-            if (in.w_a) {
-                double sa = 0.0;
-                for (uint32_t i = tid; i < K; i += nt) {
-                    const double v = (double)in.x[i];
-                    sa += v * v;
+    constexpr int PER = 4;
+    const uint32_t tid = threadIdx.x, K4 = K / 4, span = PER * blockDim.x;
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    const bool writer = blockIdx.x == 0 && in.x_out != nullptr;
+    double ss = 0.0;
+    if constexpr (IN == IN_NORM) {
+        for (uint32_t b = 0; b < K4; b += span) {
+            float4 v[PER];
+            load_f4(in.x, b, K4, v);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const uint32_t i = b + j * blockDim.x + tid;
+                if (i < K4) {
+                    xs4[i] = v[j];
+                    ss += sq4(v[j]);
                 }
-                ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
-            }
-            for (uint32_t i = tid; i < K; i += nt) {
-                const float t = in.w_a ? norm_apply(in.x[i], ra, in.w_a[i]) : in.x[i];
-                const float v = __fmul_rn(__fadd_rn(t, in.res[i]), in.scale);
-                xs[i] = v;
-                if (blockIdx.x == 0 && in.x_out) in.x_out[i] = v;
-                ss += (double)v * (double)v;
-            }
-        } else {  // IN_EMBED
-            embed_row(in, xs, K);
-            __syncthreads();
-            for (uint32_t i = tid; i < K; i += nt) {
-                const float v = xs[i];
-                if (blockIdx.x == 0 && in.x_out) in.x_out[i] = v;
-                ss += (double)v * (double)v;
             }
         }
-        const double r = inv_rms(block_sum_d(ss, red), K, in.eps_n);
-        for (uint32_t i = tid; i < K; i += nt) xs[i] = norm_apply(xs[i], r, in.w_n[i]);
+    } else if constexpr (IN == IN_RESID) {
+        double ra = 1.0;
+        if (in.w_a) {
+            double sa = 0.0;
+            for (uint32_t b = 0; b < K4; b += span) {
+                float4 v[PER];
+                load_f4(in.x, b, K4, v);
+#pragma unroll
+                for (int j = 0; j < PER; ++j) sa += sq4(v[j]);
+            }
+            ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
+        }
+        for (uint32_t b = 0; b < K4; b += span) {
+            float4 x[PER], r[PER], w[PER];
+            load_f4(in.x, b, K4, x);
+            load_f4(in.res, b, K4, r);
+            if (in.w_a) load_f4(in.w_a, b, K4, w);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const uint32_t i = b + j * blockDim.x + tid;
+                if (i < K4) {
+                    const float4 t = in.w_a ? norm4(x[j], ra, w[j]) : x[j];
+                    const float4 v = resid4(t, r[j], in.scale);
+                    xs4[i] = v;
+                    ss += sq4(v);
+                    if (writer) reinterpret_cast<float4*>(in.x_out)[i] = v;
+                }
+            }
+        }
+    } else {  // IN_EMBED
+        embed_row(in, xs, K);
         __syncthreads();
+        for (uint32_t i = tid; i < K4; i += blockDim.x) {
+            const float4 v = xs4[i];
+            ss += sq4(v);
+            if (writer) reinterpret_cast<float4*>(in.x_out)[i] = v;
+        }
     }
+    const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
+    for (uint32_t b = 0; b < K4; b += span) {
+        float4 w[PER];
+        load_f4(in.w_n, b, K4, w);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const uint32_t i = b + j * blockDim.x + tid;
+            if (i < K4) xs4[i] = norm4(xs4[i], rn, w[j]);
+        }
+    }
+    __syncthreads();
 }
 
 // ---- Q4_0 GEMV --------------------------------------------------------------------------------
@@ -176,7 +228,10 @@ __device__ void input_stage(const InputStage& in, float* xs, uint32_t K, double*
 // slice for the whole kernel, so its 64 input values stay in registers and
 // each weight row costs it two 16-byte code loads and two scale loads.  A
 // wave-group computes R rows per iteration (R / 2 gate/up pairs for OUT_GELU);
-// lanes reduce over the wave, slices over LDS in slice order.
+// lanes reduce over the wave, slices over LDS in slice order.  The first
+// iteration's weight loads are issued before the input stage, so HBM latency
+// overlaps the prologue; each later iteration's loads are issued before the
+// previous iteration's results are stored.
 //
 // Per 32-weight block: sum (q - 8) x = sum q x - 8 sum x.  Low nibbles are
 // converted directly; high nibbles are converted in place (16 q) against
@@ -200,6 +255,29 @@ __device__ __forceinline__ float q4_block_dot(uint4 c, const float* xl, const fl
     return s0 + s1;
 }
 
+// The 32 inputs of one block: low-nibble weights take x[0..15], high-nibble weights x[16..31] / 16.
+__device__ __forceinline__ void block_inputs(const float* src, bool valid, float* xl, float* xh, float& sum) {
+    const float4* p = reinterpret_cast<const float4*>(src);
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = valid ? p[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float t = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        xl[4 * j + 0] = v[j].x;
+        xl[4 * j + 1] = v[j].y;
+        xl[4 * j + 2] = v[j].z;
+        xl[4 * j + 3] = v[j].w;
+        xh[4 * j + 0] = v[4 + j].x * 0.0625f;
+        xh[4 * j + 1] = v[4 + j].y * 0.0625f;
+        xh[4 * j + 2] = v[4 + j].z * 0.0625f;
+        xh[4 * j + 3] = v[4 + j].w * 0.0625f;
+        t += (v[j].x + v[j].y) + (v[j].z + v[j].w);
+        t += (v[4 + j].x + v[4 + j].y) + (v[4 + j].z + v[4 + j].w);
+    }
+    sum = t;
+}
+
 template <int R, int S, int IN, int OUT>
 __global__ __launch_bounds__(256) void q4_gemv_kernel(Q4Args a, uint32_t out_rows) {
     constexpr int G = S >= 4 ? 1 : 4 / S;
@@ -210,49 +288,45 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(Q4Args a, uint32_t out_row
 
     if (a.state && a.state[ST_STOP]) return;
     const uint32_t B = a.w.blocks, K = B * 32;
-    input_stage<IN>(a.in, xs, K, red);
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int s = wave % S, g = wave / S;
     const uint32_t P = (B + S - 1) / S, sb = s * P, se = min(B, sb + P);
     const uint32_t b0 = sb + lane, b1 = sb + 64 + lane;
     const bool v0 = b0 < se, v1 = b1 < se;
-
-    float xl0[16], xh0[16], xl1[16], xh1[16];
-    float sx0 = 0.0f, sx1 = 0.0f;
-    {
-        const uint32_t i0 = (v0 ? b0 : 0) * 32, i1 = (v1 ? b1 : 0) * 32;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            const float l0 = v0 ? xs[i0 + j] : 0.0f, h0 = v0 ? xs[i0 + 16 + j] : 0.0f;
-            const float l1 = v1 ? xs[i1 + j] : 0.0f, h1 = v1 ? xs[i1 + 16 + j] : 0.0f;
-            xl0[j] = l0;
-            xh0[j] = h0 * 0.0625f;
-            xl1[j] = l1;
-            xh1[j] = h1 * 0.0625f;
-            sx0 += l0 + h0;
-            sx1 += l1 + h1;
-        }
-    }
-    const float bias0 = 8.0f * sx0, bias1 = 8.0f * sx1;
-
     const uint32_t ngroups = (out_rows + RP - 1) / RP;
-    for (uint32_t base = blockIdx.x; base * G < ngroups; base += gridDim.x) {
-        const uint32_t grp = base * G + g;
-        const bool gactive = grp < ngroups;
-        uint4 c0[R], c1[R];
-        uint16_t d0[R], d1[R];
+
+    uint4 c0[R], c1[R];
+    uint16_t d0[R], d1[R];
+    auto load_group = [&](uint32_t grp) {
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             const Q4View& m = (OUT == OUT_GELU && i >= RP) ? a.w2 : a.w;
             const uint32_t row = OUT == OUT_GELU ? grp * RP + (i % RP) : grp * R + i;
-            const bool ok = gactive && row < m.rows;
+            const bool ok = grp < ngroups && row < m.rows;
             const size_t rb = (size_t)row * B;
             c0[i] = (ok && v0) ? *reinterpret_cast<const uint4*>(m.codes + (rb + b0) * 16) : make_uint4(0, 0, 0, 0);
             c1[i] = (ok && v1) ? *reinterpret_cast<const uint4*>(m.codes + (rb + b1) * 16) : make_uint4(0, 0, 0, 0);
             d0[i] = (ok && v0) ? m.scales[rb + b0] : (uint16_t)0;
             d1[i] = (ok && v1) ? m.scales[rb + b1] : (uint16_t)0;
         }
+    };
+    uint32_t base = blockIdx.x;
+    load_group(base * G + g);
+
+    float xl0[16], xh0[16], xl1[16], xh1[16], sx0, sx1;
+    if constexpr (IN == IN_PLAIN) {
+        block_inputs(a.in.x + (size_t)(v0 ? b0 : 0) * 32, v0, xl0, xh0, sx0);
+        block_inputs(a.in.x + (size_t)(v1 ? b1 : 0) * 32, v1, xl1, xh1, sx1);
+    } else {
+        input_stage<IN>(a.in, xs, K, red);
+        block_inputs(xs + (size_t)(v0 ? b0 : 0) * 32, v0, xl0, xh0, sx0);
+        block_inputs(xs + (size_t)(v1 ? b1 : 0) * 32, v1, xl1, xh1, sx1);
+    }
+    const float bias0 = 8.0f * sx0, bias1 = 8.0f * sx1;
+
+    while (base * G < ngroups) {
+        const uint32_t grp = base * G + g;
+        const bool gactive = grp < ngroups;
         float acc[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) {
@@ -260,6 +334,8 @@ __global__ __launch_bounds__(256) void q4_gemv_kernel(Q4Args a, uint32_t out_row
             t = fmaf(h2f(d1[i]), q4_block_dot(c1[i], xl1, xh1) - bias1, t);
             acc[i] = wave_sum(t);
         }
+        base += gridDim.x;
+        if (base * G < ngroups) load_group(base * G + g);
         if constexpr (S > 1) {
             if (lane == 0) {
 #pragma unroll
@@ -305,7 +381,7 @@ static hipError_t q4_launch3(const Q4Args& a, uint32_t out_rows, hipStream_t st)
     const uint32_t ngroups = (out_rows + RP - 1) / RP;
     uint32_t grid = (ngroups + G - 1) / G;
     if (grid > 8192) grid = 8192;
-    const size_t lds = (size_t)a.w.blocks * 32 * sizeof(float);
+    const size_t lds = IN == IN_PLAIN ? 0 : (size_t)a.w.blocks * 32 * sizeof(float);
     hipLaunchKernelGGL((q4_gemv_kernel<R, S, IN, OUT>), dim3(grid), dim3(64 * S * G), lds, st, a, out_rows);
     return hipGetLastError();
 }
@@ -351,6 +427,29 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);
 }
 
+template <int R>
+struct Q6Rows {
+    uint4 a[R], b[R], h[R];
+    uint32_t s[R];
+    uint16_t d[R];
+};
+
+template <int R>
+__device__ __forceinline__ void q6_load(Q6Rows<R>& o, const Q6View& w, uint32_t r0, uint32_t u, bool act) {
+    const uint32_t sblocks = w.units / 4;
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const uint32_t row = r0 + i;
+        const bool ok = act && row < w.rows;
+        const size_t off = ((size_t)row * w.units + u) * 16;
+        o.a[i] = ok ? *reinterpret_cast<const uint4*>(w.a + off) : make_uint4(0, 0, 0, 0);
+        o.b[i] = ok ? *reinterpret_cast<const uint4*>(w.b + off) : make_uint4(0, 0, 0, 0);
+        o.h[i] = ok ? *reinterpret_cast<const uint4*>(w.h + off) : make_uint4(0, 0, 0, 0);
+        o.s[i] = ok ? w.s[(size_t)row * w.units + u] : 0u;
+        o.d[i] = ok ? w.d[(size_t)row * sblocks + (u >> 2)] : (uint16_t)0;
+    }
+}
+
 template <int IN>
 __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
     constexpr int R = kHeadRows;
@@ -361,13 +460,25 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
     __shared__ bool last;
 
     if (a.state && a.state[ST_STOP]) return;
-    const uint32_t units = a.w.units, K = units * 64, sblocks = units / 4;
-    input_stage<IN>(a.in, xs, K, red);
-
+    const uint32_t units = a.w.units, K = units * 64;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const bool act = (uint32_t)lane < units;
     const uint32_t u = act ? (uint32_t)lane : 0;
-    const uint32_t sbk = u >> 2, base = sbk * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16;
+    const uint32_t rows = a.w.rows;
+    const uint32_t stride = gridDim.x * 4 * R;
+    uint32_t r0 = (blockIdx.x * 4 + wave) * R;
+    Q6Rows<R> cur;
+    q6_load(cur, a.w, r0, u, act);  // weights first: their latency overlaps the input stage
+
+    if constexpr (IN == IN_PLAIN) {
+        const float4* src = reinterpret_cast<const float4*>(a.in.x);
+        float4* dst = reinterpret_cast<float4*>(xs);
+        for (uint32_t i = threadIdx.x; i < K / 4; i += blockDim.x) dst[i] = src[i];
+        __syncthreads();
+    } else {
+        input_stage<IN>(a.in, xs, K, red);
+    }
+    const uint32_t base = (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16;
     float x[4][16], bias[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -382,30 +493,17 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
 
     float bv = -INFINITY;
     uint32_t bi = 0xFFFFFFFFu, bad = 0;
-    const uint32_t rows = a.w.rows;
-    const uint32_t stride = gridDim.x * 4 * R;
-    for (uint32_t r0 = (blockIdx.x * 4 + wave) * R; r0 < rows; r0 += stride) {
-        uint4 A[R], Bq[R], H[R];
-        uint32_t S4[R];
-        uint16_t D[R];
-#pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const uint32_t row = r0 + i;
-            const bool ok = act && row < rows;
-            const size_t o = ((size_t)row * units + u) * 16;
-            A[i] = ok ? *reinterpret_cast<const uint4*>(a.w.a + o) : make_uint4(0, 0, 0, 0);
-            Bq[i] = ok ? *reinterpret_cast<const uint4*>(a.w.b + o) : make_uint4(0, 0, 0, 0);
-            H[i] = ok ? *reinterpret_cast<const uint4*>(a.w.h + o) : make_uint4(0, 0, 0, 0);
-            S4[i] = ok ? a.w.s[(size_t)row * units + u] : 0u;
-            D[i] = ok ? a.w.d[(size_t)row * sblocks + sbk] : (uint16_t)0;
-        }
+    while (r0 < rows) {
+        const uint32_t nr = r0 + stride;
+        Q6Rows<R> nxt;
+        q6_load(nxt, a.w, nr, u, act && nr < rows);
         float acc[R];
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-            const uint32_t av[4] = {A[i].x, A[i].y, A[i].z, A[i].w};
-            const uint32_t bw[4] = {Bq[i].x, Bq[i].y, Bq[i].z, Bq[i].w};
-            const uint32_t hv[4] = {H[i].x, H[i].y, H[i].z, H[i].w};
-            const float d = h2f(D[i]);
+            const uint32_t av[4] = {cur.a[i].x, cur.a[i].y, cur.a[i].z, cur.a[i].w};
+            const uint32_t bw[4] = {cur.b[i].x, cur.b[i].y, cur.b[i].z, cur.b[i].w};
+            const uint32_t hv[4] = {cur.h[i].x, cur.h[i].y, cur.h[i].z, cur.h[i].w};
+            const float d = h2f(cur.d[i]);
             float t = 0.0f;
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
@@ -418,7 +516,7 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
                     sq = fmaf((float)((c >> 16) & 0xFFu), x[q][4 * k + 2], sq);
                     sq = fmaf((float)(c >> 24), x[q][4 * k + 3], sq);
                 }
-                const float ds = d * (float)(int8_t)(S4[i] >> (8 * q));
+                const float ds = d * (float)(int8_t)(cur.s[i] >> (8 * q));
                 t = fmaf(ds, sq - bias[q], t);
             }
             acc[i] = wave_sum(t);
@@ -444,6 +542,8 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
                 if (lane == i) v = acc[i];
             if (lane < R && r0 + lane < rows) a.logits[r0 + lane] = v;
         }
+        cur = nxt;
+        r0 = nr;
     }
     if (lane == 0) {
         wv[wave] = bv;
@@ -521,10 +621,11 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
     }
 }
 
+// Persistent grid: at most three workgroups per CU, each wave striding over row groups.
 uint32_t head_grid(uint32_t rows) {
     uint32_t per_block = 4 * kHeadRows;
     uint32_t g = (rows + per_block - 1) / per_block;
-    return g > 2048 ? 2048 : g;
+    return g > 768 ? 768 : g;
 }
 
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s) {
@@ -552,15 +653,17 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
 template <int D, int GQ>
 __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     static_assert(D == 256, "one thread per channel");
+    constexpr int NH = GQ + 2;  // query heads, then the new key and value
+    __shared__ float nrm[NH][D];
     __shared__ float qs[GQ][D];
-    __shared__ float tmp[D];
     __shared__ float scores[GQ][kAttnMaxChunkLen];
     __shared__ float vred[8][GQ][D];
-    __shared__ double red[8];
+    __shared__ double dred[4][NH];
     __shared__ float fred[8];
+    __shared__ float cw[GQ][kAttnMaxChunks];
     __shared__ bool last;
 
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (a.state && a.state[ST_STOP]) return;
     const uint32_t pos = a.state ? a.state[ST_POS] : a.position;
     const uint32_t nvis = a.window ? min(pos + 1, a.window) : pos + 1;
@@ -573,40 +676,53 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
     const uint32_t n = t1 - t0;
     const uint32_t ring = a.ring;
+    const bool append = t1 == pos + 1;  // this chunk holds the new token: append its K and V
+    const int nh = append ? NH : GQ;
 
+    // ---- prologue: RMSNorm of the query heads (and new K, V) with one block reduction, then RoPE
+    float raw[NH];
+#pragma unroll
+    for (int h = 0; h < GQ; ++h) raw[h] = a.q_raw[(size_t)(kvh * GQ + h) * D + tid];
+    raw[GQ] = append ? a.k_raw[(size_t)kvh * D + tid] : 0.0f;
+    raw[GQ + 1] = append ? a.v_raw[(size_t)kvh * D + tid] : 0.0f;
     double sn = 0.0, cs = 1.0;
     if (tid < D / 2) sincos((double)pos * a.inv_freq[tid], &sn, &cs);
-
-    auto norm_rope = [&](const float* src, const float* w, float eps, float* dst) {
-        const float v = src[tid];
-        const double r = inv_rms(block_sum_d((double)v * (double)v, red), D, eps);
-        tmp[tid] = norm_apply(v, r, w[tid]);
-        __syncthreads();
-        if (tid < D / 2) {
-            const double x = (double)tmp[tid], y = (double)tmp[tid + D / 2];
-            dst[tid] = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
-            dst[tid + D / 2] = (float)__dadd_rn(__dmul_rn(x, sn), __dmul_rn(y, cs));
-        }
-        __syncthreads();
-    };
-
 #pragma unroll
-    for (int gi = 0; gi < GQ; ++gi) norm_rope(a.q_raw + (size_t)(kvh * GQ + gi) * D, a.q_norm, a.q_eps, qs[gi]);
-
-    if (t1 == pos + 1) {  // this chunk holds the new token: append K and V
-        norm_rope(a.k_raw + (size_t)kvh * D, a.k_norm, a.k_eps, vred[0][0]);
-        float v = a.v_raw[(size_t)kvh * D + tid];
-        if (a.v_norm) {
-            const double r = inv_rms(block_sum_d((double)v * (double)v, red), D, a.v_eps);
-            v = (float)__dmul_rn((double)v, r);
-        }
-        const size_t slot = ((size_t)kvh * ring + pos % ring) * D + tid;
-        a.kcache[slot] = f2h(vred[0][0][tid]);
-        a.vcache[slot] = f2h(v);
-        __syncthreads();
+    for (int h = 0; h < NH; ++h) {
+        const double v = wave_sum((double)raw[h] * (double)raw[h]);
+        if (lane == 0) dred[wave][h] = v;
     }
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < NH; ++h) {
+        if (h >= nh) break;
+        const double ss = (dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h]);
+        if (h < GQ) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.q_eps), a.q_norm[tid]);
+        else if (h == GQ) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.k_eps), a.k_norm[tid]);
+        else nrm[h][tid] = a.v_norm ? (float)__dmul_rn((double)raw[h], inv_rms(ss, D, a.v_eps)) : raw[h];
+    }
+    __syncthreads();
+    if (tid < D / 2) {
+#pragma unroll
+        for (int h = 0; h < GQ + 1; ++h) {
+            if (h == GQ && !append) break;
+            const double x = (double)nrm[h][tid], y = (double)nrm[h][tid + D / 2];
+            const float r0 = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
+            const float r1 = (float)__dadd_rn(__dmul_rn(x, sn), __dmul_rn(y, cs));
+            if (h < GQ) {
+                qs[h][tid] = r0;
+                qs[h][tid + D / 2] = r1;
+            } else {
+                const size_t slot = ((size_t)kvh * ring + pos % ring) * D;
+                a.kcache[slot + tid] = f2h(r0);
+                a.kcache[slot + tid + D / 2] = f2h(r1);
+            }
+        }
+    }
+    if (append) a.vcache[((size_t)kvh * ring + pos % ring) * D + tid] = f2h(nrm[GQ + 1][tid]);
+    __syncthreads();
 
-    // scores: 16 lanes per token, 16 channels per lane
+    // ---- scores: 16 lanes per token, 16 channels per lane, two tokens in flight per group
     {
         const uint32_t grp = tid >> 4, j = tid & 15;
         float qr[GQ][16];
@@ -614,25 +730,35 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int gi = 0; gi < GQ; ++gi)
 #pragma unroll
             for (int e = 0; e < 16; ++e) qr[gi][e] = qs[gi][16 * j + e];
-        for (uint32_t t = t0 + grp; t < t1; t += 16) {
-            const uint16_t* kp = a.kcache + ((size_t)kvh * ring + t % ring) * D + 16 * j;
-            const uint4 k0 = *reinterpret_cast<const uint4*>(kp);
-            const uint4 k1 = *reinterpret_cast<const uint4*>(kp + 8);
-            const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
-            float kf[16];
+        for (uint32_t tb = t0 + grp; tb < t1; tb += 32) {
+            uint4 k[2][2];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
-                kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t t = tb + 16 * u;
+                const uint16_t* kp = a.kcache + ((size_t)kvh * ring + (t < t1 ? t : tb) % ring) * D + 16 * j;
+                k[u][0] = *reinterpret_cast<const uint4*>(kp);
+                k[u][1] = *reinterpret_cast<const uint4*>(kp + 8);
             }
 #pragma unroll
-            for (int gi = 0; gi < GQ; ++gi) {
-                float d = 0.0f;
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t t = tb + 16 * u;
+                const uint32_t kw[8] = {k[u][0].x, k[u][0].y, k[u][0].z, k[u][0].w,
+                                        k[u][1].x, k[u][1].y, k[u][1].z, k[u][1].w};
+                float kf[16];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
+                for (int e = 0; e < 8; ++e) {
+                    kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
+                    kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
+                }
 #pragma unroll
-                for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
-                if (j == 0) scores[gi][t - t0] = d * a.scale;
+                for (int gi = 0; gi < GQ; ++gi) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
+#pragma unroll
+                    for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+                    if (j == 0 && t < t1) scores[gi][t - t0] = d * a.scale;
+                }
             }
         }
     }
@@ -654,7 +780,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // values: 32 lanes per token row, 8 channels per lane, 8 token groups
+    // ---- values: 32 lanes per token row, 8 channels per lane, 8 token groups, 2 rows in flight
     {
         const uint32_t tg = tid >> 5, dl = tid & 31;
         float acc[GQ][8];
@@ -662,20 +788,31 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int gi = 0; gi < GQ; ++gi)
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[gi][e] = 0.0f;
-        for (uint32_t t = t0 + tg; t < t1; t += 8) {
-            const uint4 vv = *reinterpret_cast<const uint4*>(a.vcache + ((size_t)kvh * ring + t % ring) * D + 8 * dl);
-            const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-            float vf[8];
+        for (uint32_t tb = t0 + tg; tb < t1; tb += 16) {
+            uint4 vv[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
-                vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t t = tb + 8 * u;
+                vv[u] = *reinterpret_cast<const uint4*>(a.vcache + ((size_t)kvh * ring + (t < t1 ? t : tb) % ring) * D +
+                                                        8 * dl);
             }
 #pragma unroll
-            for (int gi = 0; gi < GQ; ++gi) {
-                const float p = scores[gi][t - t0];
+            for (int u = 0; u < 2; ++u) {
+                const uint32_t t = tb + 8 * u;
+                if (t >= t1) break;
+                const uint32_t vw[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+                float vf[8];
 #pragma unroll
-                for (int e = 0; e < 8; ++e) acc[gi][e] = fmaf(p, vf[e], acc[gi][e]);
+                for (int e = 0; e < 4; ++e) {
+                    vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
+                    vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
+                }
+#pragma unroll
+                for (int gi = 0; gi < GQ; ++gi) {
+                    const float p = scores[gi][t - t0];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) acc[gi][e] = fmaf(p, vf[e], acc[gi][e]);
+                }
             }
         }
 #pragma unroll
@@ -697,6 +834,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
         for (int gi = 0; gi < GQ; ++gi) a.out[(size_t)(kvh * GQ + gi) * D + tid] = o[gi] / l[gi];
         return;
     }
+
+    // ---- split-K merge: the last block of this KV head combines the chunk partials
     const size_t stride = (size_t)GQ * (D + 2);
     float* mine = a.part + ((size_t)kvh * a.cmax + c) * stride;
 #pragma unroll
@@ -717,18 +856,33 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     if (!last) return;
     __threadfence();
     const float* all = a.part + (size_t)kvh * a.cmax * stride;
+    // chunk maxima and sums into LDS (one load per thread), then the weights exp(m_c - M)
+    for (uint32_t i = tid; i < chunks * GQ; i += blockDim.x) {
+        const uint32_t k = i / GQ, gi = i % GQ;
+        cw[gi][k] = all[k * stride + gi * (D + 2) + D];
+        vred[0][gi][k] = all[k * stride + gi * (D + 2) + D + 1];
+    }
+    __syncthreads();
+    float M[GQ], L[GQ];
 #pragma unroll
     for (int gi = 0; gi < GQ; ++gi) {
-        float M = -INFINITY;
-        for (uint32_t k = 0; k < chunks; ++k) M = fmaxf(M, all[k * stride + gi * (D + 2) + D]);
-        float L = 0.0f, acc = 0.0f;
-        for (uint32_t k = 0; k < chunks; ++k) {
-            const float* p = all + k * stride + gi * (D + 2);
-            const float w = expf(p[D] - M);
-            L = fmaf(w, p[D + 1], L);
-            acc = fmaf(w, p[tid], acc);
-        }
-        a.out[(size_t)(kvh * GQ + gi) * D + tid] = acc / L;
+        M[gi] = -INFINITY;
+        for (uint32_t k = 0; k < chunks; ++k) M[gi] = fmaxf(M[gi], cw[gi][k]);
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < chunks * GQ; i += blockDim.x) {
+        const uint32_t k = i / GQ, gi = i % GQ;
+        cw[gi][k] = expf(cw[gi][k] - M[gi]);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int gi = 0; gi < GQ; ++gi) {
+        L[gi] = 0.0f;
+        for (uint32_t k = 0; k < chunks; ++k) L[gi] = fmaf(cw[gi][k], vred[0][gi][k], L[gi]);
+        float acc = 0.0f;
+#pragma unroll 8
+        for (uint32_t k = 0; k < chunks; ++k) acc = fmaf(cw[gi][k], all[k * stride + gi * (D + 2) + tid], acc);
+        a.out[(size_t)(kvh * GQ + gi) * D + tid] = acc / L[gi];
     }
     if (tid == 0) a.counters[kvh] = 0u;
 }

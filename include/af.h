@@ -221,6 +221,21 @@ int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, 
 int af_session_reset(af_session* s);
 void af_session_close(af_session* s);
 
+/* Per-kernel decode timing, the event-based ADAFORGE_TIMING_DECODE diagnostic
+ * (crates/cuda-backend/src/stack.rs:1245-1251, 1340-1372) at kernel granularity: behaves as
+ * af_session_generate without stop ids, but launches every step's kernels directly with a
+ * hipEvent pair around each launch on the session stream.  timings[i] aggregates one kernel
+ * kind ("qkv", "attention", "o_proj", "gate_up", "down", "head"); bytes_per_launch is its
+ * algorithmic HBM traffic (weights + activations read and written) averaged over launches. */
+typedef struct {
+    char name[32];
+    uint64_t launches;
+    double total_ms;
+    double bytes_per_launch;
+} af_kernel_timing;
+int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, uint32_t max_new, uint32_t* ids_out,
+                       size_t* n_out, af_kernel_timing* timings, size_t capacity, size_t* n_timings);
+
 /* GpuDiagnostics::generate (crates/application/src/lib.rs:38-47, stack.rs:820-833): a session
  * sized prompt + max_new, one generation, closed. */
 int af_generate(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head,
