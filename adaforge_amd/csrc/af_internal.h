@@ -11,16 +11,20 @@ namespace af {
 
 // ---- device-resident weight layouts ----------------------------------------------------------
 //
-// Q4_0 (GGUF: 18 B per 32 weights) is split at upload into two planes so every
-// lane issues one aligned 16-byte load per block:
-//   codes  [rows][blocks][16]  the block's nibble bytes, unchanged (byte j: low
-//                              nibble = weight j, high nibble = weight j + 16)
-//   scales [rows][blocks]      the block's fp16 d
+// Q4_0 (GGUF: 18 B per 32 weights) is retiled at upload for the matrix-core GEMV.
+// Rows are grouped in tiles of 16 and blocks in super-tiles of 4 (128 columns), both
+// zero-padded; each (row tile rt, super-tile st) owns one contiguous 1 KB code tile
+// and one 128 B scale tile:
+//   codes  [rt][st][16 rows][4 blocks][16]  the block's nibble bytes, unchanged
+//                                           (byte j: low nibble = weight j, high = j + 16)
+//   scales [rt][st][4 blocks][16 rows]      the block's fp16 d
+// so one 16-byte load per lane reads a whole 16 x 128 tile with a wave.
 struct Q4View {
     const uint8_t* codes;
     const uint16_t* scales;
-    uint32_t rows;
-    uint32_t blocks;  // columns / 32
+    uint32_t rows;    // real rows
+    uint32_t blocks;  // real columns / 32
+    uint32_t nst;     // super-tiles per row tile: ceil(blocks / 4)
 };
 
 // Q6_K (GGUF: 210 B per 256 weights) is split into "units" of 64 weights.  Unit
@@ -49,6 +53,15 @@ enum InputKind : int {
     IN_RESID = 2,  // v = (f32(rms(x) * w_a) + res) * scale  [w_a null: (x + res) * scale];
                    // block 0 stores v to x_out; input = f32(rms(v) * w_n)
     IN_EMBED = 3,  // v = Q6_K row ids[state[0]] * emb_scale; block 0 stores v; input = f32(rms(v) * w_n)
+    IN_DIGITS = 4, // the input's int8 digit planes, written by the producing kernel (see DigitTab)
+};
+
+// Exact int8 digit form of an fp32 vector for the matrix-core GEMV: block b of 32 elements
+// is s_b (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21).  dig[((b / 4) * 4 + b % 4) * 4 + t][32] int8
+// holds digit t; tab[b * 4 + t] = {s_b 2^-7t, t == 0 ? 8 sum_j x_j : 0}.
+struct DigitTab {
+    float scale;
+    float bias;
 };
 
 struct InputStage {
@@ -64,6 +77,8 @@ struct InputStage {
     const uint32_t* ids;
     const uint32_t* state;
     float emb_scale;
+    const int8_t* dig;      // IN_DIGITS
+    const DigitTab* tab;
 };
 
 enum OutputKind : int {
@@ -79,6 +94,9 @@ struct Q4Args {
     float* y;
     const float* add;
     const uint32_t* state;  // session state (null for standalone use): exit at once when stopped
+    uint32_t slices;        // waves splitting the super-tiles of a row tile (1, 2, 4 or 8)
+    int8_t* dig_out;        // OUT_GELU: digits of the output for the next GEMV (may be null)
+    DigitTab* tab_out;
 };
 
 // Session state words (device): position to consume next, sticky non-finite flag,
@@ -128,6 +146,8 @@ struct AttnArgs {
     float* out;              // [q_heads][head_width]
     float* part;             // [kv_heads][cmax][group][head_width + 2]
     uint32_t* counters;      // [kv_heads]
+    int8_t* dig_out;         // digits of `out` for the output projection (may be null)
+    DigitTab* tab_out;
     uint32_t cmax;
     uint32_t min_chunk;
     uint32_t kv_heads;

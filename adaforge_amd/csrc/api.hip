@@ -210,26 +210,33 @@ std::vector<double> inverse_frequencies(const af_rope_params& r) {
 struct Q4Dev {
     DevMem codes, scales;
     uint32_t rows = 0, columns = 0;
-    Q4View view() const { return Q4View{codes.as<uint8_t>(), scales.as<uint16_t>(), rows, columns / 32}; }
+    Q4View view() const {
+        const uint32_t B = columns / 32;
+        return Q4View{codes.as<uint8_t>(), scales.as<uint16_t>(), rows, B, (B + 3) / 4};
+    }
 };
 
-// Concatenates the row blocks of several Q4_0 matrices (same columns) into one device matrix.
+// Concatenates the rows of several Q4_0 matrices (same columns) into one device matrix in the
+// tiled layout of Q4View: 16-row tiles x 4-block super-tiles, zero-padded.
 int upload_q4(Q4Dev& d, const std::vector<af_matrix>& parts) {
-    const uint32_t columns = parts[0].columns, B = columns / 32;
+    const uint32_t columns = parts[0].columns, B = columns / 32, nst = (B + 3) / 4;
     uint64_t rows = 0;
     for (auto& p : parts) rows += p.rows;
-    std::vector<uint8_t> codes(rows * B * 16);
-    std::vector<uint16_t> scales(rows * B);
+    const uint64_t tiles = (rows + 15) / 16;
+    std::vector<uint8_t> codes(tiles * nst * 1024, 0);
+    std::vector<uint16_t> scales(tiles * nst * 64, 0);
     uint64_t r0 = 0;
     for (auto& p : parts) {
         const uint8_t* src = p.bytes;
-        uint8_t* cd = codes.data() + r0 * B * 16;
-        uint16_t* sc = scales.data() + r0 * B;
-        parallel_rows((uint64_t)p.rows * B, [&](uint64_t b, uint64_t e) {
-            for (uint64_t i = b; i < e; ++i) {
-                const uint8_t* blk = src + i * 18;
-                sc[i] = (uint16_t)(blk[0] | (blk[1] << 8));
-                std::memcpy(cd + i * 16, blk + 2, 16);
+        parallel_rows(p.rows, [&](uint64_t b, uint64_t e) {
+            for (uint64_t r = b; r < e; ++r) {
+                const uint64_t R = r0 + r, rt = R / 16, rr = R % 16;
+                for (uint32_t k = 0; k < B; ++k) {
+                    const uint8_t* blk = src + (r * B + k) * 18;
+                    const uint64_t tile = rt * nst + k / 4;
+                    std::memcpy(&codes[(tile * 64 + rr * 4 + (k & 3)) * 16], blk + 2, 16);
+                    scales[tile * 64 + (k & 3) * 16 + rr] = (uint16_t)(blk[0] | (blk[1] << 8));
+                }
             }
         });
         r0 += p.rows;
@@ -733,6 +740,7 @@ struct af_session {
     uint32_t max_kv_rows = 0;
     StepRecord* records = nullptr;      // mapped host memory, capacity + 2 entries (host view)
     StepRecord* records_dev = nullptr;  // the same memory as the device addresses it
+    uint32_t* state_host = nullptr;     // pinned staging for state uploads (read by the async copy)
     hipStream_t stream = nullptr;
     hipGraphExec_t decode_exec = nullptr, prefill_exec = nullptr;
     hipGraph_t decode_graph = nullptr, prefill_graph = nullptr;
@@ -770,6 +778,7 @@ struct af_session {
         for (auto e : events) (void)hipEventDestroy(e);
         if (ev_start) (void)hipEventDestroy(ev_start);
         if (records) (void)hipHostFree(records);
+        if (state_host) (void)hipHostFree(state_host);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -922,9 +931,14 @@ struct af_session {
         return enqueue_step(with_head);
     }
 
+    // The staging words are only rewritten after the stream has drained (every caller
+    // synchronises before returning), so the async copy never reads a changed value.
     int set_state(uint32_t pos, uint32_t nstop) {
-        uint32_t st[ST_WORDS] = {pos, 0u, 0u, nstop};
-        HIP_OK(hipMemcpyAsync(STATE.p, st, sizeof(st), hipMemcpyHostToDevice, stream), "state upload");
+        state_host[ST_POS] = pos;
+        state_host[ST_BAD] = 0u;
+        state_host[ST_STOP] = 0u;
+        state_host[ST_NSTOP] = nstop;
+        HIP_OK(hipMemcpyAsync(STATE.p, state_host, ST_WORDS * 4, hipMemcpyHostToDevice, stream), "state upload");
         return AF_OK;
     }
 };
@@ -1050,6 +1064,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
            "step records");
     std::memset(s->records, 0, ((size_t)capacity + 2) * sizeof(StepRecord));
     HIP_OK(hipHostGetDevicePointer((void**)&s->records_dev, s->records, 0), "step records mapping");
+    HIP_OK(hipHostMalloc((void**)&s->state_host, ST_WORDS * 4, hipHostMallocDefault), "state staging");
     s->events.resize(AF_MAX_NEW_TOKENS);
     for (auto& e : s->events) HIP_OK(hipEventCreate(&e), "event");
     HIP_OK(hipEventCreate(&s->ev_start), "event");

@@ -221,191 +221,243 @@ __device__ void input_stage(const InputStage& in, float* xs, uint32_t K, double*
     __syncthreads();
 }
 
-// ---- Q4_0 GEMV --------------------------------------------------------------------------------
+// ---- Q4_0 GEMV on the int8 matrix cores ---------------------------------------------------------
 //
-// A workgroup has S * G waves.  The S waves of a wave-group split the columns
-// into S slices of at most 128 blocks; lane l owns blocks l and l + 64 of its
-// slice for the whole kernel, so its 64 input values stay in registers and
-// each weight row costs it two 16-byte code loads and two scale loads.  A
-// wave-group computes R rows per iteration (R / 2 gate/up pairs for OUT_GELU);
-// lanes reduce over the wave, slices over LDS in slice order.  The first
-// iteration's weight loads are issued before the input stage, so HBM latency
-// overlaps the prologue; each later iteration's loads are issued before the
-// previous iteration's results are stored.
-//
-// Per 32-weight block: sum (q - 8) x = sum q x - 8 sum x.  Low nibbles are
-// converted directly; high nibbles are converted in place (16 q) against
-// x / 16, which is exact.
+// y = W x with W in Q4_0 and x fp32.  Each 32-element block b of x is written exactly as
+//   x_j = s_b (q0_j + q1_j 2^-7 + q2_j 2^-14 + q3_j 2^-21),  s_b = 2^(ilogb(max |x_b|) - 5),
+// with integer digits |q| <= 64 (every step is exact in fp32: scaling by a power of two,
+// rint, and subtracting an integer within 0.5).  Then for row r and block b
+//   sum_j (n_rj - 8) x_j = sum_t 2^-7t s_b sum_j n_rj q_tj  -  8 sum_j x_j,
+// and the integer sums over j come from v_mfma_i32_16x16x64_i8: A = the raw nibbles n of a
+// 16-row tile (lane (r, g) holds block g of row r: low nibbles feed one MFMA, high nibbles a
+// second), B = the digits, with MFMA column n = (block n / 4, digit n % 4), so both MFMAs of
+// a 128-column super-tile accumulate into one 16 x 16 int32 tile.  Lanes then fold the tile
+// into fp32 row partials with the block scales d, reduce over the 16 columns, and the waves
+// that split the super-tiles of a row tile add their partials in LDS in slice order.
 
-__device__ __forceinline__ float q4_block_dot(uint4 c, const float* xl, const float* xh) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-    float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = w[k] & 0x0F0F0F0Fu, hi = w[k] & 0xF0F0F0F0u;
-        s0 = fmaf((float)(lo & 0xFFu), xl[4 * k + 0], s0);
-        s0 = fmaf((float)((lo >> 8) & 0xFFu), xl[4 * k + 1], s0);
-        s0 = fmaf((float)((lo >> 16) & 0xFFu), xl[4 * k + 2], s0);
-        s0 = fmaf((float)(lo >> 24), xl[4 * k + 3], s0);
-        s1 = fmaf((float)(hi & 0xFFu), xh[4 * k + 0], s1);
-        s1 = fmaf((float)((hi >> 8) & 0xFFu), xh[4 * k + 1], s1);
-        s1 = fmaf((float)((hi >> 16) & 0xFFu), xh[4 * k + 2], s1);
-        s1 = fmaf((float)(hi >> 24), xh[4 * k + 3], s1);
-    }
-    return s0 + s1;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+
+// Streaming loads of weights (read once per step): non-temporal hint.
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint2 ld_stream(const uint2* p) {
+    const v2u t = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
+    return make_uint2(t.x, t.y);
 }
 
-// The 32 inputs of one block: low-nibble weights take x[0..15], high-nibble weights x[16..31] / 16.
-__device__ __forceinline__ void block_inputs(const float* src, bool valid, float* xl, float* xh, float& sum) {
-    const float4* p = reinterpret_cast<const float4*>(src);
-    float4 v[8];
+// Digits of 8 consecutive elements v of block b (part p of 4), given the block's max |x| m:
+// 8 bytes per digit t stored at dig[((st * 4 + g) * 4 + t) * 32 + 8 p].
+__device__ __forceinline__ void digits8(const float (&v)[8], float m, int8_t* dig, uint32_t b, uint32_t p) {
+    const int e = m > 0.0f ? ilogbf(m) : 0;
+    uint32_t w[4][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = valid ? p[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-    float t = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        xl[4 * j + 0] = v[j].x;
-        xl[4 * j + 1] = v[j].y;
-        xl[4 * j + 2] = v[j].z;
-        xl[4 * j + 3] = v[j].w;
-        xh[4 * j + 0] = v[4 + j].x * 0.0625f;
-        xh[4 * j + 1] = v[4 + j].y * 0.0625f;
-        xh[4 * j + 2] = v[4 + j].z * 0.0625f;
-        xh[4 * j + 3] = v[4 + j].w * 0.0625f;
-        t += (v[j].x + v[j].y) + (v[j].z + v[j].w);
-        t += (v[4 + j].x + v[4 + j].y) + (v[4 + j].z + v[4 + j].w);
+    for (int k = 0; k < 8; ++k) {
+        const float u = m > 0.0f ? ldexpf(v[k], 5 - e) : 0.0f;  // |u| < 64, exact
+        const float q0 = rintf(u);
+        float r = (u - q0) * 128.0f;
+        const float q1 = rintf(r);
+        r = (r - q1) * 128.0f;
+        const float q2 = rintf(r);
+        r = (r - q2) * 128.0f;
+        const float q3 = rintf(r);
+        const int sh = 8 * (k & 3);
+        w[0][k >> 2] |= ((uint32_t)(int)q0 & 0xFFu) << sh;
+        w[1][k >> 2] |= ((uint32_t)(int)q1 & 0xFFu) << sh;
+        w[2][k >> 2] |= ((uint32_t)(int)q2 & 0xFFu) << sh;
+        w[3][k >> 2] |= ((uint32_t)(int)q3 & 0xFFu) << sh;
     }
-    sum = t;
+    const uint32_t st = b >> 2, g = b & 3;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        *reinterpret_cast<uint2*>(dig + ((size_t)(st * 4 + g) * 4 + t) * 32 + 8 * p) = make_uint2(w[t][0], w[t][1]);
 }
 
-template <int R, int S, int IN, int OUT>
-__global__ __launch_bounds__(256) void q4_gemv_kernel(Q4Args a, uint32_t out_rows) {
-    constexpr int G = S >= 4 ? 1 : 4 / S;
-    constexpr int RP = OUT == OUT_GELU ? R / 2 : R;
-    extern __shared__ float xs[];
+// Block max |x| and sum over the 4 lanes (a quad) that hold a block's 8-element parts.
+__device__ __forceinline__ void quad_stats(const float (&v)[8], float& m, float& sum) {
+    float mm = 0.0f, ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        mm = fmaxf(mm, fabsf(v[k]));
+        ss += v[k];
+    }
+    mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
+    mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    m = mm;
+    sum = ss;
+}
+
+__device__ __forceinline__ void digit_tab(DigitTab* tab, uint32_t b, float m, float sum) {
+    const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) tab[b * 4 + t] = DigitTab{ldexpf(s, -7 * t), t == 0 ? 8.0f * sum : 0.0f};
+}
+
+// Digits of the input vector src (K = 32 B floats, 16-byte aligned; global or LDS) for all
+// nst * 4 blocks (blocks >= B are zero): four threads per block, eight elements each.
+// Layout: dig[(st * 4 + g) * 4 + t][32] int8 for block b = 4 st + g, tab[b * 4 + t].
+__device__ void make_digits(const float* src, uint32_t B, uint32_t nst, int8_t* dig, DigitTab* tab) {
+    const uint32_t nb = nst * 4;
+    for (uint32_t base = 0; base < nb * 4; base += blockDim.x) {
+        const uint32_t i = base + threadIdx.x, b = i >> 2, p = i & 3;
+        float v[8];
+        const bool ok = b < B;
+        const float4* q = reinterpret_cast<const float4*>(src + (size_t)(ok ? b : 0) * 32 + 8 * p);
+        const float4 a0 = ok ? q[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 a1 = ok ? q[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+        float m, sum;
+        quad_stats(v, m, sum);  // every lane of the quad takes part, in range or not
+        if (b < nb) {
+            digits8(v, m, dig, b, p);
+            if (p == 0) digit_tab(tab, b, m, sum);
+        }
+    }
+}
+
+constexpr int kQ4Ahead = 16;  // super-tiles loaded ahead per wave
+
+struct Q4Tile {
+    uint4 code;
+    uint2 scale;
+};
+
+template <int T, int IN, int OUT>
+__global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_rows) {
+    extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[8];
-    __shared__ float part[G][S][R];
+    __shared__ float part[T][8][16];
 
     if (a.state && a.state[ST_STOP]) return;
-    const uint32_t B = a.w.blocks, K = B * 32;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int s = wave % S, g = wave / S;
-    const uint32_t P = (B + S - 1) / S, sb = s * P, se = min(B, sb + P);
-    const uint32_t b0 = sb + lane, b1 = sb + 64 + lane;
-    const bool v0 = b0 < se, v1 = b1 < se;
-    const uint32_t ngroups = (out_rows + RP - 1) / RP;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t S = a.slices, tile = wave / S, sl = wave % S;
+    const Q4View& m = (T == 2 && tile == 1) ? a.w2 : a.w;
+    const uint32_t B = a.w.blocks, K = B * 32, nst = a.w.nst;
+    const uint32_t per = (nst + S - 1) / S, st0 = min(nst, sl * per), st1 = min(nst, st0 + per);
+    const size_t tile_base = (size_t)blockIdx.x * nst;
+    const uint32_t r_ld = lane & 15, g_ld = lane >> 4;  // A operand: row, block in super-tile
+    const uint32_t q = lane >> 4, n = lane & 15;         // D tile: rows 4q..4q+3, column n
+    const uint32_t blk = n >> 2, t = n & 3;
 
-    uint4 c0[R], c1[R];
-    uint16_t d0[R], d1[R];
-    auto load_group = [&](uint32_t grp) {
+    const uint4* codes = reinterpret_cast<const uint4*>(m.codes);
+    const uint2* scales = reinterpret_cast<const uint2*>(m.scales);
+    auto load = [&](Q4Tile (&buf)[kQ4Ahead], uint32_t c0) {
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const Q4View& m = (OUT == OUT_GELU && i >= RP) ? a.w2 : a.w;
-            const uint32_t row = OUT == OUT_GELU ? grp * RP + (i % RP) : grp * R + i;
-            const bool ok = grp < ngroups && row < m.rows;
-            const size_t rb = (size_t)row * B;
-            c0[i] = (ok && v0) ? *reinterpret_cast<const uint4*>(m.codes + (rb + b0) * 16) : make_uint4(0, 0, 0, 0);
-            c1[i] = (ok && v1) ? *reinterpret_cast<const uint4*>(m.codes + (rb + b1) * 16) : make_uint4(0, 0, 0, 0);
-            d0[i] = (ok && v0) ? m.scales[rb + b0] : (uint16_t)0;
-            d1[i] = (ok && v1) ? m.scales[rb + b1] : (uint16_t)0;
+        for (int u = 0; u < kQ4Ahead; ++u) {
+            const uint32_t st = c0 + u;
+            if (st < st1) {
+                buf[u].code = ld_stream(codes + (tile_base + st) * 64 + r_ld * 4 + g_ld);
+                buf[u].scale = ld_stream(scales + (tile_base + st) * 16 + blk * 4 + q);
+            }
         }
     };
-    uint32_t base = blockIdx.x;
-    load_group(base * G + g);
+    Q4Tile buf[kQ4Ahead];
+    load(buf, st0);  // weights first: their latency overlaps the input stage
 
-    float xl0[16], xh0[16], xl1[16], xh1[16], sx0, sx1;
+    const size_t xs_bytes = IN == IN_PLAIN ? 0 : (size_t)K * 4;
+    int8_t* dig = reinterpret_cast<int8_t*>(smem + xs_bytes);
+    DigitTab* tab = reinterpret_cast<DigitTab*>(smem + xs_bytes + (size_t)nst * 512);
     if constexpr (IN == IN_PLAIN) {
-        block_inputs(a.in.x + (size_t)(v0 ? b0 : 0) * 32, v0, xl0, xh0, sx0);
-        block_inputs(a.in.x + (size_t)(v1 ? b1 : 0) * 32, v1, xl1, xh1, sx1);
+        make_digits(a.in.x, B, nst, dig, tab);
     } else {
+        float* xs = reinterpret_cast<float*>(smem);
         input_stage<IN>(a.in, xs, K, red);
-        block_inputs(xs + (size_t)(v0 ? b0 : 0) * 32, v0, xl0, xh0, sx0);
-        block_inputs(xs + (size_t)(v1 ? b1 : 0) * 32, v1, xl1, xh1, sx1);
+        make_digits(xs, B, nst, dig, tab);
     }
-    const float bias0 = 8.0f * sx0, bias1 = 8.0f * sx1;
+    __syncthreads();
 
-    while (base * G < ngroups) {
-        const uint32_t grp = base * G + g;
-        const bool gactive = grp < ngroups;
-        float acc[R];
+    const bool bsel = (n >> 2) == q;  // B lane (k-group q, column n) is non-zero for block q only
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    const v4i zero = {0, 0, 0, 0};
+    for (uint32_t c0 = st0; c0 < st1; c0 += kQ4Ahead) {
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            float t = h2f(d0[i]) * (q4_block_dot(c0[i], xl0, xh0) - bias0);
-            t = fmaf(h2f(d1[i]), q4_block_dot(c1[i], xl1, xh1) - bias1, t);
-            acc[i] = wave_sum(t);
+        for (int u = 0; u < kQ4Ahead; ++u) {
+            const uint32_t st = c0 + u;
+            if (st >= st1) break;
+            const uint4 cw = buf[u].code;
+            const uint2 sw = buf[u].scale;
+            const v4i a1 = {(int)(cw.x & 0x0F0F0F0Fu), (int)(cw.y & 0x0F0F0F0Fu), (int)(cw.z & 0x0F0F0F0Fu),
+                            (int)(cw.w & 0x0F0F0F0Fu)};
+            const v4i a2 = {(int)((cw.x >> 4) & 0x0F0F0F0Fu), (int)((cw.y >> 4) & 0x0F0F0F0Fu),
+                            (int)((cw.z >> 4) & 0x0F0F0F0Fu), (int)((cw.w >> 4) & 0x0F0F0F0Fu)};
+            v4i b1 = zero, b2 = zero;
+            if (bsel) {
+                const uint4* dp = reinterpret_cast<const uint4*>(dig + ((size_t)(st * 4 + q) * 4 + t) * 32);
+                const uint4 lo = dp[0], hi = dp[1];
+                b1 = v4i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w};
+                b2 = v4i{(int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+            }
+            v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, zero, 0, 0, 0);
+            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, b2, d, 0, 0, 0);
+            const DigitTab tb = tab[(st * 4 + blk) * 4 + t];
+            const uint16_t dh[4] = {(uint16_t)(sw.x & 0xFFFFu), (uint16_t)(sw.x >> 16), (uint16_t)(sw.y & 0xFFFFu),
+                                    (uint16_t)(sw.y >> 16)};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] = fmaf(h2f(dh[i]), fmaf((float)d[i], tb.scale, -tb.bias), acc[i]);
         }
-        base += gridDim.x;
-        if (base * G < ngroups) load_group(base * G + g);
-        if constexpr (S > 1) {
-            if (lane == 0) {
+        if (c0 + kQ4Ahead < st1) load(buf, c0 + kQ4Ahead);
+    }
+    // sum the 16 columns of each row, then the slices
 #pragma unroll
-                for (int i = 0; i < R; ++i) part[g][s][i] = acc[i];
-            }
-            __syncthreads();
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int i = 0; i < R; ++i) {
-                float t = part[g][0][i];
+        for (int o = 8; o > 0; o >>= 1) acc[i] += __shfl_xor(acc[i], o, 16);
+    if (n == 0) {
 #pragma unroll
-                for (int q = 1; q < S; ++q) t += part[g][q][i];
-                acc[i] = t;
-            }
-            __syncthreads();
+        for (int i = 0; i < 4; ++i) part[tile][sl][4 * q + i] = acc[i];
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float v[T];
+#pragma unroll
+        for (int k = 0; k < T; ++k) {
+            float s = part[k][0][tid];
+            for (uint32_t j = 1; j < S; ++j) s += part[k][j][tid];
+            v[k] = s;
         }
-        if (s == 0 && gactive) {
-            if constexpr (OUT == OUT_GELU) {
-                float gv = acc[0], uv = acc[RP];
-#pragma unroll
-                for (int i = 1; i < RP; ++i)
-                    if (lane == i) {
-                        gv = acc[i];
-                        uv = acc[RP + i];
-                    }
-                const uint32_t row = grp * RP + lane;
-                if (lane < RP && row < out_rows) a.y[row] = gelu_mul(gv, uv);
-            } else {
-                float v = acc[0];
-#pragma unroll
-                for (int i = 1; i < R; ++i)
-                    if (lane == i) v = acc[i];
-                const uint32_t row = grp * R + lane;
-                if (lane < R && row < out_rows) a.y[row] = OUT == OUT_ADD ? __fadd_rn(v, a.add[row]) : v;
-            }
+        const uint32_t row = blockIdx.x * 16 + tid;
+        if (row < out_rows) {
+            if constexpr (OUT == OUT_GELU) a.y[row] = gelu_mul(v[0], v[T - 1]);
+            else if constexpr (OUT == OUT_ADD) a.y[row] = __fadd_rn(v[0], a.add[row]);
+            else a.y[row] = v[0];
         }
     }
 }
 
-template <int R, int S, int IN, int OUT>
-static hipError_t q4_launch3(const Q4Args& a, uint32_t out_rows, hipStream_t st) {
-    constexpr int G = S >= 4 ? 1 : 4 / S;
-    constexpr int RP = OUT == OUT_GELU ? R / 2 : R;
-    const uint32_t ngroups = (out_rows + RP - 1) / RP;
-    uint32_t grid = (ngroups + G - 1) / G;
-    if (grid > 8192) grid = 8192;
-    const size_t lds = IN == IN_PLAIN ? 0 : (size_t)a.w.blocks * 32 * sizeof(float);
-    hipLaunchKernelGGL((q4_gemv_kernel<R, S, IN, OUT>), dim3(grid), dim3(64 * S * G), lds, st, a, out_rows);
+// Waves per row tile: enough waves to fill the chip (~2048), within the super-tiles and 8 per block.
+static uint32_t q4_slices(uint32_t tiles, uint32_t per_tile, uint32_t nst) {
+    uint32_t s = 1;
+    while (s < 8 && per_tile * s * 2 <= 8 && tiles * per_tile * s < 2048 && s * 2 <= nst) s *= 2;
+    return s;
+}
+
+template <int T, int IN, int OUT>
+static hipError_t q4_launch2(Q4Args a, uint32_t out_rows, hipStream_t st) {
+    const uint32_t tiles = (out_rows + 15) / 16;
+    a.slices = q4_slices(tiles, T, a.w.nst);
+    const size_t lds = (IN == IN_PLAIN ? 0 : (size_t)a.w.blocks * 32 * 4) + (size_t)a.w.nst * (512 + 128);
+    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT>), dim3(tiles), dim3(64 * T * a.slices), lds, st, a, out_rows);
     return hipGetLastError();
-}
-
-template <int IN, int OUT>
-static hipError_t q4_launch2(const Q4Args& a, uint32_t out_rows, hipStream_t st) {
-    const uint32_t B = a.w.blocks;
-    if (B <= 128) return q4_launch3<OUT == OUT_GELU ? 8 : 4, 1, IN, OUT>(a, out_rows, st);
-    if (B <= 256) return q4_launch3<OUT == OUT_GELU ? 8 : 4, 2, IN, OUT>(a, out_rows, st);
-    if (B <= 512) return q4_launch3<OUT == OUT_GELU ? 8 : 4, 4, IN, OUT>(a, out_rows, st);
-    return hipErrorInvalidValue;
 }
 
 template <int IN>
 static hipError_t q4_launch1(const Q4Args& a, int out_kind, uint32_t out_rows, hipStream_t st) {
     switch (out_kind) {
-        case OUT_PLAIN: return q4_launch2<IN, OUT_PLAIN>(a, out_rows, st);
-        case OUT_GELU: return q4_launch2<IN, OUT_GELU>(a, out_rows, st);
-        case OUT_ADD: return q4_launch2<IN, OUT_ADD>(a, out_rows, st);
+        case OUT_PLAIN: return q4_launch2<1, IN, OUT_PLAIN>(a, out_rows, st);
+        case OUT_GELU: return q4_launch2<2, IN, OUT_GELU>(a, out_rows, st);
+        case OUT_ADD: return q4_launch2<1, IN, OUT_ADD>(a, out_rows, st);
         default: return hipErrorInvalidValue;
     }
 }
 
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s) {
+    if (a.w.nst > 128) return hipErrorInvalidValue;  // columns <= 16384
     switch (in_kind) {
         case IN_PLAIN: return q4_launch1<IN_PLAIN>(a, out_kind, out_rows, s);
         case IN_NORM: return q4_launch1<IN_NORM>(a, out_kind, out_rows, s);
