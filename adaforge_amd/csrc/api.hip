@@ -1260,8 +1260,8 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
                      float* logits, float* hidden) {
     if (!s) return fail(AF_ERR_INVALID, "null session");
     if (s->poisoned) return fail(AF_ERR_POISONED, "invalid HIP session; restart the chat");
-    if (!ids || n == 0 || s->cached.size() + n > s->capacity || s->consumed != s->cached.size())
-        return fail(AF_ERR_INVALID, "trace ids exceed the session capacity or follow an unconsumed token");
+    if (!ids || n == 0 || s->cached.size() + n > s->capacity)
+        return fail(AF_ERR_INVALID, "trace ids exceed the session capacity");
     for (size_t i = 0; i < n; ++i)
         if (ids[i] >= s->vocabulary) return fail(AF_ERR_INVALID, "token id outside the vocabulary");
     s->poisoned = true;
@@ -1271,14 +1271,23 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     if (layer_outputs && (rc = grow(s->SNAP, nl * H * 4, false, "trace buffer"))) return rc;
     const size_t kvr = s->max_kv_rows, kv_bytes = nl * 2 * kvr * 2;
     if (kv_appended && (rc = grow(s->KVSNAP, kv_bytes, true, "trace buffer"))) return rc;
-    HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, ids, n * 4, hipMemcpyHostToDevice, st), "ids upload");
+    // Tokens generated but not yet run through the layers go first, unreported.
+    const size_t pend = s->cached.size() - s->consumed;
+    std::vector<uint32_t> run(s->cached.begin() + s->consumed, s->cached.end());
+    run.insert(run.end(), ids, ids + n);
+    HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, run.data(), run.size() * 4, hipMemcpyHostToDevice, st),
+           "ids upload");
     if ((rc = s->set_state(s->consumed, 0))) return rc;
+    for (size_t i = 0; i < pend; ++i) {
+        for (uint32_t l = 0; l < nl; ++l) HIP_OK(s->enqueue_layer(l, true), "trace layer");
+        HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+    }
     for (size_t t = 0; t < n; ++t) {
         for (uint32_t l = 0; l < nl; ++l) {
             HIP_OK(s->enqueue_layer(l, true), "trace layer");
             if (kv_appended) {
                 const LayerDev& L = s->layers[l];
-                const size_t slot = (s->consumed + t) % L.ring, row = (size_t)L.width * 2;
+                const size_t slot = (s->consumed + pend + t) % L.ring, row = (size_t)L.width * 2;
                 uint8_t* dst = s->KVSNAP.as<uint8_t>() + (size_t)l * 2 * kvr * 2;
                 HIP_OK(hipMemcpy2DAsync(dst, row, L.kcache.as<uint8_t>() + slot * row, (size_t)L.ring * row, row,
                                         L.kv_heads, hipMemcpyDeviceToDevice, st),

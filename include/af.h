@@ -249,7 +249,8 @@ int af_generate(const af_layer_weights* layers, uint32_t n_layers, const af_outp
  * (kv_appended: [n][layers][2][kv_rows] fp16 bits, kv_rows = the largest kv_heads * width, may be
  * NULL), the raw logits after the last token (logits: [vocabulary], may be NULL) and the final
  * RMSNorm input after the last token (hidden: [hidden], may be NULL).  The ids join the
- * session's cached tokens. */
+ * session's cached tokens.  A token that a generation emitted last is cached but has not run
+ * through the layers yet; it runs first, unreported. */
 int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_outputs, uint16_t* kv_appended,
                      float* logits, float* hidden);
 
