@@ -53,12 +53,13 @@ enum InputKind : int {
     IN_RESID = 2,  // v = (f32(rms(x) * w_a) + res) * scale  [w_a null: (x + res) * scale];
                    // block 0 stores v to x_out; input = f32(rms(v) * w_n)
     IN_EMBED = 3,  // v = Q6_K row ids[state[0]] * emb_scale; block 0 stores v; input = f32(rms(v) * w_n)
-    IN_DIGITS = 4, // the input's int8 digit planes, written by the producing kernel (see DigitTab)
+    IN_DIGITS = 4, // the input's digit image (below), written by the producing kernel
 };
 
 // Exact int8 digit form of an fp32 vector for the matrix-core GEMV: block b of 32 elements
-// is s_b (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21).  dig[((b / 4) * 4 + b % 4) * 4 + t][32] int8
-// holds digit t; tab[b * 4 + t] = {s_b 2^-7t, t == 0 ? 8 sum_j x_j : 0}.
+// is s_b (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21).  The image of a vector of nst super-tiles
+// (128 elements each) is nst * 640 bytes: dig[b * 4 + t][32] int8 holds digit t of block b
+// (nst * 512 bytes), then tab[b * 4 + t] = {s_b 2^-7t, t == 0 ? 8 sum_j x_j : 0}.
 struct DigitTab {
     float scale;
     float bias;
@@ -77,8 +78,7 @@ struct InputStage {
     const uint32_t* ids;
     const uint32_t* state;
     float emb_scale;
-    const int8_t* dig;      // IN_DIGITS
-    const DigitTab* tab;
+    const int8_t* dig;      // IN_DIGITS: the input's digit image
 };
 
 enum OutputKind : int {
@@ -95,8 +95,7 @@ struct Q4Args {
     const float* add;
     const uint32_t* state;  // session state (null for standalone use): exit at once when stopped
     uint32_t slices;        // waves splitting the super-tiles of a row tile (1, 2, 4 or 8)
-    int8_t* dig_out;        // OUT_GELU: digits of the output for the next GEMV (may be null)
-    DigitTab* tab_out;
+    int8_t* dig_out;        // OUT_GELU: digit image of the output for the next GEMV (may be null)
 };
 
 // Session state words (device): position to consume next, sticky non-finite flag,
@@ -146,8 +145,7 @@ struct AttnArgs {
     float* out;              // [q_heads][head_width]
     float* part;             // [kv_heads][cmax][group][head_width + 2]
     uint32_t* counters;      // [kv_heads]
-    int8_t* dig_out;         // digits of `out` for the output projection (may be null)
-    DigitTab* tab_out;
+    int8_t* dig_out;         // digit image of `out` for the output projection (may be null)
     uint32_t cmax;
     uint32_t min_chunk;
     uint32_t kv_heads;
@@ -167,5 +165,45 @@ constexpr uint32_t kAttnMinChunk = 32;
 constexpr uint32_t kAttnMaxChunkLen = 2048;
 constexpr uint32_t kAttnMaxChunks = 64;  // cmax bound: capacity <= 64 * kAttnMaxChunkLen
 constexpr uint32_t kHeadRows = 4;  // rows per wave iteration in the head kernel
+
+// ---- persistent decode step (step.hip) ----------------------------------------------------------
+
+// One layer as the step kernel reads it (device memory, one entry per layer).
+struct StepLayer {
+    Q4View qkv, o, gate, up, down;  // q, k (, v) rows stacked in qkv
+    const float *input_norm, *q_norm, *k_norm, *post_attn, *ffn_norm, *post_ffn;
+    const double* inv_freq;  // RoPE inverse frequencies (width / 2)
+    uint16_t *kcache, *vcache;  // fp16 [kv_heads][ring][256]
+    float input_eps, q_eps, k_eps, v_eps, post_attn_eps, ffn_eps, post_ffn_eps, layer_scale, scale;
+    uint32_t q_heads, kv_heads, qn, kn, v_off, ring, window, v_norm;
+};
+
+struct StepArgs {
+    const StepLayer* layers;
+    uint32_t n_layers, hidden, inter;
+    Q6View table;  // tied embedding (layer 0 input)
+    float emb_scale;
+    const uint32_t* ids;
+    uint32_t* state;
+    float *X, *H, *QKV, *PROJ, *D;  // activations exchanged inside the launch
+    int8_t *att_img, *act_img;      // digit images of the o-proj and down inputs
+    float* part;                    // attention chunk partials
+    uint32_t* counters;             // attention merge tickets, one per KV head
+    uint32_t* bar;                  // grid barrier words (kStepBarBytes, zero between launches)
+    uint32_t cmax;                  // attention chunk slots (the grid size)
+    uint32_t advance;               // 1: move ST_POS on at the end (a step without the head)
+    float* snap;                    // optional: layer outputs [n_layers][hidden] (the last by the head)
+    uint64_t* clock;                // optional: [2 + 2 * barriers][grid] timestamps (100 MHz): start,
+                                    // then arrival and departure of every barrier, then the end
+};
+
+constexpr uint32_t kStepMaxClen = 2048;   // tokens per attention chunk
+constexpr uint32_t kStepMaxChunks = 256;  // chunks per KV head
+constexpr uint32_t kStepMaxUnits = 2;     // GEMV row units per workgroup (16 rows, 32 for gate/up)
+constexpr size_t kStepBarBytes = 32 * 10 * 4;
+
+size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group);
+hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid);
+hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s);
 
 }  // namespace af

@@ -699,8 +699,8 @@ int validate_layer(const af_layer_weights& w, uint32_t hidden, uint32_t capacity
     return AF_OK;
 }
 
-enum KernelKind { K_QKV = 0, K_ATTN, K_OPROJ, K_GATEUP, K_DOWN, K_HEAD, K_KINDS };
-const char* const kKindNames[K_KINDS] = {"qkv", "attention", "o_proj", "gate_up", "down", "head"};
+enum KernelKind { K_QKV = 0, K_ATTN, K_OPROJ, K_GATEUP, K_DOWN, K_HEAD, K_LAYERS, K_BARRIER, K_KINDS };
+const char* const kKindNames[K_KINDS] = {"qkv", "attention", "o_proj", "gate_up", "down", "head", "layers", "barrier"};
 
 // Event pairs around individual launches (direct-launch profiling only).
 struct KernelTimer {
@@ -737,6 +737,12 @@ struct af_session {
     uint32_t hidden = 0, intermediate = 0, vocabulary = 0, capacity = 0;
     uint32_t max_qkv = 0, max_q = 0, cmax = 0, head_blocks = 0;
     DevMem X, H, QKV, ATT, PROJ, ACT, D, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
+    // persistent step kernel: layer table, digit images, barrier words
+    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK;
+    uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
+    bool use_step = true;     // all layers of a step in one cooperative launch
+    uint32_t step_grid = 0, group = 0;
+    size_t step_lds = 0;
     uint32_t max_kv_rows = 0;
     StepRecord* records = nullptr;      // mapped host memory, capacity + 2 entries (host view)
     StepRecord* records_dev = nullptr;  // the same memory as the device addresses it
@@ -904,7 +910,51 @@ struct af_session {
         return h;
     }
 
+    StepArgs step_args(bool advance, float* snap) {
+        StepArgs a{};
+        a.layers = STEP_LAYERS.as<StepLayer>();
+        a.n_layers = (uint32_t)layers.size();
+        a.hidden = hidden;
+        a.inter = intermediate;
+        a.table = head.view();
+        a.emb_scale = emb_scale;
+        a.ids = IDS.as<uint32_t>();
+        a.state = STATE.as<uint32_t>();
+        a.X = X.as<float>();
+        a.H = H.as<float>();
+        a.QKV = QKV.as<float>();
+        a.PROJ = PROJ.as<float>();
+        a.D = D.as<float>();
+        a.att_img = ATT_IMG.as<int8_t>();
+        a.act_img = ACT_IMG.as<int8_t>();
+        a.part = PART.as<float>();
+        a.counters = COUNTERS.as<uint32_t>();
+        a.bar = BAR.as<uint32_t>();
+        a.cmax = step_grid;
+        a.advance = advance ? 1u : 0u;
+        a.snap = snap;
+        return a;
+    }
+
+    uint32_t barriers() const { return 5 * (uint32_t)layers.size() - 1; }
+    size_t clock_words() const { return (size_t)(2 + 2 * barriers()) * step_grid; }
+
+    double layer_bytes() const {
+        double b = 0;
+        for (const LayerDev& L : layers)
+            b += q4_bytes(L.qkv) + q4_bytes(L.o) + q4_bytes(L.gate) + q4_bytes(L.up) + q4_bytes(L.down);
+        return b;
+    }
+
     hipError_t enqueue_step(bool with_head) {
+        if (use_step) {
+            StepArgs a = step_args(!with_head, nullptr);
+            if (timer && clock_used < clock_steps) a.clock = CLOCK.as<uint64_t>() + (size_t)clock_used++ * clock_words();
+            hipError_t e = timed(K_LAYERS, layer_bytes(), [&] { return launch_step(a, group, step_grid, step_lds, stream); });
+            if (e != hipSuccess || !with_head) return e;
+            return timed(K_HEAD, (double)head.rows * (head.columns / 256) * 210.0 + 4.0 * 3.0 * hidden,
+                         [&] { return launch_head(head_args(true, false), IN_RESID, head_blocks, stream); });
+        }
         for (uint32_t l = 0; l < layers.size(); ++l) {
             hipError_t e = enqueue_layer(l, true);
             if (e != hipSuccess) return e;
@@ -927,7 +977,7 @@ struct af_session {
     }
 
     hipError_t run_step(bool with_head) {
-        if (use_graphs) return hipGraphLaunch(with_head ? decode_exec : prefill_exec, stream);
+        if (use_graphs && !use_step) return hipGraphLaunch(with_head ? decode_exec : prefill_exec, stream);
         return enqueue_step(with_head);
     }
 
@@ -944,6 +994,84 @@ struct af_session {
 };
 
 namespace {
+
+// Prepares the persistent step kernel: one launch of one workgroup per CU runs every layer.  A
+// model outside its limits (GEMV rows beyond two units per workgroup, attention chunks beyond
+// its LDS, mixed query groups) keeps the per-operation kernels in a graph instead.
+int setup_step(af_session& s) {
+    if (!s.use_step) return AF_OK;
+    const LayerDev& L0 = s.layers[0];
+    const uint32_t group = L0.q_heads / L0.kv_heads;
+    const size_t lds = step_lds_bytes(s.hidden, s.intermediate, s.max_q, group);
+    uint32_t grid = 0;
+    HIP_OK(step_max_grid(group, lds, &grid), "step kernel occupancy");
+    bool fits = grid >= 8 && s.hidden <= 4096 && s.hidden % 32 == 0;
+    for (const LayerDev& L : s.layers) {
+        const uint32_t cm = grid / std::max<uint32_t>(L.kv_heads, 1);
+        const uint32_t span = L.window ? std::min(L.window, s.capacity) : s.capacity;
+        fits = fits && L.q_heads / L.kv_heads == group && L.width == 256 && cm >= 1 && cm <= kStepMaxChunks &&
+               (span + cm - 1) / cm <= kStepMaxClen && (L.qkv.rows + 15) / 16 <= kStepMaxUnits * grid &&
+               (L.o.rows + 15) / 16 <= kStepMaxUnits * grid && (s.intermediate + 31) / 32 <= kStepMaxUnits * grid &&
+               (L.down.rows + 15) / 16 <= kStepMaxUnits * grid && L.o.columns == s.max_q;
+    }
+    if (!fits) {
+        s.use_step = false;
+        return AF_OK;
+    }
+    s.step_grid = grid;
+    s.group = group;
+    s.step_lds = lds;
+    std::vector<StepLayer> table(s.layers.size());
+    for (size_t i = 0; i < s.layers.size(); ++i) {
+        const LayerDev& L = s.layers[i];
+        StepLayer& t = table[i];
+        t.qkv = L.qkv.view();
+        t.o = L.o.view();
+        t.gate = L.gate.view();
+        t.up = L.up.view();
+        t.down = L.down.view();
+        t.input_norm = L.input_norm.as<float>();
+        t.q_norm = L.q_norm.as<float>();
+        t.k_norm = L.k_norm.as<float>();
+        t.post_attn = L.post_attn.as<float>();
+        t.ffn_norm = L.ffn_norm.as<float>();
+        t.post_ffn = L.post_ffn.as<float>();
+        t.inv_freq = L.inv_freq.as<double>();
+        t.kcache = L.kcache.as<uint16_t>();
+        t.vcache = L.vcache.as<uint16_t>();
+        t.input_eps = L.input_eps;
+        t.q_eps = L.q_eps;
+        t.k_eps = L.k_eps;
+        t.v_eps = L.input_eps;
+        t.post_attn_eps = L.post_attn_eps;
+        t.ffn_eps = L.ffn_eps;
+        t.post_ffn_eps = L.post_ffn_eps;
+        t.layer_scale = L.layer_scale;
+        t.scale = L.scale;
+        t.q_heads = L.q_heads;
+        t.kv_heads = L.kv_heads;
+        t.qn = L.qn;
+        t.kn = L.kn;
+        t.v_off = L.shared_v ? L.qn : L.qn + L.kn;
+        t.ring = L.ring;
+        t.window = L.window;
+        t.v_norm = L.v_norm ? 1u : 0u;
+    }
+    int rc;
+    if ((rc = dev_upload(s.STEP_LAYERS, table.data(), table.size() * sizeof(StepLayer), "layer table"))) return rc;
+    const size_t att_img = (size_t)((s.max_q / 32 + 3) / 4) * 640, act_img = (size_t)((s.intermediate / 32 + 3) / 4) * 640;
+    if ((rc = dev_alloc(s.ATT_IMG, att_img, "digit image"))) return rc;
+    if ((rc = dev_alloc(s.ACT_IMG, act_img, "digit image"))) return rc;
+    if ((rc = dev_alloc(s.BAR, kStepBarBytes, "barrier words"))) return rc;
+    HIP_OK(hipMemset(s.ATT_IMG.p, 0, att_img), "digit image clear");
+    HIP_OK(hipMemset(s.ACT_IMG.p, 0, act_img), "digit image clear");
+    HIP_OK(hipMemset(s.BAR.p, 0, kStepBarBytes), "barrier clear");
+    const size_t part = (size_t)grid * group * (256 + 2) * 4;
+    if (s.PART.bytes < part) {
+        if ((rc = dev_alloc(s.PART, part, "attention partials"))) return rc;
+    }
+    return AF_OK;
+}
 
 int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head, uint32_t capacity,
                  af_session** out) {
@@ -976,6 +1104,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     s->emb_scale = std::sqrt((float)hidden);  // EmbeddingBatch::scale (crates/domain/src/embedding.rs:49-51)
     const char* env = std::getenv("AF_DISABLE_GRAPHS");
     s->use_graphs = !(env && *env && std::strcmp(env, "0") != 0);
+    const char* step_env = std::getenv("AF_STEP_KERNEL");
+    s->use_step = !(step_env && std::strcmp(step_env, "0") == 0);
     HIP_OK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "session stream");
 
     uint32_t max_kv = 0, max_q = 0, max_group = 1;
@@ -1068,8 +1198,9 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     s->events.resize(AF_MAX_NEW_TOKENS);
     for (auto& e : s->events) HIP_OK(hipEventCreate(&e), "event");
     HIP_OK(hipEventCreate(&s->ev_start), "event");
+    if ((rc = setup_step(*s))) return rc;
     HIP_OK(hipDeviceSynchronize(), "session upload");
-    if (s->use_graphs) {
+    if (s->use_graphs && !s->use_step) {
         if ((rc = s->capture(true, s->decode_graph, s->decode_exec))) return rc;
         if ((rc = s->capture(false, s->prefill_graph, s->prefill_exec))) return rc;
     }
@@ -1182,7 +1313,12 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
         if (on_token) on_token(user, r.id);
     }
     HIP_OK(hipStreamSynchronize(st), "generation");
-    if (bad) return fail(AF_ERR_NONFINITE, "non-finite logits or invalid greedy id");
+    if (bad) {
+        uint32_t words[ST_WORDS] = {};
+        HIP_OK(hipMemcpy(words, s->STATE.p, sizeof(words), hipMemcpyDeviceToHost), "state download");
+        if (words[ST_BAD] == 2u) return fail(AF_ERR_DEVICE, "decode step grid barrier did not complete");
+        return fail(AF_ERR_NONFINITE, "non-finite logits or invalid greedy id");
+    }
     for (size_t i = 0; i < ids.size(); ++i) ids_out[i] = ids[i];
     s->cached.assign(prompt, prompt + n_prompt);
     s->cached.insert(s->cached.end(), ids.begin(), ids.end());
@@ -1219,8 +1355,19 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
                        size_t* n_out, af_kernel_timing* timings, size_t capacity, size_t* n_timings) {
     if (!timings || !n_timings || capacity < K_KINDS) return fail(AF_ERR_INVALID, "timing output too small");
     KernelTimer timer;
+    if (s && s->use_step && !s->poisoned) {
+        const size_t bytes = (size_t)max_new * s->clock_words() * 8;
+        if (s->CLOCK.bytes < bytes) {
+            int r = dev_alloc(s->CLOCK, bytes, "step timeline");
+            if (r) return r;
+        }
+        s->clock_steps = max_new;
+        s->clock_used = 0;
+    }
     int rc = generate_core(s, prompt, n_prompt, nullptr, 0, max_new, nullptr, nullptr, ids_out, n_out, nullptr,
                            nullptr, &timer);
+    const uint32_t timed_steps = s ? s->clock_used : 0;
+    if (s) s->clock_steps = 0;
     if (rc) return rc;
     for (int k = 0; k < K_KINDS; ++k) {
         std::memset(&timings[k], 0, sizeof(timings[k]));
@@ -1234,6 +1381,45 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
         t.launches += 1;
         t.total_ms += ms;
         t.bytes_per_launch += r.bytes;
+    }
+    // Step kernel timelines: a phase runs from its opening barrier's departure (workgroup 0) to
+    // the last workgroup's arrival at the closing barrier; the barrier itself from that arrival
+    // to workgroup 0's departure.
+    if (timed_steps) {
+        const size_t words = s->clock_words();
+        std::vector<uint64_t> clk((size_t)timed_steps * words);
+        HIP_OK(hipMemcpy(clk.data(), s->CLOCK.p, clk.size() * 8, hipMemcpyDeviceToHost), "timeline download");
+        const uint32_t G = s->step_grid, nb = s->barriers();
+        const double tick_ms = 1e-5;  // 100 MHz
+        for (uint32_t st = 0; st < timed_steps; ++st) {
+            const uint64_t* c = clk.data() + (size_t)st * words;
+            auto ev = [&](uint32_t e, uint32_t b) { return c[(size_t)e * G + b]; };
+            auto max_arrive = [&](uint32_t e) {
+                uint64_t m = 0;
+                for (uint32_t b = 0; b < G; ++b) m = std::max(m, ev(e, b));
+                return m;
+            };
+            uint64_t open = ev(0, 0);
+            for (uint32_t k = 0; k <= nb; ++k) {
+                const uint64_t arrive = max_arrive(1 + 2 * k);
+                const int kind = K_QKV + (int)(k % 5);
+                af_kernel_timing& t = timings[kind];
+                t.launches += 1;
+                t.total_ms += (double)(arrive - std::min(arrive, open)) * tick_ms;
+                if (k < nb) {
+                    const uint64_t depart = ev(2 + 2 * k, 0);
+                    timings[K_BARRIER].launches += 1;
+                    timings[K_BARRIER].total_ms += (double)(depart - std::min(depart, arrive)) * tick_ms;
+                    open = depart;
+                }
+            }
+        }
+        const LayerDev& L0 = s->layers[0];
+        timings[K_QKV].bytes_per_launch += af_session::q4_bytes(L0.qkv) * timings[K_QKV].launches;
+        timings[K_OPROJ].bytes_per_launch += af_session::q4_bytes(L0.o) * timings[K_OPROJ].launches;
+        timings[K_GATEUP].bytes_per_launch +=
+            (af_session::q4_bytes(L0.gate) + af_session::q4_bytes(L0.up)) * timings[K_GATEUP].launches;
+        timings[K_DOWN].bytes_per_launch += af_session::q4_bytes(L0.down) * timings[K_DOWN].launches;
     }
     for (int k = 0; k < K_KINDS; ++k)
         if (timings[k].launches) timings[k].bytes_per_launch /= (double)timings[k].launches;
@@ -1278,32 +1464,49 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, run.data(), run.size() * 4, hipMemcpyHostToDevice, st),
            "ids upload");
     if ((rc = s->set_state(s->consumed, 0))) return rc;
+    const bool step = s->use_step;
     for (size_t i = 0; i < pend; ++i) {
-        for (uint32_t l = 0; l < nl; ++l) HIP_OK(s->enqueue_layer(l, true), "trace layer");
-        HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+        if (step) {
+            HIP_OK(launch_step(s->step_args(true, nullptr), s->group, s->step_grid, s->step_lds, st), "trace step");
+        } else {
+            for (uint32_t l = 0; l < nl; ++l) HIP_OK(s->enqueue_layer(l, true), "trace layer");
+            HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+        }
     }
+    // layer l's output: (rms(D) post_ffn + H) * scale after layer l
+    auto snapshot = [&](uint32_t l) -> hipError_t {
+        InputStage r{};
+        r.x = s->D.as<float>();
+        r.res = s->H.as<float>();
+        r.w_a = s->layers[l].post_ffn.as<float>();
+        r.eps_a = s->layers[l].post_ffn_eps;
+        r.scale = s->layers[l].layer_scale;
+        return launch_resid(r, s->hidden, s->SNAP.as<float>() + l * H, st);
+    };
+    auto kv_copy = [&](uint32_t l, size_t t) -> hipError_t {
+        const LayerDev& L = s->layers[l];
+        const size_t slot = (s->consumed + pend + t) % L.ring, row = (size_t)L.width * 2;
+        uint8_t* dst = s->KVSNAP.as<uint8_t>() + (size_t)l * 2 * kvr * 2;
+        hipError_t e = hipMemcpy2DAsync(dst, row, L.kcache.as<uint8_t>() + slot * row, (size_t)L.ring * row, row,
+                                        L.kv_heads, hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return e;
+        return hipMemcpy2DAsync(dst + kvr * 2, row, L.vcache.as<uint8_t>() + slot * row, (size_t)L.ring * row, row,
+                                L.kv_heads, hipMemcpyDeviceToDevice, st);
+    };
     for (size_t t = 0; t < n; ++t) {
-        for (uint32_t l = 0; l < nl; ++l) {
-            HIP_OK(s->enqueue_layer(l, true), "trace layer");
-            if (kv_appended) {
-                const LayerDev& L = s->layers[l];
-                const size_t slot = (s->consumed + pend + t) % L.ring, row = (size_t)L.width * 2;
-                uint8_t* dst = s->KVSNAP.as<uint8_t>() + (size_t)l * 2 * kvr * 2;
-                HIP_OK(hipMemcpy2DAsync(dst, row, L.kcache.as<uint8_t>() + slot * row, (size_t)L.ring * row, row,
-                                        L.kv_heads, hipMemcpyDeviceToDevice, st),
-                       "trace K copy");
-                HIP_OK(hipMemcpy2DAsync(dst + kvr * 2, row, L.vcache.as<uint8_t>() + slot * row, (size_t)L.ring * row,
-                                        row, L.kv_heads, hipMemcpyDeviceToDevice, st),
-                       "trace V copy");
-            }
-            if (layer_outputs) {
-                InputStage r{};
-                r.x = s->D.as<float>();
-                r.res = s->H.as<float>();
-                r.w_a = s->layers[l].post_ffn.as<float>();
-                r.eps_a = s->layers[l].post_ffn_eps;
-                r.scale = s->layers[l].layer_scale;
-                HIP_OK(launch_resid(r, s->hidden, s->SNAP.as<float>() + l * H, st), "trace snapshot");
+        if (step) {
+            // the step kernel writes layers 0..L-2's outputs; the last comes from D and H after it
+            HIP_OK(launch_step(s->step_args(true, layer_outputs ? s->SNAP.as<float>() : nullptr), s->group,
+                               s->step_grid, s->step_lds, st),
+                   "trace step");
+            if (layer_outputs) HIP_OK(snapshot(nl - 1), "trace snapshot");
+            if (kv_appended)
+                for (uint32_t l = 0; l < nl; ++l) HIP_OK(kv_copy(l, t), "trace K/V copy");
+        } else {
+            for (uint32_t l = 0; l < nl; ++l) {
+                HIP_OK(s->enqueue_layer(l, true), "trace layer");
+                if (kv_appended) HIP_OK(kv_copy(l, t), "trace K/V copy");
+                if (layer_outputs) HIP_OK(snapshot(l), "trace snapshot");
             }
         }
         if (layer_outputs)
@@ -1312,12 +1515,12 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
         if (kv_appended)
             HIP_OK(hipMemcpyAsync(kv_appended + t * nl * 2 * kvr, s->KVSNAP.p, kv_bytes, hipMemcpyDeviceToHost, st),
                    "trace download");
-        if (t + 1 < n) HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+        if (!step && t + 1 < n) HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
     }
-    // head on the last token: raw logits, no state change; then advance past it
+    // head on the last token: raw logits, no state change (the step kernel already advanced)
     HeadArgs h = s->head_args(false, true);
     HIP_OK(launch_head(h, IN_RESID, s->head_blocks, st), "trace head");
-    HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
+    if (!step) HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
     if (logits) HIP_OK(hipMemcpyAsync(logits, s->LOGITS.p, (size_t)s->vocabulary * 4, hipMemcpyDeviceToHost, st), "logits");
     if (hidden) HIP_OK(hipMemcpyAsync(hidden, s->X.p, H * 4, hipMemcpyDeviceToHost, st), "hidden");
     HIP_OK(hipStreamSynchronize(st), "trace");

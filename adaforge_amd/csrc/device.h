@@ -1,0 +1,530 @@
+// Device helpers shared by the per-operation kernels and the persistent decode-step kernel
+// (gfx950): half conversions, wave/block reductions, the reference's fp64 rounding points,
+// Q6_K code unpacking, and the Q4_0 GEMV input prologue (exact int8 digit planes in LDS).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <math.h>
+
+#include "af_internal.h"
+
+namespace af {
+
+// ---- helpers ----------------------------------------------------------------------------------
+
+// Global-address-space views of generic pointers: loads and stores through them are global
+// (vector memory counter only) instead of flat (which also counts against the LDS counter).
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(1))) T* gp(const T* p) {
+    return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T* gp(T* p) {
+    return (__attribute__((address_space(1))) T*)p;
+}
+
+// The wave's index in its workgroup, known to the compiler as wave-uniform (an SGPR), so that
+// control flow derived from it stays scalar.
+__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Sum over the block of one double per thread (blockDim a multiple of 64, <= 512).
+__device__ inline double block_sum_d(double v, double* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    double t = 0.0;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    return t;
+}
+
+__device__ inline float block_sum_f(float v, float* red) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    return t;
+}
+
+__device__ inline float block_max_f(float v, float* red) {
+    v = wave_max(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = red[0];
+    for (int w = 1; w < nw; ++w) t = fmaxf(t, red[w]);
+    return t;
+}
+
+// f32(x * r * w) with the products in double, as the FP64 RMSNorm oracle rounds its output.
+__device__ __forceinline__ float norm_apply(float x, double r, float w) {
+    return (float)__dmul_rn(__dmul_rn((double)x, r), (double)w);
+}
+
+__device__ __forceinline__ double inv_rms(double sumsq, uint32_t n, float eps) {
+    return 1.0 / sqrt(__dadd_rn(sumsq / (double)n, (double)eps));
+}
+
+// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in double, rounded to f32, times up in f32.
+__device__ __forceinline__ float gelu_mul(float g, float u) {
+    const double x = (double)g;
+    const double c = sqrt(2.0 / 3.14159265358979323846);
+    const double inner = __dadd_rn(x, __dmul_rn(__dmul_rn(__dmul_rn(0.044715, x), x), x));
+    const double t = tanh(__dmul_rn(c, inner));
+    const float gl = (float)__dmul_rn(__dmul_rn(0.5, x), __dadd_rn(1.0, t));
+    return __fmul_rn(gl, u);
+}
+
+// One 64-weight Q6_K unit's code bytes for quarter q from its ql/ql/qh dwords.
+__device__ __forceinline__ uint32_t q6_codes(uint32_t a, uint32_t b, uint32_t h, int q) {
+    switch (q) {
+        case 0: return (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+        case 1: return (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+        case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+        default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+    }
+}
+
+// ---- input stage: builds the fp32 GEMV input vector in LDS ------------------------------------
+
+// Embedding row (Q6_K, repacked) times emb_scale into xs; one thread per unit dword (16 elements).
+__device__ inline void embed_row(const InputStage& in, float* xs, uint32_t K) {
+    const Q6View& t = in.table;
+    const uint32_t row = min(gp(in.ids)[gp(in.state)[ST_POS]], t.rows - 1);  // ids are validated; never read past the table
+    const uint32_t units = t.units, sblocks = units / 4;
+    const auto* A = gp(reinterpret_cast<const uint32_t*>(t.a + (size_t)row * units * 16));
+    const auto* B = gp(reinterpret_cast<const uint32_t*>(t.b + (size_t)row * units * 16));
+    const auto* H = gp(reinterpret_cast<const uint32_t*>(t.h + (size_t)row * units * 16));
+    for (uint32_t w = threadIdx.x; w < units * 4; w += blockDim.x) {
+        const uint32_t u = w >> 2, k = w & 3;
+        const uint32_t sb = u >> 2, g = (u >> 1) & 1, hh = u & 1;
+        const uint32_t a = A[w], b = B[w], h = H[w];
+        const uint32_t sc = gp(t.s)[(size_t)row * units + u];
+        const float d = h2f(gp(t.d)[(size_t)row * sblocks + sb]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t c = q6_codes(a, b, h, q);
+            const float ds = __fmul_rn(d, (float)(int8_t)(sc >> (8 * q)));
+#pragma unroll
+            for (int n = 0; n < 4; ++n) {
+                const int code = (int)((c >> (8 * n)) & 0xFF) - 32;
+                const uint32_t e = sb * 256 + g * 128 + q * 32 + hh * 16 + 4 * k + n;
+                xs[e] = __fmul_rn(__fmul_rn(ds, (float)code), in.emb_scale);
+            }
+        }
+    }
+    (void)K;
+}
+
+// Loads N float4 per thread from p at float4 indices base + j * blockDim + thread (zero past n4).
+// All loads are issued before any is used, so one memory latency covers the whole batch.
+template <int N>
+__device__ __forceinline__ void load_f4(const float* __restrict__ p, uint32_t base, uint32_t n4, float4 (&o)[N]) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+        const uint32_t i = base + j * blockDim.x + threadIdx.x;
+        o[j] = i < n4 ? reinterpret_cast<const float4*>(p)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+}
+
+__device__ __forceinline__ double sq4(float4 v) {
+    return (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
+}
+
+__device__ __forceinline__ float4 norm4(float4 x, double r, float4 w) {
+    return make_float4(norm_apply(x.x, r, w.x), norm_apply(x.y, r, w.y), norm_apply(x.z, r, w.z),
+                       norm_apply(x.w, r, w.w));
+}
+
+__device__ __forceinline__ float4 resid4(float4 t, float4 res, float scale) {
+    return make_float4(__fmul_rn(__fadd_rn(t.x, res.x), scale), __fmul_rn(__fadd_rn(t.y, res.y), scale),
+                       __fmul_rn(__fadd_rn(t.z, res.z), scale), __fmul_rn(__fadd_rn(t.w, res.w), scale));
+}
+
+// Builds the normalised fp32 input vector in LDS (IN_NORM, IN_RESID, IN_EMBED).  K % 4 == 0 and
+// every vector is 16-byte aligned.  Passes cover 4 float4 per thread (4096 floats at 256
+// threads), so for the model widths each loop body runs once with its loads batched.
+template <int IN>
+__device__ inline void input_stage(const InputStage& in, float* xs, uint32_t K, double* red) {
+    constexpr int PER = 4;
+    const uint32_t tid = threadIdx.x, K4 = K / 4, span = PER * blockDim.x;
+    float4* xs4 = reinterpret_cast<float4*>(xs);
+    const bool writer = blockIdx.x == 0 && in.x_out != nullptr;
+    double ss = 0.0;
+    if constexpr (IN == IN_NORM) {
+        for (uint32_t b = 0; b < K4; b += span) {
+            float4 v[PER];
+            load_f4(in.x, b, K4, v);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const uint32_t i = b + j * blockDim.x + tid;
+                if (i < K4) {
+                    xs4[i] = v[j];
+                    ss += sq4(v[j]);
+                }
+            }
+        }
+    } else if constexpr (IN == IN_RESID) {
+        double ra = 1.0;
+        if (in.w_a) {
+            double sa = 0.0;
+            for (uint32_t b = 0; b < K4; b += span) {
+                float4 v[PER];
+                load_f4(in.x, b, K4, v);
+#pragma unroll
+                for (int j = 0; j < PER; ++j) sa += sq4(v[j]);
+            }
+            ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
+        }
+        for (uint32_t b = 0; b < K4; b += span) {
+            float4 x[PER], r[PER], w[PER];
+            load_f4(in.x, b, K4, x);
+            load_f4(in.res, b, K4, r);
+            if (in.w_a) load_f4(in.w_a, b, K4, w);
+#pragma unroll
+            for (int j = 0; j < PER; ++j) {
+                const uint32_t i = b + j * blockDim.x + tid;
+                if (i < K4) {
+                    const float4 t = in.w_a ? norm4(x[j], ra, w[j]) : x[j];
+                    const float4 v = resid4(t, r[j], in.scale);
+                    xs4[i] = v;
+                    ss += sq4(v);
+                    if (writer) reinterpret_cast<float4*>(in.x_out)[i] = v;
+                }
+            }
+        }
+    } else {  // IN_EMBED
+        embed_row(in, xs, K);
+        __syncthreads();
+        for (uint32_t i = tid; i < K4; i += blockDim.x) {
+            const float4 v = xs4[i];
+            ss += sq4(v);
+            if (writer) reinterpret_cast<float4*>(in.x_out)[i] = v;
+        }
+    }
+    const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
+    for (uint32_t b = 0; b < K4; b += span) {
+        float4 w[PER];
+        load_f4(in.w_n, b, K4, w);
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+            const uint32_t i = b + j * blockDim.x + tid;
+            if (i < K4) xs4[i] = norm4(xs4[i], rn, w[j]);
+        }
+    }
+    __syncthreads();
+}
+
+// ---- Q4_0 GEMV on the int8 matrix cores ---------------------------------------------------------
+//
+// y = W x with W in Q4_0 and x fp32.  Each 32-element block b of x is written exactly as
+//   x_j = s_b (q0_j + q1_j 2^-7 + q2_j 2^-14 + q3_j 2^-21),  s_b = 2^(ilogb(max |x_b|) - 5),
+// with integer digits |q| <= 64 (every step is exact in fp32: scaling by a power of two,
+// rint, and subtracting an integer within 0.5).  Then for row r and block b
+//   sum_j (n_rj - 8) x_j = sum_t 2^-7t s_b sum_j n_rj q_tj  -  8 sum_j x_j,
+// and the integer sums over j come from v_mfma_i32_16x16x64_i8: A = the raw nibbles n of a
+// 16-row tile (lane (r, g) holds block g of row r: low nibbles feed one MFMA, high nibbles a
+// second), B = the digits, with MFMA column n = (block n / 4, digit n % 4), so both MFMAs of
+// a 128-column super-tile accumulate into one 16 x 16 int32 tile.  Lanes then fold the tile
+// into fp32 row partials with the block scales d, reduce over the 16 columns, and the waves
+// that split the super-tiles of a row tile add their partials in LDS in slice order.
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+
+// Streaming loads of weights (read once per step): non-temporal hint, global address space
+// (a generic pointer would become a flat load, which also counts against the LDS counter).
+typedef const __attribute__((address_space(1))) v4u* gv4u;
+typedef const __attribute__((address_space(1))) v2u* gv2u;
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+    const v4u t = __builtin_nontemporal_load((gv4u)(p));
+    return make_uint4(t.x, t.y, t.z, t.w);
+}
+__device__ __forceinline__ uint2 ld_stream(const uint2* p) {
+    const v2u t = __builtin_nontemporal_load((gv2u)(p));
+    return make_uint2(t.x, t.y);
+}
+
+// Digit words of 8 consecutive elements v of a block whose max |x| is m: w[t] holds the 8
+// int8 digits of plane t.
+__device__ __forceinline__ void digit_words(const float (&v)[8], float m, uint32_t (&w)[4][2]) {
+    const int e = m > 0.0f ? ilogbf(m) : 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) w[t][0] = w[t][1] = 0u;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float u = m > 0.0f ? ldexpf(v[k], 5 - e) : 0.0f;  // |u| < 64, exact
+        const float q0 = rintf(u);
+        float r = (u - q0) * 128.0f;
+        const float q1 = rintf(r);
+        r = (r - q1) * 128.0f;
+        const float q2 = rintf(r);
+        r = (r - q2) * 128.0f;
+        const float q3 = rintf(r);
+        const int sh = 8 * (k & 3);
+        w[0][k >> 2] |= ((uint32_t)(int)q0 & 0xFFu) << sh;
+        w[1][k >> 2] |= ((uint32_t)(int)q1 & 0xFFu) << sh;
+        w[2][k >> 2] |= ((uint32_t)(int)q2 & 0xFFu) << sh;
+        w[3][k >> 2] |= ((uint32_t)(int)q3 & 0xFFu) << sh;
+    }
+}
+
+// Digits of 8 consecutive elements v of block b (part p of 4), stored at dig[(b * 4 + t) * 32 + 8 p].
+__device__ __forceinline__ void digits8(const float (&v)[8], float m, int8_t* dig, uint32_t b, uint32_t p) {
+    uint32_t w[4][2];
+    digit_words(v, m, w);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        *reinterpret_cast<uint2*>(dig + ((size_t)b * 4 + t) * 32 + 8 * p) = make_uint2(w[t][0], w[t][1]);
+}
+
+// Block max |x| and sum over the 4 lanes (a quad) that hold a block's 8-element parts.
+__device__ __forceinline__ void quad_stats(const float (&v)[8], float& m, float& sum) {
+    float mm = 0.0f, ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        mm = fmaxf(mm, fabsf(v[k]));
+        ss += v[k];
+    }
+    mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
+    mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    m = mm;
+    sum = ss;
+}
+
+// Table entries of a block (max |x| m, element sum `sum`): plane scales s 2^-7t and the bias.
+__device__ __forceinline__ DigitTab digit_entry(float m, float sum, int t) {
+    const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
+    return DigitTab{ldexpf(s, -7 * t), t == 0 ? 8.0f * sum : 0.0f};
+}
+
+__device__ __forceinline__ void digit_tab(DigitTab* tab, uint32_t b, float m, float sum) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) tab[b * 4 + t] = digit_entry(m, sum, t);
+}
+
+// ---- GEMV prologue: the input's digit image in LDS ----------------------------------------------
+//
+// Thread i takes the octets (8 consecutive elements) o = i + j * blockDim, j < Q, so the four
+// threads of a quad hold one 32-element block.  The kernel issues these input loads before its
+// weight loads: vector memory loads return in issue order, so input loads queued behind the
+// weight stream would wait for all of it, while issued first they return early and the
+// prologue's arithmetic runs while the weights stream in.
+
+template <int IN, int Q>
+struct InputRegs {
+    float4 x[Q][2], r[Q][2], wa[Q][2], wn[Q][2];
+    uint4 d[3 * Q];  // IN_DIGITS: the digit image, 16 bytes per thread and slot
+};
+
+__device__ __forceinline__ void ld_oct(const float* p, uint32_t o, bool ok, float4 (&v)[2]) {
+    const float4* q = reinterpret_cast<const float4*>(p) + 2 * (size_t)(ok ? o : 0);
+    v[0] = ok ? q[0] : make_float4(0.f, 0.f, 0.f, 0.f);
+    v[1] = ok ? q[1] : make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+__device__ __forceinline__ void oct_f(const float4 (&v)[2], float (&o)[8]) {
+    o[0] = v[0].x; o[1] = v[0].y; o[2] = v[0].z; o[3] = v[0].w;
+    o[4] = v[1].x; o[5] = v[1].y; o[6] = v[1].z; o[7] = v[1].w;
+}
+
+// Issues every global load the prologue needs (no use of the results).
+template <int IN, int Q>
+__device__ __forceinline__ void input_load(const InputStage& in, uint32_t K, uint32_t nst, InputRegs<IN, Q>& g) {
+    const uint32_t tid = threadIdx.x;
+    if constexpr (IN == IN_DIGITS) {
+        const uint4* src = reinterpret_cast<const uint4*>(in.dig);
+        const uint32_t n16 = nst * 40;
+#pragma unroll
+        for (int j = 0; j < 3 * Q; ++j) {
+            const uint32_t i = tid + j * blockDim.x;
+            g.d[j] = i < n16 ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+        }
+    } else {
+        const uint32_t n8 = K / 8;
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t o = tid + j * blockDim.x;
+            const bool ok = o < n8;
+            if constexpr (IN != IN_EMBED) ld_oct(in.x, o, ok, g.x[j]);
+            if constexpr (IN == IN_RESID) {
+                ld_oct(in.res, o, ok, g.r[j]);
+                if (in.w_a) ld_oct(in.w_a, o, ok, g.wa[j]);
+            }
+            if constexpr (IN != IN_PLAIN) ld_oct(in.w_n, o, ok, g.wn[j]);
+        }
+    }
+}
+
+// Finishes the prologue from the registers input_load filled: the LDS digit image of the
+// (normalised) input.  xs (K floats of LDS) is used by IN_EMBED only.  The caller syncs.
+template <int IN, int Q>
+__device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t nst, InputRegs<IN, Q>& g, float* xs,
+                             int8_t* dig, DigitTab* tab, double* red) {
+    const uint32_t tid = threadIdx.x, n8 = K / 8;
+    if constexpr (IN == IN_DIGITS) {
+        uint4* dst = reinterpret_cast<uint4*>(dig);  // digits and table are contiguous
+#pragma unroll
+        for (int j = 0; j < 3 * Q; ++j) {
+            const uint32_t i = tid + j * blockDim.x;
+            if (i < nst * 40) dst[i] = g.d[j];
+        }
+        return;
+    } else {
+        float v[Q][8];
+        if constexpr (IN == IN_PLAIN) {
+#pragma unroll
+            for (int j = 0; j < Q; ++j) oct_f(g.x[j], v[j]);
+        } else {
+            float t[Q][8];
+            if constexpr (IN == IN_EMBED) {
+                embed_row(in, xs, K);
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < Q; ++j) {
+                    const uint32_t o = tid + j * blockDim.x;
+                    float4 e[2];
+                    if (o < n8) {
+                        e[0] = reinterpret_cast<const float4*>(xs)[2 * o];
+                        e[1] = reinterpret_cast<const float4*>(xs)[2 * o + 1];
+                    } else {
+                        e[0] = e[1] = make_float4(0.f, 0.f, 0.f, 0.f);
+                    }
+                    oct_f(e, t[j]);
+                }
+            } else if constexpr (IN == IN_NORM) {
+#pragma unroll
+                for (int j = 0; j < Q; ++j) oct_f(g.x[j], t[j]);
+            } else {  // IN_RESID: t = ((w_a ? rms(x) w_a : x) + res) * scale
+                double ra = 1.0;
+                if (in.w_a) {
+                    double sa = 0.0;
+#pragma unroll
+                    for (int j = 0; j < Q; ++j) sa += sq4(g.x[j][0]) + sq4(g.x[j][1]);
+                    ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
+                }
+#pragma unroll
+                for (int j = 0; j < Q; ++j) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const float4 u = in.w_a ? norm4(g.x[j][h], ra, g.wa[j][h]) : g.x[j][h];
+                        g.x[j][h] = resid4(u, g.r[j][h], in.scale);
+                    }
+                    oct_f(g.x[j], t[j]);
+                }
+            }
+            double ss = 0.0;
+#pragma unroll
+            for (int j = 0; j < Q; ++j)
+#pragma unroll
+                for (int k = 0; k < 8; ++k) ss += (double)t[j][k] * t[j][k];
+            if (IN != IN_NORM && blockIdx.x == 0 && in.x_out != nullptr) {
+#pragma unroll
+                for (int j = 0; j < Q; ++j) {
+                    const uint32_t o = tid + j * blockDim.x;
+                    if (o < n8) {
+                        float4* dst = reinterpret_cast<float4*>(in.x_out) + 2 * (size_t)o;
+                        dst[0] = make_float4(t[j][0], t[j][1], t[j][2], t[j][3]);
+                        dst[1] = make_float4(t[j][4], t[j][5], t[j][6], t[j][7]);
+                    }
+                }
+            }
+            const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
+#pragma unroll
+            for (int j = 0; j < Q; ++j) {
+                float w[8];
+                oct_f(g.wn[j], w);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v[j][k] = norm_apply(t[j][k], rn, w[k]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < Q; ++j) {
+            const uint32_t o = tid + j * blockDim.x, b = o >> 2, p = o & 3;
+            float m, sum;
+            quad_stats(v[j], m, sum);  // every lane of the quad takes part, in range or not
+            if (b < nst * 4) {
+                digits8(v[j], m, dig, b, p);
+                if (p == 0) digit_tab(tab, b, m, sum);
+            }
+        }
+    }
+}
+
+constexpr int kQ4Ahead = 16;  // super-tiles loaded ahead per wave
+
+struct Q4Tile {
+    uint4 code;   // lane (r, g): the 16 code bytes of block g of row r of the super-tile
+    uint2 scale;  // lane (q, n): the fp16 scales of rows 4q..4q+3 for block n / 4
+};
+
+// Loads lane's share of super-tile st of 16-row tile `tile` (tiled layout: codes
+// [tile][st][16 rows][4 blocks][16 bytes], scales [tile][st][4 blocks][16 rows]).
+__device__ __forceinline__ void q4_tile_load(const uint4* codes, const uint2* scales, size_t tile, uint32_t nst,
+                                             uint32_t st, uint32_t lane, Q4Tile& t) {
+    const size_t base = tile * nst + st;
+    t.code = ld_stream(codes + base * 64 + (lane & 15) * 4 + (lane >> 4));
+    t.scale = ld_stream(scales + base * 16 + ((lane & 15) >> 2) * 4 + (lane >> 4));
+}
+
+// acc[i] += row (4q + i) of the tile times the input, summed over the lane's column n: two
+// int8 MFMAs (low then high nibbles) against the digit planes of super-tile st in LDS, folded
+// with the block scales.  Lane l = 16 q + n; column n is (block n / 4, digit plane n % 4).
+__device__ __forceinline__ void q4_mfma_tile(const Q4Tile& w, uint32_t st, const int8_t* dig, const DigitTab* tab,
+                                             uint32_t lane, float (&acc)[4]) {
+    const uint32_t q = lane >> 4, n = lane & 15, blk = n >> 2, t = n & 3;
+    const uint4 cw = w.code;
+    const uint2 sw = w.scale;
+    const v4i a1 = {(int)(cw.x & 0x0F0F0F0Fu), (int)(cw.y & 0x0F0F0F0Fu), (int)(cw.z & 0x0F0F0F0Fu),
+                    (int)(cw.w & 0x0F0F0F0Fu)};
+    const v4i a2 = {(int)((cw.x >> 4) & 0x0F0F0F0Fu), (int)((cw.y >> 4) & 0x0F0F0F0Fu),
+                    (int)((cw.z >> 4) & 0x0F0F0F0Fu), (int)((cw.w >> 4) & 0x0F0F0F0Fu)};
+    const v4i zero = {0, 0, 0, 0};
+    v4i b1 = zero, b2 = zero;
+    if (blk == q) {  // B lane (k-group q, column n) is non-zero for block q only
+        const uint4* dp = reinterpret_cast<const uint4*>(dig + ((size_t)(st * 4 + q) * 4 + t) * 32);
+        const uint4 lo = dp[0], hi = dp[1];
+        b1 = v4i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w};
+        b2 = v4i{(int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    }
+    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, zero, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, b2, d, 0, 0, 0);
+    const DigitTab tb = tab[(st * 4 + blk) * 4 + t];
+    const uint16_t dh[4] = {(uint16_t)(sw.x & 0xFFFFu), (uint16_t)(sw.x >> 16), (uint16_t)(sw.y & 0xFFFFu),
+                            (uint16_t)(sw.y >> 16)};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = fmaf(h2f(dh[i]), fmaf((float)d[i], tb.scale, -tb.bias), acc[i]);
+}
+
+// Sum of acc over the 16 columns of each row (lanes of a 16-lane group hold one row quad).
+__device__ __forceinline__ void q4_row_sums(float (&acc)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) acc[i] += __shfl_xor(acc[i], o, 16);
+}
+
+}  // namespace af

@@ -1,349 +1,25 @@
-// HIP kernels for gfx950 (MI355X): the batch-1 decode step of a Q4_0 / Q6_K
-// transformer.  Every kernel is bandwidth-bound GEMV or streaming work; none
-// uses MFMA.  Cross-workgroup results (attention chunks, argmax partials) are
-// combined by the last workgroup to finish, found with a device-scope counter
+// HIP kernels for gfx950 (MI355X): the per-operation entry points of the decode step of a
+// Q4_0 / Q6_K transformer (Q4_0 GEMV on the int8 matrix cores, Q6_K head with greedy argmax,
+// GQA decode attention, RMSNorm).  Cross-workgroup results (attention chunks, argmax
+// partials) are combined by the last workgroup to finish, found with a device-scope counter
 // that the last workgroup resets, so the kernels can be replayed in a graph.
-#include <hip/hip_runtime.h>
-#include <math.h>
-
-#include "af_internal.h"
+#include "device.h"
 
 namespace af {
 
-// ---- helpers ----------------------------------------------------------------------------------
-
-__device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
-
-template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
-}
-
-// Sum over the block of one double per thread (blockDim a multiple of 64, <= 512).
-__device__ double block_sum_d(double v, double* red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    double t = 0.0;
-    for (int w = 0; w < nw; ++w) t += red[w];
-    return t;
-}
-
-__device__ float block_sum_f(float v, float* red) {
-    v = wave_sum(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = 0.0f;
-    for (int w = 0; w < nw; ++w) t += red[w];
-    return t;
-}
-
-__device__ float block_max_f(float v, float* red) {
-    v = wave_max(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    __syncthreads();
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = red[0];
-    for (int w = 1; w < nw; ++w) t = fmaxf(t, red[w]);
-    return t;
-}
-
-// f32(x * r * w) with the products in double, as the FP64 RMSNorm oracle rounds its output.
-__device__ __forceinline__ float norm_apply(float x, double r, float w) {
-    return (float)__dmul_rn(__dmul_rn((double)x, r), (double)w);
-}
-
-__device__ __forceinline__ double inv_rms(double sumsq, uint32_t n, float eps) {
-    return 1.0 / sqrt(__dadd_rn(sumsq / (double)n, (double)eps));
-}
-
-// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in double, rounded to f32, times up in f32.
-__device__ __forceinline__ float gelu_mul(float g, float u) {
-    const double x = (double)g;
-    const double c = sqrt(2.0 / 3.14159265358979323846);
-    const double inner = __dadd_rn(x, __dmul_rn(__dmul_rn(__dmul_rn(0.044715, x), x), x));
-    const double t = tanh(__dmul_rn(c, inner));
-    const float gl = (float)__dmul_rn(__dmul_rn(0.5, x), __dadd_rn(1.0, t));
-    return __fmul_rn(gl, u);
-}
-
-// One 64-weight Q6_K unit's code bytes for quarter q from its ql/ql/qh dwords.
-__device__ __forceinline__ uint32_t q6_codes(uint32_t a, uint32_t b, uint32_t h, int q) {
-    switch (q) {
-        case 0: return (a & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
-        case 1: return (b & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
-        case 2: return ((a >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
-        default: return ((b >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
-    }
-}
-
-// ---- input stage: builds the fp32 GEMV input vector in LDS ------------------------------------
-
-// Embedding row (Q6_K, repacked) times emb_scale into xs; one thread per unit dword (16 elements).
-__device__ void embed_row(const InputStage& in, float* xs, uint32_t K) {
-    const Q6View& t = in.table;
-    const uint32_t row = min(in.ids[in.state[ST_POS]], t.rows - 1);  // ids are validated; never read past the table
-    const uint32_t units = t.units, sblocks = units / 4;
-    const uint32_t* A = reinterpret_cast<const uint32_t*>(t.a + (size_t)row * units * 16);
-    const uint32_t* B = reinterpret_cast<const uint32_t*>(t.b + (size_t)row * units * 16);
-    const uint32_t* H = reinterpret_cast<const uint32_t*>(t.h + (size_t)row * units * 16);
-    for (uint32_t w = threadIdx.x; w < units * 4; w += blockDim.x) {
-        const uint32_t u = w >> 2, k = w & 3;
-        const uint32_t sb = u >> 2, g = (u >> 1) & 1, hh = u & 1;
-        const uint32_t a = A[w], b = B[w], h = H[w];
-        const uint32_t sc = t.s[(size_t)row * units + u];
-        const float d = h2f(t.d[(size_t)row * sblocks + sb]);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const uint32_t c = q6_codes(a, b, h, q);
-            const float ds = __fmul_rn(d, (float)(int8_t)(sc >> (8 * q)));
-#pragma unroll
-            for (int n = 0; n < 4; ++n) {
-                const int code = (int)((c >> (8 * n)) & 0xFF) - 32;
-                const uint32_t e = sb * 256 + g * 128 + q * 32 + hh * 16 + 4 * k + n;
-                xs[e] = __fmul_rn(__fmul_rn(ds, (float)code), in.emb_scale);
-            }
-        }
-    }
-    (void)K;
-}
-
-// Loads N float4 per thread from p at float4 indices base + j * blockDim + thread (zero past n4).
-// All loads are issued before any is used, so one memory latency covers the whole batch.
-template <int N>
-__device__ __forceinline__ void load_f4(const float* __restrict__ p, uint32_t base, uint32_t n4, float4 (&o)[N]) {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-        const uint32_t i = base + j * blockDim.x + threadIdx.x;
-        o[j] = i < n4 ? reinterpret_cast<const float4*>(p)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-}
-
-__device__ __forceinline__ double sq4(float4 v) {
-    return (double)v.x * v.x + (double)v.y * v.y + (double)v.z * v.z + (double)v.w * v.w;
-}
-
-__device__ __forceinline__ float4 norm4(float4 x, double r, float4 w) {
-    return make_float4(norm_apply(x.x, r, w.x), norm_apply(x.y, r, w.y), norm_apply(x.z, r, w.z),
-                       norm_apply(x.w, r, w.w));
-}
-
-__device__ __forceinline__ float4 resid4(float4 t, float4 res, float scale) {
-    return make_float4(__fmul_rn(__fadd_rn(t.x, res.x), scale), __fmul_rn(__fadd_rn(t.y, res.y), scale),
-                       __fmul_rn(__fadd_rn(t.z, res.z), scale), __fmul_rn(__fadd_rn(t.w, res.w), scale));
-}
-
-// Builds the normalised fp32 input vector in LDS (IN_NORM, IN_RESID, IN_EMBED).  K % 4 == 0 and
-// every vector is 16-byte aligned.  Passes cover 4 float4 per thread (4096 floats at 256
-// threads), so for the model widths each loop body runs once with its loads batched.
-template <int IN>
-__device__ void input_stage(const InputStage& in, float* xs, uint32_t K, double* red) {
-    constexpr int PER = 4;
-    const uint32_t tid = threadIdx.x, K4 = K / 4, span = PER * blockDim.x;
-    float4* xs4 = reinterpret_cast<float4*>(xs);
-    const bool writer = blockIdx.x == 0 && in.x_out != nullptr;
-    double ss = 0.0;
-    if constexpr (IN == IN_NORM) {
-        for (uint32_t b = 0; b < K4; b += span) {
-            float4 v[PER];
-            load_f4(in.x, b, K4, v);
-#pragma unroll
-            for (int j = 0; j < PER; ++j) {
-                const uint32_t i = b + j * blockDim.x + tid;
-                if (i < K4) {
-                    xs4[i] = v[j];
-                    ss += sq4(v[j]);
-                }
-            }
-        }
-    } else if constexpr (IN == IN_RESID) {
-        double ra = 1.0;
-        if (in.w_a) {
-            double sa = 0.0;
-            for (uint32_t b = 0; b < K4; b += span) {
-                float4 v[PER];
-                load_f4(in.x, b, K4, v);
-#pragma unroll
-                for (int j = 0; j < PER; ++j) sa += sq4(v[j]);
-            }
-            ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
-        }
-        for (uint32_t b = 0; b < K4; b += span) {
-            float4 x[PER], r[PER], w[PER];
-            load_f4(in.x, b, K4, x);
-            load_f4(in.res, b, K4, r);
-            if (in.w_a) load_f4(in.w_a, b, K4, w);
-#pragma unroll
-            for (int j = 0; j < PER; ++j) {
-                const uint32_t i = b + j * blockDim.x + tid;
-                if (i < K4) {
-                    const float4 t = in.w_a ? norm4(x[j], ra, w[j]) : x[j];
-                    const float4 v = resid4(t, r[j], in.scale);
-                    xs4[i] = v;
-                    ss += sq4(v);
-                    if (writer) reinterpret_cast<float4*>(in.x_out)[i] = v;
-                }
-            }
-        }
-    } else {  // IN_EMBED
-        embed_row(in, xs, K);
-        __syncthreads();
-        for (uint32_t i = tid; i < K4; i += blockDim.x) {
-            const float4 v = xs4[i];
-            ss += sq4(v);
-            if (writer) reinterpret_cast<float4*>(in.x_out)[i] = v;
-        }
-    }
-    const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
-    for (uint32_t b = 0; b < K4; b += span) {
-        float4 w[PER];
-        load_f4(in.w_n, b, K4, w);
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-            const uint32_t i = b + j * blockDim.x + tid;
-            if (i < K4) xs4[i] = norm4(xs4[i], rn, w[j]);
-        }
-    }
-    __syncthreads();
-}
-
-// ---- Q4_0 GEMV on the int8 matrix cores ---------------------------------------------------------
-//
-// y = W x with W in Q4_0 and x fp32.  Each 32-element block b of x is written exactly as
-//   x_j = s_b (q0_j + q1_j 2^-7 + q2_j 2^-14 + q3_j 2^-21),  s_b = 2^(ilogb(max |x_b|) - 5),
-// with integer digits |q| <= 64 (every step is exact in fp32: scaling by a power of two,
-// rint, and subtracting an integer within 0.5).  Then for row r and block b
-//   sum_j (n_rj - 8) x_j = sum_t 2^-7t s_b sum_j n_rj q_tj  -  8 sum_j x_j,
-// and the integer sums over j come from v_mfma_i32_16x16x64_i8: A = the raw nibbles n of a
-// 16-row tile (lane (r, g) holds block g of row r: low nibbles feed one MFMA, high nibbles a
-// second), B = the digits, with MFMA column n = (block n / 4, digit n % 4), so both MFMAs of
-// a 128-column super-tile accumulate into one 16 x 16 int32 tile.  Lanes then fold the tile
-// into fp32 row partials with the block scales d, reduce over the 16 columns, and the waves
-// that split the super-tiles of a row tile add their partials in LDS in slice order.
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
-typedef unsigned v2u __attribute__((ext_vector_type(2)));
-
-// Streaming loads of weights (read once per step): non-temporal hint.
-__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
-    const v4u t = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(p));
-    return make_uint4(t.x, t.y, t.z, t.w);
-}
-__device__ __forceinline__ uint2 ld_stream(const uint2* p) {
-    const v2u t = __builtin_nontemporal_load(reinterpret_cast<const v2u*>(p));
-    return make_uint2(t.x, t.y);
-}
-
-// Digits of 8 consecutive elements v of block b (part p of 4), given the block's max |x| m:
-// 8 bytes per digit t stored at dig[((st * 4 + g) * 4 + t) * 32 + 8 p].
-__device__ __forceinline__ void digits8(const float (&v)[8], float m, int8_t* dig, uint32_t b, uint32_t p) {
-    const int e = m > 0.0f ? ilogbf(m) : 0;
-    uint32_t w[4][2] = {{0u, 0u}, {0u, 0u}, {0u, 0u}, {0u, 0u}};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const float u = m > 0.0f ? ldexpf(v[k], 5 - e) : 0.0f;  // |u| < 64, exact
-        const float q0 = rintf(u);
-        float r = (u - q0) * 128.0f;
-        const float q1 = rintf(r);
-        r = (r - q1) * 128.0f;
-        const float q2 = rintf(r);
-        r = (r - q2) * 128.0f;
-        const float q3 = rintf(r);
-        const int sh = 8 * (k & 3);
-        w[0][k >> 2] |= ((uint32_t)(int)q0 & 0xFFu) << sh;
-        w[1][k >> 2] |= ((uint32_t)(int)q1 & 0xFFu) << sh;
-        w[2][k >> 2] |= ((uint32_t)(int)q2 & 0xFFu) << sh;
-        w[3][k >> 2] |= ((uint32_t)(int)q3 & 0xFFu) << sh;
-    }
-    const uint32_t st = b >> 2, g = b & 3;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-        *reinterpret_cast<uint2*>(dig + ((size_t)(st * 4 + g) * 4 + t) * 32 + 8 * p) = make_uint2(w[t][0], w[t][1]);
-}
-
-// Block max |x| and sum over the 4 lanes (a quad) that hold a block's 8-element parts.
-__device__ __forceinline__ void quad_stats(const float (&v)[8], float& m, float& sum) {
-    float mm = 0.0f, ss = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        mm = fmaxf(mm, fabsf(v[k]));
-        ss += v[k];
-    }
-    mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
-    mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
-    m = mm;
-    sum = ss;
-}
-
-__device__ __forceinline__ void digit_tab(DigitTab* tab, uint32_t b, float m, float sum) {
-    const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) tab[b * 4 + t] = DigitTab{ldexpf(s, -7 * t), t == 0 ? 8.0f * sum : 0.0f};
-}
-
-// Digits of the input vector src (K = 32 B floats, 16-byte aligned; global or LDS) for all
-// nst * 4 blocks (blocks >= B are zero): four threads per block, eight elements each.
-// Layout: dig[(st * 4 + g) * 4 + t][32] int8 for block b = 4 st + g, tab[b * 4 + t].
-__device__ void make_digits(const float* src, uint32_t B, uint32_t nst, int8_t* dig, DigitTab* tab) {
-    const uint32_t nb = nst * 4;
-    for (uint32_t base = 0; base < nb * 4; base += blockDim.x) {
-        const uint32_t i = base + threadIdx.x, b = i >> 2, p = i & 3;
-        float v[8];
-        const bool ok = b < B;
-        const float4* q = reinterpret_cast<const float4*>(src + (size_t)(ok ? b : 0) * 32 + 8 * p);
-        const float4 a0 = ok ? q[0] : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 a1 = ok ? q[1] : make_float4(0.f, 0.f, 0.f, 0.f);
-        v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
-        v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
-        float m, sum;
-        quad_stats(v, m, sum);  // every lane of the quad takes part, in range or not
-        if (b < nb) {
-            digits8(v, m, dig, b, p);
-            if (p == 0) digit_tab(tab, b, m, sum);
-        }
-    }
-}
-
-constexpr int kQ4Ahead = 16;  // super-tiles loaded ahead per wave
-
-struct Q4Tile {
-    uint4 code;
-    uint2 scale;
-};
-
-template <int T, int IN, int OUT>
+template <int T, int IN, int OUT, int Q>
 __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_rows) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[8];
     __shared__ float part[T][8][16];
 
     if (a.state && a.state[ST_STOP]) return;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t S = a.slices, tile = wave / S, sl = wave % S;
     const Q4View& m = (T == 2 && tile == 1) ? a.w2 : a.w;
     const uint32_t B = a.w.blocks, K = B * 32, nst = a.w.nst;
     const uint32_t per = (nst + S - 1) / S, st0 = min(nst, sl * per), st1 = min(nst, st0 + per);
-    const size_t tile_base = (size_t)blockIdx.x * nst;
-    const uint32_t r_ld = lane & 15, g_ld = lane >> 4;  // A operand: row, block in super-tile
-    const uint32_t q = lane >> 4, n = lane & 15;         // D tile: rows 4q..4q+3, column n
-    const uint32_t blk = n >> 2, t = n & 3;
+    const uint32_t q = lane >> 4, n = lane & 15;  // D tile: rows 4q..4q+3, column n
 
     const uint4* codes = reinterpret_cast<const uint4*>(m.codes);
     const uint2* scales = reinterpret_cast<const uint2*>(m.scales);
@@ -351,63 +27,34 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
 #pragma unroll
         for (int u = 0; u < kQ4Ahead; ++u) {
             const uint32_t st = c0 + u;
-            if (st < st1) {
-                buf[u].code = ld_stream(codes + (tile_base + st) * 64 + r_ld * 4 + g_ld);
-                buf[u].scale = ld_stream(scales + (tile_base + st) * 16 + blk * 4 + q);
-            }
+            if (st < st1) q4_tile_load(codes, scales, blockIdx.x, nst, st, lane, buf[u]);
         }
     };
+    InputRegs<IN, Q> g;
+    input_load<IN, Q>(a.in, K, nst, g);  // inputs first (see input_load)
+    __builtin_amdgcn_sched_barrier(0);
     Q4Tile buf[kQ4Ahead];
-    load(buf, st0);  // weights first: their latency overlaps the input stage
+    load(buf, st0);
+    __builtin_amdgcn_sched_barrier(0);
 
-    const size_t xs_bytes = IN == IN_PLAIN ? 0 : (size_t)K * 4;
+    const size_t xs_bytes = IN == IN_EMBED ? (size_t)K * 4 : 0;
     int8_t* dig = reinterpret_cast<int8_t*>(smem + xs_bytes);
     DigitTab* tab = reinterpret_cast<DigitTab*>(smem + xs_bytes + (size_t)nst * 512);
-    if constexpr (IN == IN_PLAIN) {
-        make_digits(a.in.x, B, nst, dig, tab);
-    } else {
-        float* xs = reinterpret_cast<float*>(smem);
-        input_stage<IN>(a.in, xs, K, red);
-        make_digits(xs, B, nst, dig, tab);
-    }
+    input_digits<IN, Q>(a.in, K, nst, g, reinterpret_cast<float*>(smem), dig, tab, red);
     __syncthreads();
 
-    const bool bsel = (n >> 2) == q;  // B lane (k-group q, column n) is non-zero for block q only
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    const v4i zero = {0, 0, 0, 0};
     for (uint32_t c0 = st0; c0 < st1; c0 += kQ4Ahead) {
 #pragma unroll
         for (int u = 0; u < kQ4Ahead; ++u) {
             const uint32_t st = c0 + u;
             if (st >= st1) break;
-            const uint4 cw = buf[u].code;
-            const uint2 sw = buf[u].scale;
-            const v4i a1 = {(int)(cw.x & 0x0F0F0F0Fu), (int)(cw.y & 0x0F0F0F0Fu), (int)(cw.z & 0x0F0F0F0Fu),
-                            (int)(cw.w & 0x0F0F0F0Fu)};
-            const v4i a2 = {(int)((cw.x >> 4) & 0x0F0F0F0Fu), (int)((cw.y >> 4) & 0x0F0F0F0Fu),
-                            (int)((cw.z >> 4) & 0x0F0F0F0Fu), (int)((cw.w >> 4) & 0x0F0F0F0Fu)};
-            v4i b1 = zero, b2 = zero;
-            if (bsel) {
-                const uint4* dp = reinterpret_cast<const uint4*>(dig + ((size_t)(st * 4 + q) * 4 + t) * 32);
-                const uint4 lo = dp[0], hi = dp[1];
-                b1 = v4i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w};
-                b2 = v4i{(int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-            }
-            v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, zero, 0, 0, 0);
-            d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, b2, d, 0, 0, 0);
-            const DigitTab tb = tab[(st * 4 + blk) * 4 + t];
-            const uint16_t dh[4] = {(uint16_t)(sw.x & 0xFFFFu), (uint16_t)(sw.x >> 16), (uint16_t)(sw.y & 0xFFFFu),
-                                    (uint16_t)(sw.y >> 16)};
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] = fmaf(h2f(dh[i]), fmaf((float)d[i], tb.scale, -tb.bias), acc[i]);
+            q4_mfma_tile(buf[u], st, dig, tab, lane, acc);
         }
         if (c0 + kQ4Ahead < st1) load(buf, c0 + kQ4Ahead);
     }
     // sum the 16 columns of each row, then the slices
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) acc[i] += __shfl_xor(acc[i], o, 16);
+    q4_row_sums(acc);
     if (n == 0) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) part[tile][sl][4 * q + i] = acc[i];
@@ -430,20 +77,25 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
     }
 }
 
-// Waves per row tile: enough waves to fill the chip (~2048), within the super-tiles and 8 per block.
-static uint32_t q4_slices(uint32_t tiles, uint32_t per_tile, uint32_t nst) {
-    uint32_t s = 1;
-    while (s < 8 && per_tile * s * 2 <= 8 && tiles * per_tile * s < 2048 && s * 2 <= nst) s *= 2;
-    return s;
+// Every GEMV block has 512 threads: T row tiles, each split over 8 / T waves by super-tile.
+constexpr uint32_t kQ4Threads = 512;
+
+template <int T, int IN, int OUT, int Q>
+static hipError_t q4_launch3(Q4Args a, uint32_t out_rows, hipStream_t st) {
+    const uint32_t tiles = (out_rows + 15) / 16;
+    a.slices = kQ4Threads / 64 / T;
+    const size_t lds = (IN == IN_EMBED ? (size_t)a.w.blocks * 32 * 4 : 0) + (size_t)a.w.nst * (512 + 128);
+    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT, Q>), dim3(tiles), dim3(kQ4Threads), lds, st, a, out_rows);
+    return hipGetLastError();
 }
 
+// Octets per thread: the prologue covers 16 nst octets (128 nst elements) with 512 threads.
 template <int T, int IN, int OUT>
-static hipError_t q4_launch2(Q4Args a, uint32_t out_rows, hipStream_t st) {
-    const uint32_t tiles = (out_rows + 15) / 16;
-    a.slices = q4_slices(tiles, T, a.w.nst);
-    const size_t lds = (IN == IN_PLAIN ? 0 : (size_t)a.w.blocks * 32 * 4) + (size_t)a.w.nst * (512 + 128);
-    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT>), dim3(tiles), dim3(64 * T * a.slices), lds, st, a, out_rows);
-    return hipGetLastError();
+static hipError_t q4_launch2(const Q4Args& a, uint32_t out_rows, hipStream_t st) {
+    const uint32_t oct = a.w.nst * 16;
+    if (oct <= kQ4Threads) return q4_launch3<T, IN, OUT, 1>(a, out_rows, st);
+    if (oct <= 2 * kQ4Threads) return q4_launch3<T, IN, OUT, 2>(a, out_rows, st);
+    return q4_launch3<T, IN, OUT, 4>(a, out_rows, st);
 }
 
 template <int IN>
@@ -463,6 +115,7 @@ hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t o
         case IN_NORM: return q4_launch1<IN_NORM>(a, out_kind, out_rows, s);
         case IN_RESID: return q4_launch1<IN_RESID>(a, out_kind, out_rows, s);
         case IN_EMBED: return q4_launch1<IN_EMBED>(a, out_kind, out_rows, s);
+        case IN_DIGITS: return q4_launch1<IN_DIGITS>(a, out_kind, out_rows, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -513,7 +166,7 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
 
     if (a.state && a.state[ST_STOP]) return;
     const uint32_t units = a.w.units, K = units * 64;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63, wave = (int)wave_id();
     const bool act = (uint32_t)lane < units;
     const uint32_t u = act ? (uint32_t)lane : 0;
     const uint32_t rows = a.w.rows;
@@ -715,7 +368,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     __shared__ float cw[GQ][kAttnMaxChunks];
     __shared__ bool last;
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     if (a.state && a.state[ST_STOP]) return;
     const uint32_t pos = a.state ? a.state[ST_POS] : a.position;
     const uint32_t nvis = a.window ? min(pos + 1, a.window) : pos + 1;
