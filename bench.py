@@ -4,13 +4,14 @@ Workload: a 48-layer Gemma-3-12B-shaped model with seeded random weights (hidden
 FFN 15360, 16 q / 8 kv heads of width 256, 5:1 local(window 1024):global layers, Q4_0
 projections, tied Q6_K embedding/lm-head over 262144 ids); a 128-token random prompt is
 prefilled, then W warm-up and K timed greedy decode steps run through
-GenerationSession::generate (whole step = one hipGraph replay, head + argmax on device).
+GenerationSession::generate (per token: one persistent launch for all 48 layers, one launch
+for the Q6_K head + greedy argmax; ids come back through mapped host memory).
 A "step" is one decoded token; `value` is tokens per second over the K timed steps.
 
-After the timed region, a few more decode steps run with direct launches and a hipEvent
-pair around every kernel (af_session_profile) to time the dominant kernel (the fused
-gate/up GEMV) for the roofline object.  The CPU baseline is the C oracle (a port of the
-reference's FP64 CPU path) timed on a bounded sample on this host.
+After the timed region, a few more decode steps run with a hipEvent pair around every launch
+(af_session_profile) to time the dominant kernel (the layers kernel) for the roofline object,
+with its per-phase timeline from in-kernel timestamps.  The CPU baseline is the C oracle (a
+port of the reference's FP64 CPU path) timed on a bounded sample on this host.
 
     python bench.py [--gpus 1] [--steps 240] [--warmup 16]
 """
@@ -50,6 +51,26 @@ def cpu_baseline(model, prompt, tokens, threads):
     return tokens / dt, dt
 
 
+def measured_traffic(kernel="void af::decode_step_kernel<2>(af::StepArgs)"):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+    (profiles/traffic_config4.json, calibrated against a copy of known size), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic_config4.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][kernel]["hbm_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def kv_read_bytes(model, tokens):
+    """fp16 K and V rows one decode step reads at context `tokens` (window-limited layers)."""
+    total = 0
+    for L in model.layers:
+        vis = min(tokens, L.window) if L.window else tokens
+        total += vis * L.kv_heads * L.head_width * 2 * 2
+    return total
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -79,7 +100,7 @@ def main():
     log(f"device {dev.device_name} {dev.arch} CUs={dev.compute_units}")
     t = time.perf_counter()
     session = diag.open_session(model, capacity)
-    log(f"session open (upload + graph capture) in {time.perf_counter() - t:.1f}s")
+    log(f"session open (weight upload) in {time.perf_counter() - t:.1f}s")
 
     first = session.generate(prompt, stop, a.warmup)
     cached = prompt + first.ids
@@ -102,16 +123,25 @@ def main():
 
     _, timings = session.profile(cached, PROFILE_STEPS)
     session.close()
-    per_token_bytes = 0.0
-    for name, (n, ms, b) in timings.items():
-        if n:
-            per_launch_us = 1000.0 * ms / n
-            per_token_bytes += b * n / PROFILE_STEPS
-            log(f"  {name:10s} launches {n:4d}  avg {per_launch_us:8.2f} us  {b / 1e6:9.3f} MB  "
-                f"{b / (per_launch_us * 1e3):8.1f} GB/s")
-    n, ms, b = timings["gate_up"]
+    # dominant kernel: the persistent step kernel (all 48 layers of one token), timed with a
+    # hipEvent pair around every launch on the session stream
+    n, ms, b = timings["layers"]
     avg_ms = ms / n
-    achieved = b / (avg_ms * 1e6)
+    kv_bytes = kv_read_bytes(model, len(cached))
+    step_bytes = b + kv_bytes
+    achieved = step_bytes / (avg_ms * 1e6)
+    hn, hms, hb = timings["head"]
+    per_token_bytes = step_bytes + hb
+    log(f"  layers kernel: {n} launches, avg {1000 * avg_ms:.1f} us, {step_bytes / 1e9:.3f} GB "
+        f"(weights {b / 1e9:.3f} + KV {kv_bytes / 1e6:.1f} MB) -> {achieved:.0f} GB/s")
+    log(f"  head kernel:   {hn} launches, avg {1000 * hms / hn:.1f} us, {hb / 1e6:.1f} MB -> "
+        f"{hb / (hms / hn * 1e6):.0f} GB/s")
+    for name in ("qkv", "attention", "o_proj", "gate_up", "down", "barrier"):
+        pn, pms, pb = timings[name]
+        if pn:
+            us = 1000.0 * pms / pn
+            rate = f"{pb / (us * 1e3):8.1f} GB/s" if pb else ""
+            log(f"    phase {name:10s} x{pn:5d}  avg {us:7.2f} us  {pb / 1e6:8.3f} MB  {rate}")
     log(f"algorithmic bytes per token {per_token_bytes / 1e9:.3f} GB -> roofline {PEAK_GBS * 1e9 / per_token_bytes:.0f} "
         f"tok/s at 8 TB/s; measured {tok_s:.1f} tok/s = {tok_s * per_token_bytes / (PEAK_GBS * 1e9):.3f} of it")
 
@@ -141,21 +171,24 @@ def main():
         "config": {
             "workload": "config4: 48-layer Gemma-3-12B-shaped decode loop, Q4_0 projections + tied Q6_K "
                         "embedding/lm-head (vocab 262144), 128-token prompt prefill then greedy decode steps "
-                        "replayed as one hipGraph each, fp16 KV cache",
+                        "(one persistent launch for the 48 layers + one head launch per token), fp16 KV cache",
             "hidden": 3840, "intermediate": 15360, "layers": 48, "q_heads": 16, "kv_heads": 8, "head_width": 256,
             "prompt_tokens": PROMPT, "decode_tokens": a.warmup + produced, "batch": 1,
             "algorithmic_bytes_per_token": round(per_token_bytes),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "gate_up (fused RMSNorm prologue + Q4_0 gate/up GEMV + tanh-GELU*up), 48 per token",
+            "kernel": "decode_step_kernel: all 48 layers of one token in one cooperative launch (Q4_0 "
+                      "GEMVs on int8 MFMA, fused norms, GQA attention over fp16 KV)",
             "achieved": round(achieved, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_GBS, 4),
-            "traffic": None,
-            "avg_us": round(1000.0 * avg_ms, 3),
-            "bytes_per_launch": round(b),
+            "traffic": measured_traffic(),
+            "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per launch, calibrated on a 256 MiB copy "
+                              "(profiles/decode_step_kernel_config4.md)",
+            "avg_us": round(1000.0 * avg_ms, 2),
+            "bytes_per_launch": round(step_bytes),
             "launches": n,
         },
         "cpu_baseline": cpu,
