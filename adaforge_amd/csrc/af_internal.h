@@ -15,10 +15,11 @@ namespace af {
 // Rows are grouped in tiles of 16 and blocks in super-tiles of 4 (128 columns), both
 // zero-padded; each (row tile rt, super-tile st) owns one contiguous 1 KB code tile
 // and one 128 B scale tile:
-//   codes  [rt][st][16 rows][4 blocks][16]  the block's nibble bytes, unchanged
+//   codes  [rt][st][4 blocks][16 rows][16]  the block's nibble bytes, unchanged
 //                                           (byte j: low nibble = weight j, high = j + 16)
 //   scales [rt][st][4 blocks][16 rows]      the block's fp16 d
-// so one 16-byte load per lane reads a whole 16 x 128 tile with a wave.
+// so one 16-byte load per lane, lane l at byte 16 l (block l / 16, row l % 16: the matrix
+// cores' A-operand layout), reads a whole 16 x 128 tile with a wave in address order.
 struct Q4View {
     const uint8_t* codes;
     const uint16_t* scales;
@@ -190,12 +191,19 @@ struct StepArgs {
     float* part;                    // attention chunk partials
     uint32_t* counters;             // attention merge tickets, one per KV head
     uint32_t* bar;                  // grid barrier words (kStepBarBytes, zero between launches)
-    uint32_t cmax;                  // attention chunk slots (the grid size)
+    const uint8_t* idle;            // 1152 readable bytes for placeholder weight loads
+    uint32_t cmax;                  // attention chunks per KV head (at most grid / kv_heads, and
+                                    // what the merge can hold in LDS: step_merge_chunks)
     uint32_t advance;               // 1: move ST_POS on at the end (a step without the head)
     float* snap;                    // optional: layer outputs [n_layers][hidden] (the last by the head)
-    uint64_t* clock;                // optional: [2 + 2 * barriers][grid] timestamps (100 MHz): start,
-                                    // then arrival and departure of every barrier, then the end
+    uint64_t* clock;                // optional: [phases][kStepMarks][grid] timestamps (100 MHz), one
+                                    // phase per barrier interval (see StepMark)
 };
+
+// Timeline marks of a phase (workgroup's thread 0): start (barrier departure or kernel start),
+// inputs staged, digit image built, weights streamed, outputs stored, arrival at the closing
+// barrier (or kernel end), and the pre-barrier work of the next phase done.
+enum StepMark { M_START = 0, M_STAGED, M_DIGITS, M_STREAMED, M_STORED, M_ARRIVE, M_PRE, kStepMarks = 8 };
 
 constexpr uint32_t kStepMaxClen = 2048;   // tokens per attention chunk
 constexpr uint32_t kStepMaxChunks = 256;  // chunks per KV head
@@ -203,6 +211,7 @@ constexpr uint32_t kStepMaxUnits = 2;     // GEMV row units per workgroup (16 ro
 constexpr size_t kStepBarBytes = 32 * 10 * 4;
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group);
+uint32_t step_merge_chunks(uint32_t group, size_t lds);  // chunk partials one merge holds in LDS
 hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid);
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s);
 

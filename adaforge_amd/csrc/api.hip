@@ -234,7 +234,7 @@ int upload_q4(Q4Dev& d, const std::vector<af_matrix>& parts) {
                 for (uint32_t k = 0; k < B; ++k) {
                     const uint8_t* blk = src + (r * B + k) * 18;
                     const uint64_t tile = rt * nst + k / 4;
-                    std::memcpy(&codes[(tile * 64 + rr * 4 + (k & 3)) * 16], blk + 2, 16);
+                    std::memcpy(&codes[(tile * 64 + (k & 3) * 16 + rr) * 16], blk + 2, 16);
                     scales[tile * 64 + (k & 3) * 16 + rr] = (uint16_t)(blk[0] | (blk[1] << 8));
                 }
             }
@@ -738,10 +738,10 @@ struct af_session {
     uint32_t max_qkv = 0, max_q = 0, cmax = 0, head_blocks = 0;
     DevMem X, H, QKV, ATT, PROJ, ACT, D, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
     // persistent step kernel: layer table, digit images, barrier words
-    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK;
+    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, IDLE;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
     bool use_step = true;     // all layers of a step in one cooperative launch
-    uint32_t step_grid = 0, group = 0;
+    uint32_t step_grid = 0, step_cmax = 0, group = 0;
     size_t step_lds = 0;
     uint32_t max_kv_rows = 0;
     StepRecord* records = nullptr;      // mapped host memory, capacity + 2 entries (host view)
@@ -930,14 +930,15 @@ struct af_session {
         a.part = PART.as<float>();
         a.counters = COUNTERS.as<uint32_t>();
         a.bar = BAR.as<uint32_t>();
-        a.cmax = step_grid;
+        a.idle = IDLE.as<uint8_t>();
+        a.cmax = step_cmax;
         a.advance = advance ? 1u : 0u;
         a.snap = snap;
         return a;
     }
 
     uint32_t barriers() const { return 5 * (uint32_t)layers.size() - 1; }
-    size_t clock_words() const { return (size_t)(2 + 2 * barriers()) * step_grid; }
+    size_t clock_words() const { return (size_t)(barriers() + 1) * kStepMarks * step_grid; }
 
     double layer_bytes() const {
         double b = 0;
@@ -949,7 +950,11 @@ struct af_session {
     hipError_t enqueue_step(bool with_head) {
         if (use_step) {
             StepArgs a = step_args(!with_head, nullptr);
-            if (timer && clock_used < clock_steps) a.clock = CLOCK.as<uint64_t>() + (size_t)clock_used++ * clock_words();
+            if (timer && clock_used < clock_steps) {
+                a.clock = CLOCK.as<uint64_t>() + (size_t)clock_used++ * clock_words();
+                hipError_t e = hipMemsetAsync(a.clock, 0, clock_words() * 8, stream);  // profiling only
+                if (e != hipSuccess) return e;
+            }
             hipError_t e = timed(K_LAYERS, layer_bytes(), [&] { return launch_step(a, group, step_grid, step_lds, stream); });
             if (e != hipSuccess || !with_head) return e;
             return timed(K_HEAD, (double)head.rows * (head.columns / 256) * 210.0 + 4.0 * 3.0 * hidden,
@@ -1006,8 +1011,10 @@ int setup_step(af_session& s) {
     uint32_t grid = 0;
     HIP_OK(step_max_grid(group, lds, &grid), "step kernel occupancy");
     bool fits = grid >= 8 && s.hidden <= 4096 && s.hidden % 32 == 0;
+    uint32_t kv_max = 1;
+    for (const LayerDev& L : s.layers) kv_max = std::max(kv_max, L.kv_heads);
+    const uint32_t cm = std::min(grid / kv_max, step_merge_chunks(group, lds));
     for (const LayerDev& L : s.layers) {
-        const uint32_t cm = grid / std::max<uint32_t>(L.kv_heads, 1);
         const uint32_t span = L.window ? std::min(L.window, s.capacity) : s.capacity;
         fits = fits && L.q_heads / L.kv_heads == group && L.width == 256 && cm >= 1 && cm <= kStepMaxChunks &&
                (span + cm - 1) / cm <= kStepMaxClen && (L.qkv.rows + 15) / 16 <= kStepMaxUnits * grid &&
@@ -1019,6 +1026,7 @@ int setup_step(af_session& s) {
         return AF_OK;
     }
     s.step_grid = grid;
+    s.step_cmax = cm;
     s.group = group;
     s.step_lds = lds;
     std::vector<StepLayer> table(s.layers.size());
@@ -1063,6 +1071,8 @@ int setup_step(af_session& s) {
     if ((rc = dev_alloc(s.ATT_IMG, att_img, "digit image"))) return rc;
     if ((rc = dev_alloc(s.ACT_IMG, act_img, "digit image"))) return rc;
     if ((rc = dev_alloc(s.BAR, kStepBarBytes, "barrier words"))) return rc;
+    if ((rc = dev_alloc(s.IDLE, 1152, "placeholder tile"))) return rc;
+    HIP_OK(hipMemset(s.IDLE.p, 0, 1152), "placeholder tile clear");
     HIP_OK(hipMemset(s.ATT_IMG.p, 0, att_img), "digit image clear");
     HIP_OK(hipMemset(s.ACT_IMG.p, 0, act_img), "digit image clear");
     HIP_OK(hipMemset(s.BAR.p, 0, kStepBarBytes), "barrier clear");
@@ -1384,33 +1394,77 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
     }
     // Step kernel timelines: a phase runs from its opening barrier's departure (workgroup 0) to
     // the last workgroup's arrival at the closing barrier; the barrier itself from that arrival
-    // to workgroup 0's departure.
+    // to workgroup 0's departure.  "<phase>.<mark>" entries split the slowest workgroup's phase
+    // at its marks (time since its previous mark), and "<phase>.mean" is the mean over
+    // workgroups of their own start-to-arrival time.
+    std::vector<af_kernel_timing> extra;
     if (timed_steps) {
         const size_t words = s->clock_words();
         std::vector<uint64_t> clk((size_t)timed_steps * words);
         HIP_OK(hipMemcpy(clk.data(), s->CLOCK.p, clk.size() * 8, hipMemcpyDeviceToHost), "timeline download");
         const uint32_t G = s->step_grid, nb = s->barriers();
         const double tick_ms = 1e-5;  // 100 MHz
+        static const char* const kMarkNames[kStepMarks] = {"start", "stage", "digits", "stream", "store", "tail", "pre", ""};
+        static const int kOrder[] = {M_START, M_STAGED, M_DIGITS, M_STREAMED, M_STORED, M_PRE, M_ARRIVE};
+        auto entry = [&](const std::string& name) -> af_kernel_timing& {
+            for (auto& t : extra)
+                if (name == t.name) return t;
+            af_kernel_timing t{};
+            std::snprintf(t.name, sizeof(t.name), "%s", name.c_str());
+            extra.push_back(t);
+            return extra.back();
+        };
         for (uint32_t st = 0; st < timed_steps; ++st) {
             const uint64_t* c = clk.data() + (size_t)st * words;
-            auto ev = [&](uint32_t e, uint32_t b) { return c[(size_t)e * G + b]; };
-            auto max_arrive = [&](uint32_t e) {
-                uint64_t m = 0;
-                for (uint32_t b = 0; b < G; ++b) m = std::max(m, ev(e, b));
-                return m;
-            };
-            uint64_t open = ev(0, 0);
-            for (uint32_t k = 0; k <= nb; ++k) {
-                const uint64_t arrive = max_arrive(1 + 2 * k);
-                const int kind = K_QKV + (int)(k % 5);
-                af_kernel_timing& t = timings[kind];
-                t.launches += 1;
-                t.total_ms += (double)(arrive - std::min(arrive, open)) * tick_ms;
-                if (k < nb) {
-                    const uint64_t depart = ev(2 + 2 * k, 0);
+            auto ev = [&](uint32_t ph, int mark, uint32_t b) { return c[((size_t)ph * kStepMarks + mark) * G + b]; };
+            for (uint32_t p = 0; p <= nb; ++p) {
+                uint32_t crit = 0;
+                uint64_t arrive = 0;
+                double mean = 0;
+                for (uint32_t b = 0; b < G; ++b) {
+                    const uint64_t t = ev(p, M_ARRIVE, b);
+                    if (t > arrive) {
+                        arrive = t;
+                        crit = b;
+                    }
+                    const uint64_t t0 = ev(p, M_START, b);
+                    mean += t > t0 ? (double)(t - t0) : 0.0;
+                }
+                const uint64_t open = ev(p, M_START, 0);
+                const int kind = K_QKV + (int)(p % 5);
+                timings[kind].launches += 1;
+                timings[kind].total_ms += (double)(arrive - std::min(arrive, open)) * tick_ms;
+                const std::string base = kKindNames[kind];
+                af_kernel_timing& m = entry(base + ".mean");
+                m.launches += 1;
+                m.total_ms += mean / G * tick_ms;
+                uint64_t prev = ev(p, M_START, crit);
+                for (int mk : kOrder) {
+                    if (mk == M_START) continue;
+                    const uint64_t t = ev(p, mk, crit);
+                    if (!t || t < prev) continue;
+                    af_kernel_timing& e = entry(base + "." + kMarkNames[mk == M_ARRIVE ? 5 : mk]);
+                    e.launches += 1;
+                    e.total_ms += (double)(t - prev) * tick_ms;
+                    prev = t;
+                }
+                // the same split averaged over every workgroup ("<phase>.<mark>~")
+                for (uint32_t b = 0; b < G; ++b) {
+                    uint64_t pv = ev(p, M_START, b);
+                    for (int mk : kOrder) {
+                        if (mk == M_START) continue;
+                        const uint64_t t = ev(p, mk, b);
+                        if (!t || t < pv) continue;
+                        af_kernel_timing& e = entry(base + "." + kMarkNames[mk == M_ARRIVE ? 5 : mk] + "~");
+                        e.launches += 1;
+                        e.total_ms += (double)(t - pv) * tick_ms;
+                        pv = t;
+                    }
+                }
+                if (p < nb) {
+                    const uint64_t depart = ev(p + 1, M_START, 0);
                     timings[K_BARRIER].launches += 1;
                     timings[K_BARRIER].total_ms += (double)(depart - std::min(depart, arrive)) * tick_ms;
-                    open = depart;
                 }
             }
         }
@@ -1423,7 +1477,10 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
     }
     for (int k = 0; k < K_KINDS; ++k)
         if (timings[k].launches) timings[k].bytes_per_launch /= (double)timings[k].launches;
-    *n_timings = K_KINDS;
+    size_t n = K_KINDS;
+    for (const auto& e : extra)
+        if (n < capacity) timings[n++] = e;
+    *n_timings = n;
     return AF_OK;
 }
 

@@ -29,17 +29,63 @@ __device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirs
 __device__ __forceinline__ float h2f(uint16_t b) { return (float)__builtin_bit_cast(_Float16, b); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 
+// Cross-lane exchanges on the DPP path (a VALU operand modifier, a few cycles) instead of
+// ds_bpermute (an LDS round trip per step).  Controls: quad_perm [1,0,3,2] = lane ^ 1,
+// quad_perm [2,3,0,1] = lane ^ 2, row_half_mirror (lane 7 - i within 8), row_mirror (lane
+// 15 - i within 16).  Every lane of the 16-lane row must be active.
+enum DppCtrl { kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140 };
+
+template <int C>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), C, 0xF, 0xF, false));
+}
+template <int C>
+__device__ __forceinline__ double dpp(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, C, 0xF, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), C, 0xF, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sum (max) over each 16-lane row, left in every lane of the row.  After the two quad steps
+// every lane of a quad holds the quad's value, so mirroring pairs each lane with the other
+// quad (half row), then with the other half row.
 template <typename T>
-__device__ __forceinline__ T wave_sum(T v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+__device__ __forceinline__ T row_sum(T v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
+    return v;
+}
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
     return v;
 }
 
+__device__ __forceinline__ float lane_value(float v, int l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ double lane_value(double v, int l) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Sum (max) over the wave (all 64 lanes active), the same value in every lane.
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+    v = row_sum(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+}
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = row_max(v);
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
 // Sum over the block of one double per thread (blockDim a multiple of 64, <= 512).
@@ -107,15 +153,16 @@ __device__ __forceinline__ uint32_t q6_codes(uint32_t a, uint32_t b, uint32_t h,
 
 // ---- input stage: builds the fp32 GEMV input vector in LDS ------------------------------------
 
-// Embedding row (Q6_K, repacked) times emb_scale into xs; one thread per unit dword (16 elements).
-__device__ inline void embed_row(const InputStage& in, float* xs, uint32_t K) {
+// Embedding row (Q6_K, repacked) times emb_scale into xs; one thread per unit dword (16
+// elements), threads first, first + step, ... of the caller's range.
+__device__ inline void embed_row(const InputStage& in, float* xs, uint32_t first, uint32_t step) {
     const Q6View& t = in.table;
     const uint32_t row = min(gp(in.ids)[gp(in.state)[ST_POS]], t.rows - 1);  // ids are validated; never read past the table
     const uint32_t units = t.units, sblocks = units / 4;
     const auto* A = gp(reinterpret_cast<const uint32_t*>(t.a + (size_t)row * units * 16));
     const auto* B = gp(reinterpret_cast<const uint32_t*>(t.b + (size_t)row * units * 16));
     const auto* H = gp(reinterpret_cast<const uint32_t*>(t.h + (size_t)row * units * 16));
-    for (uint32_t w = threadIdx.x; w < units * 4; w += blockDim.x) {
+    for (uint32_t w = first; w < units * 4; w += step) {
         const uint32_t u = w >> 2, k = w & 3;
         const uint32_t sb = u >> 2, g = (u >> 1) & 1, hh = u & 1;
         const uint32_t a = A[w], b = B[w], h = H[w];
@@ -133,7 +180,6 @@ __device__ inline void embed_row(const InputStage& in, float* xs, uint32_t K) {
             }
         }
     }
-    (void)K;
 }
 
 // Loads N float4 per thread from p at float4 indices base + j * blockDim + thread (zero past n4).
@@ -214,7 +260,7 @@ __device__ inline void input_stage(const InputStage& in, float* xs, uint32_t K, 
             }
         }
     } else {  // IN_EMBED
-        embed_row(in, xs, K);
+        embed_row(in, xs, threadIdx.x, blockDim.x);
         __syncthreads();
         for (uint32_t i = tid; i < K4; i += blockDim.x) {
             const float4 v = xs4[i];
@@ -307,10 +353,10 @@ __device__ __forceinline__ void quad_stats(const float (&v)[8], float& m, float&
         mm = fmaxf(mm, fabsf(v[k]));
         ss += v[k];
     }
-    mm = fmaxf(mm, __shfl_xor(mm, 1, 64));
-    mm = fmaxf(mm, __shfl_xor(mm, 2, 64));
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
+    mm = fmaxf(mm, dpp<kDppXor1>(mm));
+    mm = fmaxf(mm, dpp<kDppXor2>(mm));
+    ss += dpp<kDppXor1>(ss);
+    ss += dpp<kDppXor2>(ss);
     m = mm;
     sum = ss;
 }
@@ -401,7 +447,7 @@ __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t n
         } else {
             float t[Q][8];
             if constexpr (IN == IN_EMBED) {
-                embed_row(in, xs, K);
+                embed_row(in, xs, threadIdx.x, blockDim.x);
                 __syncthreads();
 #pragma unroll
                 for (int j = 0; j < Q; ++j) {
@@ -477,16 +523,17 @@ __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t n
 constexpr int kQ4Ahead = 16;  // super-tiles loaded ahead per wave
 
 struct Q4Tile {
-    uint4 code;   // lane (r, g): the 16 code bytes of block g of row r of the super-tile
+    uint4 code;   // lane 16 g + r: the 16 code bytes of block g of row r of the super-tile
     uint2 scale;  // lane (q, n): the fp16 scales of rows 4q..4q+3 for block n / 4
 };
 
 // Loads lane's share of super-tile st of 16-row tile `tile` (tiled layout: codes
-// [tile][st][16 rows][4 blocks][16 bytes], scales [tile][st][4 blocks][16 rows]).
+// [tile][st][4 blocks][16 rows][16 bytes], scales [tile][st][4 blocks][16 rows]).  The code
+// load is lane-linear: each 64-byte line is requested by four consecutive lanes.
 __device__ __forceinline__ void q4_tile_load(const uint4* codes, const uint2* scales, size_t tile, uint32_t nst,
                                              uint32_t st, uint32_t lane, Q4Tile& t) {
     const size_t base = tile * nst + st;
-    t.code = ld_stream(codes + base * 64 + (lane & 15) * 4 + (lane >> 4));
+    t.code = ld_stream(codes + base * 64 + lane);
     t.scale = ld_stream(scales + base * 16 + ((lane & 15) >> 2) * 4 + (lane >> 4));
 }
 
@@ -522,9 +569,7 @@ __device__ __forceinline__ void q4_mfma_tile(const Q4Tile& w, uint32_t st, const
 // Sum of acc over the 16 columns of each row (lanes of a 16-lane group hold one row quad).
 __device__ __forceinline__ void q4_row_sums(float (&acc)[4]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) acc[i] += __shfl_xor(acc[i], o, 16);
+    for (int i = 0; i < 4; ++i) acc[i] = row_sum(acc[i]);
 }
 
 }  // namespace af

@@ -460,8 +460,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
                     float d = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
-#pragma unroll
-                    for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+                    d = row_sum(d);
                     if (j == 0 && t < t1) scores[gi][t - t0] = d * a.scale;
                 }
             }

@@ -42,11 +42,17 @@ constexpr uint32_t kBarAll = 0, kBarExit = 32 * 9;
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
+// The layer table is read through the constant address space: uniform scalar loads.  Through a
+// generic pointer the compiler would use vector loads (it cannot rule out that the kernel's
+// stores alias the table) and wait for every load in flight, weight prefetch included.
+typedef const __attribute__((address_space(4))) StepLayer CLayer;
+typedef const __attribute__((address_space(4))) Q4View CQ4View;
+__device__ __forceinline__ CLayer& layer_at(const StepArgs& a, uint32_t l) {
+    return ((CLayer*)(a.layers))[l];
+}
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), 0, 0x7FFFFFFF, 0x00020000);
-}
-__device__ __forceinline__ uint32_t ldc(const void* base, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(rsrc(base), off, 0, kSC1);
 }
 __device__ __forceinline__ void stc(void* base, uint32_t off, uint32_t v) {
     __builtin_amdgcn_raw_buffer_store_b32(v, rsrc(base), off, 0, kSC1);
@@ -78,8 +84,14 @@ struct Grid {
     uint64_t* clock;  // optional timeline (StepArgs::clock)
 };
 
-__device__ __forceinline__ void stamp(const Grid& g, uint32_t e) {
-    if (g.clock) g.clock[(size_t)e * gridDim.x + blockIdx.x] = wall_clock64();
+// Thread 0 only.  Phase = barriers passed so far.
+__device__ __forceinline__ void stamp_at(const Grid& g, uint32_t phase, uint32_t mark) {
+    if (g.clock) g.clock[((size_t)phase * kStepMarks + mark) * gridDim.x + blockIdx.x] = wall_clock64();
+}
+// Wave 0 stores (every lane the same value to the same word): a branch on the wave index is
+// uniform, where one on the thread index would make the phase loop's control flow divergent.
+__device__ __forceinline__ void stamp(const Grid& g, uint32_t mark) {
+    if (wave_id() == 0) stamp_at(g, g.k, mark);
 }
 
 // All threads call it.  Returns false (in every thread) if the barrier did not complete within
@@ -87,7 +99,7 @@ __device__ __forceinline__ void stamp(const Grid& g, uint32_t e) {
 __device__ __forceinline__ bool grid_sync(Grid& g) {
     __syncthreads();
     if (threadIdx.x == 0) {
-        stamp(g, 1 + 2 * g.k);
+        stamp_at(g, g.k, M_ARRIVE);
         const uint32_t per = gridDim.x / 8, grp = blockIdx.x & 7, k = g.k + 1;
         const uint32_t old =
             __hip_atomic_fetch_add(g.bar + 32 * (1 + grp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -102,11 +114,11 @@ __device__ __forceinline__ bool grid_sync(Grid& g) {
             }
         }
         *g.ok = ok;
-        stamp(g, 2 + 2 * g.k);
+        stamp_at(g, g.k + 1, M_START);
     }
     __syncthreads();
     ++g.k;
-    return *g.ok != 0;
+    return __builtin_amdgcn_readfirstlane(*g.ok) != 0;  // uniform: keeps the phase loop scalar
 }
 
 // Last workgroup out resets the barrier words for the next launch; with `advance` it also moves
@@ -114,7 +126,7 @@ __device__ __forceinline__ bool grid_sync(Grid& g) {
 __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance, bool failed) {
     __syncthreads();
     if (threadIdx.x == 0) {
-        stamp(g, 1 + 2 * g.k);
+        stamp_at(g, g.k, M_ARRIVE);
         if (failed) {
             __hip_atomic_store(state + ST_BAD, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(state + ST_STOP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -160,67 +172,20 @@ __device__ __forceinline__ void cur_next(Cur& c, uint32_t nst, uint32_t T) {
     }
 }
 
-struct Stream {
-    Cur ld, cs;
-    uint32_t fe;
-};
-
 __device__ __forceinline__ uint32_t my_units(uint32_t units) {
     return units > blockIdx.x ? min(kMaxUnits, (units - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0u;
 }
 
-// Issues the lane's loads for the tile at the load cursor and advances it; past the wave's
-// range it loads the first tile of the matrix instead (an L2 hit, never consumed), so every
-// call issues the same number of loads and the compiler can wait for exactly the slot in use.
-__device__ __forceinline__ void job_issue(const Job& j, Stream& s, uint32_t lane, Q4Tile& t) {
-    const bool real = s.ld.f < s.fe;
-    const uint32_t unit = blockIdx.x + s.ld.k * gridDim.x;
-    const uint32_t m = j.T == 4 ? s.ld.ts >> 1 : 0u;
-    const size_t tile = !real ? 0 : j.T == 4 ? (size_t)unit * 2 + (s.ld.ts & 1) : (size_t)unit;
-    const uint4* codes = real && m ? j.codes[1] : j.codes[0];
-    const uint2* scales = real && m ? j.scales[1] : j.scales[0];
-    q4_tile_load(codes, scales, tile, j.nst, real ? s.ld.st : 0u, lane, t);
-    if (real) cur_next(s.ld, j.nst, j.T);
-}
-
-// Streaming waves: position the cursors and issue the first kAhead tile loads.
-__device__ __forceinline__ void job_prefetch(const Job& j, Stream& s, Q4Tile (&buf)[kAhead], uint32_t wave,
-                                             uint32_t lane) {
+// This streaming wave's share [fb, fe) of a job's flattened super-tiles.
+__device__ __forceinline__ void wave_share(const Job& j, uint32_t wave, uint32_t& fb, uint32_t& fe) {
     const uint32_t F = my_units(j.units) * j.T * j.nst, w = wave - 1;
-    const uint32_t fb = (uint32_t)(((uint64_t)F * w) / kStreamWaves);
-    s.fe = (uint32_t)(((uint64_t)F * (w + 1)) / kStreamWaves);
-    s.ld = cur_at(fb, j.nst, j.T);
-    s.cs = s.ld;
-#pragma unroll
-    for (int u = 0; u < kAhead; ++u) job_issue(j, s, lane, buf[u]);
+    // wave-uniform values: readfirstlane keeps the cursors (and all control flow on them) scalar
+    fb = __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)F * w) / kStreamWaves));
+    fe = __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)F * (w + 1)) / kStreamWaves));
 }
 
-// part[(k * kMaxT + ts) * 8 + wave][16]: one wave's row sums of one tile.  Slot u of the ring
-// holds tile fb + u (mod kAhead); each consumed slot is refilled at once.
-__device__ __forceinline__ void job_stream(const Job& j, Stream& s, Q4Tile (&buf)[kAhead], const int8_t* dig,
-                                           const DigitTab* tab, float* part, uint32_t wave, uint32_t lane) {
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    const uint32_t n = s.fe - s.cs.f;
-    for (uint32_t base = 0; base < n; base += kAhead) {
-#pragma unroll
-        for (int u = 0; u < kAhead; ++u) {
-            if (base + u < n) {
-                q4_mfma_tile(buf[u], s.cs.st, dig, tab, lane, acc);
-                if (s.cs.st == j.nst - 1 || s.cs.f + 1 == s.fe) {
-                    q4_row_sums(acc);
-                    if ((lane & 15) == 0) {
-                        float* p = part + ((s.cs.k * kMaxT + s.cs.ts) * 8 + wave) * 16 + 4 * (lane >> 4);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) p[i] = acc[i];
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
-                }
-                cur_next(s.cs, j.nst, j.T);
-            }
-            job_issue(j, s, lane, buf[u]);
-        }
-    }
+__device__ __forceinline__ void zero_part_lds(float* part, uint32_t tid) {
+    for (uint32_t i = tid; i < kMaxUnits * kMaxT * 8 * 16; i += kThreads) part[i] = 0.0f;
 }
 
 __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_t ts, uint32_t r) {
@@ -243,26 +208,46 @@ struct Stage {
     float* snap;          // optional copy of x_out
 };
 
-__device__ __forceinline__ void stage_inputs(int kind, const Stage& in, uint32_t K, uint32_t nst, uint8_t* lds, uint32_t lane) {
+// Wave 0, after the barrier: the activation inputs (the norm weights are already in LDS), or
+// the embedding row of the step's token.
+__device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const InputStage& emb, uint32_t K, uint32_t nst,
+                                             uint8_t* lds, uint32_t lane) {
     uint8_t* img = lds;
     float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
-    const uint32_t kb = K * 4;
     if (kind == S_DIGITS) {
         dma(in.dig, nst * 640, img, lane);
+    } else if (kind == S_RESID) {
+        dma(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), lane);
+        dma(in.res, K * 4, reinterpret_cast<uint8_t*>(xs + K), lane);
     } else {
-        if (kind == S_RESID) {
-            dma(in.x, kb, reinterpret_cast<uint8_t*>(xs), lane);
-            dma(in.res, kb, reinterpret_cast<uint8_t*>(xs + K), lane);
-            if (in.w_a) dma(in.w_a, kb, reinterpret_cast<uint8_t*>(xs + 2 * K), lane);
-        }
-        dma(in.w_n, kb, reinterpret_cast<uint8_t*>(xs + 3 * K), lane);
+        embed_row(emb, xs, lane, 64);
     }
     wait_vm();
 }
 
-// Digit image of the normalised input (K <= 4096, so one octet per thread).
-__device__ __forceinline__ void stage_digits(int kind, const Stage& in, const InputStage& emb, uint32_t K, uint32_t nst, uint8_t* lds,
-                             double* red) {
+// Wave 0: the norm weights (constant) of a residual prologue into their LDS slots.
+__device__ __forceinline__ void preload_norms(const float* w_a, const float* w_n, uint32_t K, uint32_t nst, uint8_t* lds,
+                                              uint32_t lane) {
+    float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
+    if (w_a) dma(w_a, K * 4, reinterpret_cast<uint8_t*>(xs + 2 * K), lane);
+    dma(w_n, K * 4, reinterpret_cast<uint8_t*>(xs + 3 * K), lane);
+}
+
+// Wave 0 of workgroup 0: the residual left in xs[0, K) by stage_digits.
+__device__ __forceinline__ void store_residual(const Stage& in, const uint8_t* lds, uint32_t K, uint32_t nst,
+                                               uint32_t lane) {
+    const v4u* xs = reinterpret_cast<const v4u*>(lds + (size_t)nst * 640);
+    for (uint32_t i = lane; i < K / 4; i += 64) {
+        const v4u v = xs[i];
+        stc16(in.x_out, i * 16, v);
+        if (in.snap) stc16(in.snap, i * 16, v);
+    }
+}
+
+// Digit image of the normalised input (K <= 4096, so one octet per thread), all threads, from
+// LDS only.  The residual sum replaces x in xs[0, K) for store_residual.
+__device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t K, uint32_t nst, uint8_t* lds,
+                                             double* red) {
     int8_t* dig = reinterpret_cast<int8_t*>(lds);
     DigitTab* tab = reinterpret_cast<DigitTab*>(lds + (size_t)nst * 512);
     float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
@@ -270,8 +255,6 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, const In
     const bool ok = o < n8;
     float t[8], v[8];
     if (kind == S_EMBED) {
-        embed_row(emb, xs, K);
-        __syncthreads();
 #pragma unroll
         for (int k = 0; k < 8; ++k) t[k] = ok ? xs[8 * o + k] : 0.0f;
     } else {
@@ -290,6 +273,7 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, const In
                 const float x = xs[8 * o + k], r = xs[K + 8 * o + k];
                 const float u = in.w_a ? norm_apply(x, ra, xs[2 * K + 8 * o + k]) : x;
                 t[k] = __fmul_rn(__fadd_rn(u, r), in.scale);
+                xs[8 * o + k] = t[k];
             } else {
                 t[k] = 0.0f;
             }
@@ -298,16 +282,6 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, const In
     double ss = 0.0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) ss += (double)t[k] * t[k];
-    if (blockIdx.x == 0 && ok) {
-        const v4u a = {__float_as_uint(t[0]), __float_as_uint(t[1]), __float_as_uint(t[2]), __float_as_uint(t[3])};
-        const v4u b = {__float_as_uint(t[4]), __float_as_uint(t[5]), __float_as_uint(t[6]), __float_as_uint(t[7])};
-        stc16(in.x_out, o * 32, a);
-        stc16(in.x_out, o * 32 + 16, b);
-        if (in.snap) {
-            stc16(in.snap, o * 32, a);
-            stc16(in.snap, o * 32 + 16, b);
-        }
-    }
     const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
 #pragma unroll
     for (int k = 0; k < 8; ++k) v[k] = ok ? norm_apply(t[k], rn, xs[3 * K + 8 * o + k]) : 0.0f;
@@ -344,37 +318,128 @@ __device__ __forceinline__ void quad_digits_store(const float (&v)[8], int8_t* i
 
 // ---- attention phase ------------------------------------------------------------------------------
 
-// Work item (KV head h, chunk c) of the visible range runs on workgroup h * chunks + c with all
-// 512 threads; the last chunk of a head to finish merges the head's partials and writes the
-// digit image of its query heads' outputs for the o-proj GEMV.
+// Work item (KV head h, chunk c) of the visible range runs with all 512 threads; the last chunk
+// of a head to finish merges the head's partials and writes the digit image of its query heads'
+// outputs for the o-proj GEMV.  Chunks of at most stage_clen tokens have their cached K and V
+// rows staged in LDS before the barrier that opens the attention phase.
 template <int GQ>
-__device__ __forceinline__ void attention_item(const StepLayer& L, const StepArgs& a, uint32_t pos, uint32_t h, uint32_t c,
-                               uint32_t chunks, uint32_t cmax, uint32_t clen, uint32_t start, uint8_t* lds) {
+constexpr uint32_t stage_clen() {
+    return GQ == 4 ? 32u : 64u;
+}
+
+// LDS of an attention item.  The "pre" part (RoPE angles, q/k norm weights, staged K/V rows) is
+// written by wave 0 while the qkv phase streams its weights, so it lies above that phase's
+// digit image; the "transient" part is written after the barrier.  The merge reuses the space
+// from offset 0: the head's chunk partials, then the merged outputs.
+template <int GQ>
+struct AttnLds {
+    static constexpr int D = 256, NH = GQ + 2;
+    // transient
+    float* nrm;       // [NH][D] q heads, k, v of the new token (raw, then normalised)
+    float* qs;        // [GQ][D] rotated queries
+    float* scores;    // [GQ][kStepMaxClen]
+    float* vred;      // [16][GQ][D]
+    double* dred;     // [8][NH]
+    float* fred;      // [8]
+    uint16_t* knew;   // [D] new K row (fp16)
+    uint16_t* vnew;   // [D] new V row (fp16)
+    // pre
+    double* rope;     // cos [128], sin [128] of pos * inv_freq
+    float* qnw;       // [D] q_norm weights
+    float* knw;       // [D] k_norm weights
+    uint16_t* kst;    // [stage_clen][D] fp16 K rows of the chunk
+    uint16_t* vst;    // [stage_clen][D] fp16 V rows
+    static constexpr size_t transient_bytes() {
+        return 4 * (NH * D + GQ * D + GQ * kStepMaxClen + 16 * GQ * D) + 8 * 8 * NH + 4 * 8 + 2 * 2 * D;
+    }
+    static constexpr size_t pre_offset() { return (transient_bytes() + 255) / 256 * 256; }
+    static constexpr size_t bytes() { return pre_offset() + 8 * 256 + 4 * 2 * D + 2 * 2 * stage_clen<GQ>() * D; }
+    __device__ explicit AttnLds(uint8_t* lds) {
+        nrm = reinterpret_cast<float*>(lds);
+        qs = nrm + NH * D;
+        scores = qs + GQ * D;
+        vred = scores + GQ * kStepMaxClen;
+        dred = reinterpret_cast<double*>(vred + 16 * GQ * D);
+        fred = reinterpret_cast<float*>(dred + 8 * NH);
+        knew = reinterpret_cast<uint16_t*>(fred + 8);
+        vnew = knew + D;
+        rope = reinterpret_cast<double*>(lds + pre_offset());
+        qnw = reinterpret_cast<float*>(rope + 256);
+        knw = qnw + D;
+        kst = reinterpret_cast<uint16_t*>(knw + D);
+        vst = kst + stage_clen<GQ>() * D;
+    }
+};
+
+// Wave 0, while the qkv phase streams (nothing here depends on this step's q, k, v): the RoPE
+// angles, the q/k norm weights and the chunk's cached K and V rows, into the "pre" LDS part.
+template <int GQ>
+__device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t h, uint32_t c, uint32_t clen,
+                                              uint32_t start, uint8_t* lds, uint32_t lane) {
+    AttnLds<GQ> m(lds);
+    const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
+    dma(L.q_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.qnw), lane);
+    dma(L.k_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.knw), lane);
+    if (clen <= stage_clen<GQ>()) {
+        const uint32_t old_end = min(t1, pos);  // the new token's row is computed in the phase
+        for (uint32_t t = t0; t < old_end; t += 2) {  // two 512-byte rows per wave instruction
+            const uint32_t row = t + (lane >> 5);
+            if (row < old_end) {
+                const size_t src = ((size_t)h * L.ring + row % L.ring) * 256 + (lane & 31) * 8;
+                __builtin_amdgcn_global_load_lds(L.kcache + src, (lds_ptr)(m.kst + (t - t0) * 256), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds(L.vcache + src, (lds_ptr)(m.vst + (t - t0) * 256), 16, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t f = lane + 64 * i;
+        double sn, cs;
+        sincos((double)pos * gp(L.inv_freq)[f], &sn, &cs);
+        m.rope[f] = cs;
+        m.rope[128 + f] = sn;
+    }
+    wait_vm();
+}
+
+// One attention item.  Only wave 0 touches global memory (the streaming waves' weight loads stay
+// in flight), except for chunks too long to stage, whose K/V rows every wave reads directly.
+template <int GQ>
+__device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uint32_t pos, uint32_t h, uint32_t c,
+                                               uint32_t chunks, uint32_t cmax, uint32_t clen, uint32_t start,
+                                               uint8_t* lds, int* flag) {
     constexpr int D = 256, NH = GQ + 2;
-    float* nrm = reinterpret_cast<float*>(lds);  // [NH][D]
-    float* qs = nrm + NH * D;                     // [GQ][D]
-    float* scores = qs + GQ * D;                  // [GQ][kStepMaxClen]
-    float* vred = scores + GQ * kStepMaxClen;     // [16][GQ][D]
-    double* dred = reinterpret_cast<double*>(vred + 16 * GQ * D);  // [8][NH]
-    float* fred = reinterpret_cast<float*>(dred + 8 * NH);         // [8]
-    float* cw = fred + 8;                                          // [GQ][kStepMaxChunks] (merge)
-    float* cl = cw + GQ * kStepMaxChunks;                          // [GQ][kStepMaxChunks]
-    int* flag = reinterpret_cast<int*>(cl + GQ * kStepMaxChunks);
+    AttnLds<GQ> sh(lds);
+    float* nrm = sh.nrm;
+    float* qs = sh.qs;
+    float* scores = sh.scores;
+    float* vred = sh.vred;
+    double* dred = sh.dred;
+    float* fred = sh.fred;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen), n = t1 - t0;
     const uint32_t ring = L.ring;
     const bool append = t1 == pos + 1;
     const bool ch = tid < D;
+    const bool staged = clen <= stage_clen<GQ>();
 
-    // prologue: RMSNorm of the query heads (and the new K, V), NeoX RoPE, K/V append
+    // this token's query heads (and k, v when the chunk ends at it), computed by the qkv phase
+    if (wave == 0) {
+        dma(a.QKV + (size_t)h * GQ * D, 4 * GQ * D, reinterpret_cast<uint8_t*>(nrm), lane);
+        if (append) {
+            dma(a.QKV + L.qn + h * D, 4 * D, reinterpret_cast<uint8_t*>(nrm + GQ * D), lane);
+            dma(a.QKV + L.v_off + h * D, 4 * D, reinterpret_cast<uint8_t*>(nrm + (GQ + 1) * D), lane);
+        }
+        wait_vm();
+    }
+    __syncthreads();
+
+    // prologue: RMSNorm of the query heads (and the new K, V), NeoX RoPE
     float raw[NH];
 #pragma unroll
-    for (int q = 0; q < GQ; ++q) raw[q] = ch ? __uint_as_float(ldc(a.QKV, ((h * GQ + q) * D + tid) * 4)) : 0.0f;
-    raw[GQ] = ch && append ? __uint_as_float(ldc(a.QKV, (L.qn + h * D + tid) * 4)) : 0.0f;
-    raw[GQ + 1] = ch && append ? __uint_as_float(ldc(a.QKV, (L.v_off + h * D + tid) * 4)) : 0.0f;
-    double sn = 0.0, cs = 1.0;
-    if (tid < D / 2) sincos((double)pos * gp(L.inv_freq)[tid], &sn, &cs);
+    for (int q = 0; q < NH; ++q) raw[q] = ch && (q < GQ || append) ? nrm[q * D + tid] : 0.0f;
+    const double cs = tid < D / 2 ? sh.rope[tid] : 1.0, sn = tid < D / 2 ? sh.rope[128 + tid] : 0.0;
 #pragma unroll
     for (int q = 0; q < NH; ++q) {
         const double v = wave_sum((double)raw[q] * (double)raw[q]);
@@ -387,14 +452,13 @@ __device__ __forceinline__ void attention_item(const StepLayer& L, const StepArg
             if (q >= GQ && !append) break;
             const double ss = (dred[0 * NH + q] + dred[1 * NH + q]) + (dred[2 * NH + q] + dred[3 * NH + q]);
             float r;
-            if (q < GQ) r = norm_apply(raw[q], inv_rms(ss, D, L.q_eps), gp(L.q_norm)[tid]);
-            else if (q == GQ) r = norm_apply(raw[q], inv_rms(ss, D, L.k_eps), gp(L.k_norm)[tid]);
+            if (q < GQ) r = norm_apply(raw[q], inv_rms(ss, D, L.q_eps), sh.qnw[tid]);
+            else if (q == GQ) r = norm_apply(raw[q], inv_rms(ss, D, L.k_eps), sh.knw[tid]);
             else r = L.v_norm ? (float)__dmul_rn((double)raw[q], inv_rms(ss, D, L.v_eps)) : raw[q];
             nrm[q * D + tid] = r;
         }
     }
     __syncthreads();
-    const size_t slot = ((size_t)h * ring + pos % ring) * D;
     if (tid < D / 2) {
 #pragma unroll
         for (int q = 0; q < GQ + 1; ++q) {
@@ -406,26 +470,48 @@ __device__ __forceinline__ void attention_item(const StepLayer& L, const StepArg
                 qs[q * D + tid] = r0;
                 qs[q * D + tid + D / 2] = r1;
             } else {
-                gp(L.kcache)[slot + tid] = f2h(r0);
-                gp(L.kcache)[slot + tid + D / 2] = f2h(r1);
+                const uint16_t k0 = f2h(r0), k1 = f2h(r1);
+                sh.knew[tid] = k0;
+                sh.knew[tid + D / 2] = k1;
+                if (staged) {
+                    sh.kst[(pos - t0) * D + tid] = k0;
+                    sh.kst[(pos - t0) * D + tid + D / 2] = k1;
+                }
             }
         }
     }
-    if (append && ch) gp(L.vcache)[slot + tid] = f2h(nrm[(GQ + 1) * D + tid]);
+    if (append && ch) {
+        const uint16_t v = f2h(nrm[(GQ + 1) * D + tid]);
+        sh.vnew[tid] = v;
+        if (staged) sh.vst[(pos - t0) * D + tid] = v;
+    }
     __syncthreads();
+    // the new K/V rows into the cache (read back by later steps only: this step reads them from LDS)
+    const size_t slot = ((size_t)h * ring + pos % ring) * D;
+    if (append && wave == 0) {
+        const v2u* kn = reinterpret_cast<const v2u*>(sh.knew);
+        const v2u* vn = reinterpret_cast<const v2u*>(sh.vnew);
+        *gp(reinterpret_cast<v2u*>(L.kcache + slot) + lane) = kn[lane];
+        *gp(reinterpret_cast<v2u*>(L.vcache + slot) + lane) = vn[lane];
+        wait_vm();
+    }
 
-    // scores: 16 lanes per token (16 channels each), 32 token groups
+    // scores: 16 lanes per token (16 channels each), 32 token groups; q is re-read from LDS for
+    // every token (registers stay free for the weight loads in flight)
     {
         const uint32_t grp = tid >> 4, j = tid & 15;
-        float qr[GQ][16];
-#pragma unroll
-        for (int q = 0; q < GQ; ++q)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) qr[q][e] = qs[q * D + 16 * j + e];
         for (uint32_t t = t0 + grp; t < t1; t += 32) {
-            const uint16_t* kp = L.kcache + ((size_t)h * ring + t % ring) * D + 16 * j;
-            const v4u k0 = *gp(reinterpret_cast<const v4u*>(kp));
-            const v4u k1 = *gp(reinterpret_cast<const v4u*>(kp + 8));
+            v4u k0, k1;
+            if (staged || t == pos) {
+                const uint16_t* kr = staged ? sh.kst + (t - t0) * D : sh.knew;
+                const v4u* kp = reinterpret_cast<const v4u*>(kr + 16 * j);
+                k0 = kp[0];
+                k1 = kp[1];
+            } else {
+                const uint16_t* kp = L.kcache + ((size_t)h * ring + t % ring) * D + 16 * j;
+                k0 = *gp(reinterpret_cast<const v4u*>(kp));
+                k1 = *gp(reinterpret_cast<const v4u*>(kp + 8));
+            }
             const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
             float kf[16];
 #pragma unroll
@@ -435,11 +521,17 @@ __device__ __forceinline__ void attention_item(const StepLayer& L, const StepArg
             }
 #pragma unroll
             for (int q = 0; q < GQ; ++q) {
+                const float4* qp = reinterpret_cast<const float4*>(qs + q * D + 16 * j);
                 float d = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) d = fmaf(qr[q][e], kf[e], d);
-#pragma unroll
-                for (int o = 8; o > 0; o >>= 1) d += __shfl_xor(d, o, 16);
+                for (int e4 = 0; e4 < 4; ++e4) {
+                    const float4 qv = qp[e4];
+                    d = fmaf(qv.x, kf[4 * e4], d);
+                    d = fmaf(qv.y, kf[4 * e4 + 1], d);
+                    d = fmaf(qv.z, kf[4 * e4 + 2], d);
+                    d = fmaf(qv.w, kf[4 * e4 + 3], d);
+                }
+                d = row_sum(d);
                 if (j == 0) scores[q * kStepMaxClen + (t - t0)] = d * L.scale;
             }
         }
@@ -471,7 +563,13 @@ __device__ __forceinline__ void attention_item(const StepLayer& L, const StepArg
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
         for (uint32_t t = t0 + tg; t < t1; t += 16) {
-            const v4u vv = *gp(reinterpret_cast<const v4u*>(L.vcache + ((size_t)h * ring + t % ring) * D + 8 * dl));
+            v4u vv;
+            if (staged || t == pos) {
+                const uint16_t* vr = staged ? sh.vst + (t - t0) * D : sh.vnew;
+                vv = *reinterpret_cast<const v4u*>(vr + 8 * dl);
+            } else {
+                vv = *gp(reinterpret_cast<const v4u*>(L.vcache + ((size_t)h * ring + t % ring) * D + 8 * dl));
+            }
             const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
             float vf[8];
 #pragma unroll
@@ -493,289 +591,445 @@ __device__ __forceinline__ void attention_item(const StepLayer& L, const StepArg
     }
     __syncthreads();
 
-    // chunk partial: o[q][d] (unnormalised), m[q], l[q]
+    // chunk partial o[q][d] (unnormalised), m[q], l[q], staged in LDS and stored by wave 0
     const uint32_t stride = GQ * (D + 2);
-    const uint32_t mine = ((h * cmax + c) * stride) * 4;
+    float* pst = scores;  // [GQ][D + 2]; the scores are no longer needed
     for (uint32_t i = tid; i < GQ * D; i += kThreads) {
         const uint32_t q = i / D, d = i % D;
         float t = 0.0f;
 #pragma unroll
         for (int g = 0; g < 16; ++g) t += vred[(g * GQ + q) * D + d];
-        stc(a.part, mine + (q * (D + 2) + d) * 4, __float_as_uint(t));
+        pst[q * (D + 2) + d] = t;
     }
     if (tid < GQ) {
 #pragma unroll
         for (int q = 0; q < GQ; ++q) {
             if ((uint32_t)q == tid) {
-                stc(a.part, mine + (q * (D + 2) + D) * 4, __float_as_uint(m[q]));
-                stc(a.part, mine + (q * (D + 2) + D + 1) * 4, __float_as_uint(l[q]));
+                pst[q * (D + 2) + D] = m[q];
+                pst[q * (D + 2) + D + 1] = l[q];
             }
         }
     }
-    wait_vm();
     __syncthreads();
-    if (tid == 0) {
-        const uint32_t ticket =
-            __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        *flag = ticket == chunks - 1;
+    float* const head_part = a.part + (size_t)h * cmax * stride;
+    if (wave == 0) {
+        for (uint32_t i = lane; i < stride; i += 64) stc(head_part, (c * stride + i) * 4, __float_as_uint(pst[i]));
+        wait_vm();
+        if (lane == 0) {
+            const uint32_t ticket =
+                __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *flag = ticket == chunks - 1;
+        }
+        wait_vm();
     }
     __syncthreads();
-    if (!*flag) return;
+    if (!__builtin_amdgcn_readfirstlane(*flag)) return;
 
-    // merge (last chunk of this head): weights exp(m_c - M), output sum_c w_c o_c / sum_c w_c l_c
-    const uint32_t all = (h * cmax * stride) * 4;
-    for (uint32_t i = tid; i < chunks * GQ; i += kThreads) {
-        const uint32_t k = i / GQ, q = i % GQ;
-        cw[q * kStepMaxChunks + k] = __uint_as_float(ldc(a.part, all + (k * stride + q * (D + 2) + D) * 4));
-        cl[q * kStepMaxChunks + k] = __uint_as_float(ldc(a.part, all + (k * stride + q * (D + 2) + D + 1) * 4));
+    // merge (last chunk of this head): M = max_c m_c, w_c = exp(m_c - M), output
+    // sum_c w_c o_c / sum_c w_c l_c, in chunk order
+    float* mrg = reinterpret_cast<float*>(lds);  // [chunks][stride]
+    float* outv = mrg + chunks * stride;        // [GQ][D]
+    if (wave == 0) {
+        dma(head_part, chunks * stride * 4, lds, lane);
+        wait_vm();
     }
     __syncthreads();
-    float M[GQ];
-#pragma unroll
-    for (int q = 0; q < GQ; ++q) {
-        M[q] = -INFINITY;
-        for (uint32_t k = 0; k < chunks; ++k) M[q] = fmaxf(M[q], cw[q * kStepMaxChunks + k]);
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < chunks * GQ; i += kThreads) {
-        const uint32_t k = i / GQ, q = i % GQ;
-        cw[q * kStepMaxChunks + k] = expf(cw[q * kStepMaxChunks + k] - M[q]);
-    }
-    __syncthreads();
-    float* outv = vred;  // [GQ][D]
     for (uint32_t i = tid; i < GQ * D; i += kThreads) {
         const uint32_t q = i / D, d = i % D;
+        float M = -INFINITY;
+        for (uint32_t k = 0; k < chunks; ++k) M = fmaxf(M, mrg[k * stride + q * (D + 2) + D]);
         float Lq = 0.0f, acc = 0.0f;
         for (uint32_t k = 0; k < chunks; ++k) {
-            const float w = cw[q * kStepMaxChunks + k];
-            Lq = fmaf(w, cl[q * kStepMaxChunks + k], Lq);
-            acc = fmaf(w, __uint_as_float(ldc(a.part, all + (k * stride + q * (D + 2) + d) * 4)), acc);
+            const float* pk = mrg + k * stride + q * (D + 2);
+            const float w = expf(pk[D] - M);
+            Lq = fmaf(w, pk[D + 1], Lq);
+            acc = fmaf(w, pk[d], acc);
         }
         outv[i] = acc / Lq;
     }
     __syncthreads();
-    // digit image blocks (h GQ + q) * 8 + b of the o-proj input: 4 threads per block
+    // digit image blocks (h GQ + q) * 8 + b of the o-proj input: 4 lanes of wave 0 per block
     const uint32_t nst_att = L.o.nst;
-    if (tid < 32 * GQ) {
-        const uint32_t blk = tid >> 2, p = tid & 3;
-        float v[8];
+    if (wave == 0) {
+        for (uint32_t base = 0; base < 32 * GQ; base += 64) {
+            const uint32_t i = base + lane;
+            if (i < 32 * GQ) {
+                const uint32_t blk = i >> 2, p = i & 3;
+                float v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = outv[blk * 32 + 8 * p + k];
-        quad_digits_store(v, a.att_img, nst_att, h * GQ * 8 + blk, p);
+                for (int k = 0; k < 8; ++k) v[k] = outv[blk * 32 + 8 * p + k];
+                quad_digits_store(v, a.att_img, nst_att, h * GQ * 8 + blk, p);
+            }
+        }
+        if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vm();
     }
-    if (tid == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- the kernel -----------------------------------------------------------------------------------
+
+// Phases of a layer, in order.
+enum PhaseKind { P_QKV = 0, P_ATTN, P_OPROJ, P_GATEUP, P_DOWN, kPhases };
+
+// One GEMV phase of a layer, read from the layer table.
+struct Gemv {
+    Job job;
+    int in_kind;     // S_EMBED, S_RESID or S_DIGITS
+    Stage in;
+    InputStage emb;  // S_EMBED
+    uint32_t K;      // input width
+    float* y;        // outputs (null for gate/up, whose output is the down input's digit image)
+    uint32_t rows;
+    uint32_t act_nst;
+};
+
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ Job make_job(CQ4View& m0, CQ4View* m1) {
+    Job j{};
+    j.codes[0] = reinterpret_cast<const uint4*>(m0.codes);
+    j.scales[0] = reinterpret_cast<const uint2*>(m0.scales);
+    if (m1) {
+        j.codes[1] = reinterpret_cast<const uint4*>(m1->codes);
+        j.scales[1] = reinterpret_cast<const uint2*>(m1->scales);
+        j.units = (m0.rows + 31) / 32;
+        j.T = 4;
+    } else {
+        j.codes[1] = j.codes[0];
+        j.scales[1] = j.scales[0];
+        j.units = (m0.rows + 15) / 16;
+        j.T = 1;
+    }
+    j.nst = m0.nst;
+    // every field is wave-uniform; readfirstlane puts the job in scalar registers so the stream
+    // cursors derived from it, and the branches on them, stay scalar
+    for (int i = 0; i < 2; ++i) {
+        j.codes[i] = reinterpret_cast<const uint4*>(uniform_ptr(j.codes[i]));
+        j.scales[i] = reinterpret_cast<const uint2*>(uniform_ptr(j.scales[i]));
+    }
+    j.units = __builtin_amdgcn_readfirstlane(j.units);
+    j.T = __builtin_amdgcn_readfirstlane(j.T);
+    j.nst = __builtin_amdgcn_readfirstlane(j.nst);
+    return j;
+}
+
+__device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t kind) {
+    CLayer& L = layer_at(a, l);
+    Gemv d{};
+    if (kind == P_QKV) {
+        d.job = make_job(L.qkv, nullptr);
+        d.K = a.hidden;
+        d.y = a.QKV;
+        d.rows = L.qkv.rows;
+        if (l == 0) {
+            d.in_kind = S_EMBED;
+            d.emb.table = a.table;
+            d.emb.ids = a.ids;
+            d.emb.state = a.state;
+            d.emb.emb_scale = a.emb_scale;
+        } else {
+            CLayer& P = layer_at(a, l - 1);
+            d.in_kind = S_RESID;
+            d.in.x = a.D;
+            d.in.res = a.H;
+            d.in.w_a = P.post_ffn;
+            d.in.eps_a = P.post_ffn_eps;
+            d.in.scale = P.layer_scale;
+            d.in.snap = a.snap ? a.snap + (size_t)(l - 1) * a.hidden : nullptr;
+        }
+        d.in.w_n = L.input_norm;
+        d.in.eps_n = L.input_eps;
+        d.in.x_out = a.X;
+    } else if (kind == P_OPROJ) {
+        d.job = make_job(L.o, nullptr);
+        d.in_kind = S_DIGITS;
+        d.in.dig = a.att_img;
+        d.K = L.o.blocks * 32;
+        d.y = a.PROJ;
+        d.rows = L.o.rows;
+    } else if (kind == P_GATEUP) {
+        d.job = make_job(L.gate, &L.up);
+        d.in_kind = S_RESID;
+        d.in.x = a.PROJ;
+        d.in.res = a.X;
+        d.in.w_a = L.post_attn;
+        d.in.eps_a = L.post_attn_eps;
+        d.in.scale = 1.0f;
+        d.in.w_n = L.ffn_norm;
+        d.in.eps_n = L.ffn_eps;
+        d.in.x_out = a.H;
+        d.K = a.hidden;
+        d.act_nst = L.down.nst;
+    } else {
+        d.job = make_job(L.down, nullptr);
+        d.in_kind = S_DIGITS;
+        d.in.dig = a.act_img;
+        d.K = a.inter;
+        d.y = a.D;
+        d.rows = L.down.rows;
+    }
+    return d;
+}
+
+// Attention work of a layer at position pos: chunks of at least kAttnMinChunk tokens, at most
+// grid / kv_heads per KV head; item i runs on workgroup grid - 1 - i.
+struct AttnGeo {
+    uint32_t start, chunks, clen, cmax, items;
+};
+
+__device__ __forceinline__ AttnGeo attn_geo(CLayer& L, uint32_t pos, uint32_t cmax) {
+    AttnGeo g;
+    const uint32_t nvis = L.window ? min(pos + 1, L.window) : pos + 1;
+    g.start = pos + 1 - nvis;
+    g.cmax = cmax;
+    uint32_t chunks = min(g.cmax, (nvis + kAttnMinChunk - 1) / kAttnMinChunk);
+    g.clen = (nvis + chunks - 1) / chunks;
+    g.chunks = (nvis + g.clen - 1) / g.clen;
+    g.items = L.kv_heads * g.chunks;
+    return g;
+}
+
+// The job of GEMV phase ph.
+__device__ __forceinline__ Job phase_job(const StepArgs& a, uint32_t ph) {
+    ph = __builtin_amdgcn_readfirstlane(ph);  // wave-uniform by construction; say so
+    CLayer& L = layer_at(a, ph / kPhases);
+    const uint32_t kind = ph % kPhases;
+    if (kind == P_QKV) return make_job(L.qkv, nullptr);
+    if (kind == P_OPROJ) return make_job(L.o, nullptr);
+    if (kind == P_GATEUP) return make_job(L.gate, &L.up);
+    return make_job(L.down, nullptr);
+}
+
+// A streaming wave's weight stream over the whole step: its share of every GEMV phase in order,
+// each share padded with placeholder tiles to a multiple of kAhead so that every phase starts
+// in ring slot 0.  Ring slot u holds stream tile u mod kAhead; a consumed slot is refilled at
+// once with the tile kAhead further on, across phase boundaries, so the next phase's first
+// tiles are in flight while this one finishes and the ring never drains inside the launch.
+struct Ring {
+    Job job;       // the phase being loaded
+    Cur ld;        // its next tile
+    uint32_t fe;   // end of this wave's share
+    uint32_t pad;  // placeholders still to issue after the share
+    int32_t ph;    // the phase (n_phases once every phase is issued)
+};
+
+__device__ __forceinline__ void ring_seek(const StepArgs& a, Ring& r, int32_t ph, int32_t n_phases, uint32_t wave) {
+    for (; ph < n_phases; ++ph) {
+        if ((uint32_t)ph % kPhases == P_ATTN) continue;
+        r.job = phase_job(a, (uint32_t)ph);
+        uint32_t fb;
+        wave_share(r.job, wave, fb, r.fe);
+        if (fb < r.fe) {
+            r.ld = cur_at(fb, r.job.nst, r.job.T);
+            r.pad = (kAhead - (r.fe - fb) % kAhead) % kAhead;
+            r.ph = __builtin_amdgcn_readfirstlane(ph);
+            return;
+        }
+    }
+    r.ph = n_phases;
+    r.pad = 0;
+}
+
+// Shares are padded to multiples of kAhead and the loads run exactly kAhead tiles ahead, so a
+// round of kAhead refills never crosses a phase boundary: the next phase is sought once per round.
+__device__ __forceinline__ void ring_round(const StepArgs& a, Ring& r, int32_t n_phases, uint32_t wave) {
+    if (r.ph < n_phases && r.ld.f >= r.fe && r.pad == 0) ring_seek(a, r, r.ph + 1, n_phases, wave);
+}
+
+// Issues the next stream tile into t.  One load pair either way, addresses chosen by selects (a
+// placeholder reads the idle buffer, which stays in L2): with no branch around the loads the
+// compiler waits for exactly the slot being consumed.
+__device__ __forceinline__ void ring_issue(const StepArgs& a, Ring& r, int32_t n_phases, uint32_t lane, Q4Tile& t) {
+    const bool real = r.ph < n_phases && r.ld.f < r.fe;
+    const Job& j = r.job;
+    const bool second = j.T == 4 && (r.ld.ts >> 1) != 0;
+    const size_t tile = !real ? 0 : j.T == 4 ? (size_t)(blockIdx.x + r.ld.k * gridDim.x) * 2 + (r.ld.ts & 1)
+                                             : (size_t)(blockIdx.x + r.ld.k * gridDim.x);
+    const uint4* codes = !real ? reinterpret_cast<const uint4*>(a.idle) : second ? j.codes[1] : j.codes[0];
+    const uint2* scales = !real ? reinterpret_cast<const uint2*>(a.idle + 1024) : second ? j.scales[1] : j.scales[0];
+    q4_tile_load(codes, scales, tile, j.nst, real ? r.ld.st : 0u, lane, t);
+    if (real) cur_next(r.ld, j.nst, j.T);
+    else if (r.pad) --r.pad;
+}
+
+// Consumes this wave's share of a GEMV phase from the ring (refilling every slot it visits) and
+// leaves one partial row sum per (unit, tile, wave) in part[(k * kMaxT + ts) * 8 + wave][16].
+__device__ __forceinline__ void ring_consume(const StepArgs& a, const Job& j, Ring& r, int32_t n_phases,
+                                             Q4Tile (&buf)[kAhead], const int8_t* dig, const DigitTab* tab,
+                                             float* part, uint32_t wave, uint32_t lane) {
+    uint32_t fb, fe;
+    wave_share(j, wave, fb, fe);
+    if (fb >= fe) return;  // no tiles here, and none in the stream for this phase
+    Cur cs = cur_at(fb, j.nst, j.T);
+    const uint32_t n = fe - fb;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    for (uint32_t base = 0; base < n; base += kAhead) {
+        ring_round(a, r, n_phases, wave);
+#pragma unroll
+        for (int u = 0; u < kAhead; ++u) {
+            if (base + u < n) {
+                q4_mfma_tile(buf[u], cs.st, dig, tab, lane, acc);
+                if (cs.st == j.nst - 1 || cs.f + 1 == fe) {
+                    q4_row_sums(acc);
+                    if ((lane & 15) == 0) {
+                        float* p = part + ((cs.k * kMaxT + cs.ts) * 8 + wave) * 16 + 4 * (lane >> 4);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) p[i] = acc[i];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
+                }
+                cur_next(cs, j.nst, j.T);
+            }
+            ring_issue(a, r, n_phases, lane, buf[u]);
+        }
+    }
 }
 
 }  // namespace
 
-// ---- the kernel -----------------------------------------------------------------------------------
+// Wave 0: work for phase ph that does not depend on the phase before it (norm weights of a
+// residual prologue, or the attention item's RoPE angles, norm weights and cached K/V rows).
+template <int GQ>
+__device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t pos, uint8_t* lds,
+                                          uint32_t lane) {
+    if (ph >= n_phases) return;
+    const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
+    if (kind == P_ATTN) {
+        CLayer& L = layer_at(a, l);
+        const AttnGeo ag = attn_geo(L, pos, a.cmax);
+        const uint32_t item = gridDim.x - 1 - blockIdx.x;
+        if (item < ag.items) attention_pre<GQ>(L, pos, item / ag.chunks, item % ag.chunks, ag.clen, ag.start, lds, lane);
+    } else if (kind == P_QKV || kind == P_GATEUP) {
+        const Gemv d = describe(a, l, kind);
+        preload_norms(d.in.w_a, d.in.w_n, d.K, d.job.nst, lds, lane);
+        wait_vm();
+    }
+}
 
+// Lowest LDS byte phase_pre writes for phase ph (no write: ~0).
+template <int GQ>
+__device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, int32_t n_phases) {
+    if (ph >= n_phases) return ~(size_t)0;
+    const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
+    if (kind == P_ATTN) return AttnLds<GQ>::pre_offset();
+    if (kind == P_QKV || kind == P_GATEUP) {
+        const Gemv d = describe(a, l, kind);
+        return (size_t)d.job.nst * 640 + (size_t)8 * d.K;
+    }
+    return ~(size_t)0;
+}
+
+// Wave roles.  Waves 1-7 issue no vector memory instruction but their weight loads: the
+// compiler then waits for exactly the ring slot being consumed, and no activation or staging
+// access ever queues behind the weight loads in flight.  Wave 0 does every other global access
+// (barrier, staging DMA, stores), and every wave-0 block that issues one waits for it before the
+// block ends.  A GEMV phase: barrier; wave 0 stages the inputs; all build the digit image from
+// LDS; waves 1-7 consume their weight stream (refilling the ring with the next phase's tiles)
+// while wave 0 stores the residual and prepares the next phase when its LDS is free; wave 0
+// stores the outputs.  Every phase's code appears once in the loop over (layer, phase).
 template <int GQ>
 __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float part[kMaxUnits * kMaxT * 8 * 16];
     __shared__ double red[8];
-    __shared__ int ok_flag;
+    __shared__ int ok_flag, att_flag;
     __shared__ float act_l[kMaxUnits][32];
 
     if (a.state[ST_STOP]) return;  // uniform: written only before the launch
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t pos = a.state[ST_POS];
-    const uint32_t H = a.hidden, I = a.inter;
     Grid g{a.bar, 0u, &ok_flag, a.clock};
-    if (tid == 0) stamp(g, 0);
+    stamp(g, M_START);
     bool failed = false;
+    const int32_t n_phases = (int32_t)(kPhases * a.n_layers);
     Q4Tile buf[kAhead];
-    Stream s{};
-
-    auto gemv_job = [&](const Q4View& m0, const Q4View* m1) {
-        Job j{};
-        j.codes[0] = reinterpret_cast<const uint4*>(m0.codes);
-        j.scales[0] = reinterpret_cast<const uint2*>(m0.scales);
-        if (m1) {
-            j.codes[1] = reinterpret_cast<const uint4*>(m1->codes);
-            j.scales[1] = reinterpret_cast<const uint2*>(m1->scales);
-            j.units = (m0.rows + 31) / 32;
-            j.T = 4;
-        } else {
-            j.units = (m0.rows + 15) / 16;
-            j.T = 1;
-        }
-        j.nst = m0.nst;
-        return j;
-    };
-    auto zero_part = [&]() {
-        for (uint32_t i = tid; i < kMaxUnits * kMaxT * 8 * 16; i += kThreads) part[i] = 0.0f;
-    };
-    // Streams a GEMV (prefetched already), then leaves its row sums in `part`.
-    auto run_stream = [&](const Job& j, uint32_t nst) {
-        if (wave != 0) {
-            const int8_t* dig = reinterpret_cast<const int8_t*>(lds);
-            const DigitTab* tab = reinterpret_cast<const DigitTab*>(lds + (size_t)nst * 512);
-            job_stream(j, s, buf, dig, tab, part, wave, lane);
-        }
-        __syncthreads();
-    };
-
-    const uint32_t n_layers = a.n_layers;
-    {
-        const Job j0 = gemv_job(a.layers[0].qkv, nullptr);
-        if (wave != 0) job_prefetch(j0, s, buf, wave, lane);
-    }
-    for (uint32_t l = 0; l < n_layers; ++l) {
-        const StepLayer& L = a.layers[l];
-        // ---- qkv: x = embedding (layer 0) or the previous layer's output; y = W_qkv rms(x) w
-        {
-            if (l > 0 && !grid_sync(g)) {
-                failed = true;
-                break;
-            }
-            Stage in{};
-            InputStage emb{};
-            int kind;
-            if (l == 0) {
-                kind = S_EMBED;
-                emb.table = a.table;
-                emb.ids = a.ids;
-                emb.state = a.state;
-                emb.emb_scale = a.emb_scale;
-            } else {
-                const StepLayer& P = a.layers[l - 1];
-                kind = S_RESID;
-                in.x = a.D;
-                in.res = a.H;
-                in.w_a = P.post_ffn;
-                in.eps_a = P.post_ffn_eps;
-                in.scale = P.layer_scale;
-            }
-            in.w_n = L.input_norm;
-            in.eps_n = L.input_eps;
-            in.x_out = a.X;
-            in.snap = a.snap && l > 0 ? a.snap + (size_t)(l - 1) * H : nullptr;
-            const Job j = gemv_job(L.qkv, nullptr);
-            if (wave == 0) stage_inputs(kind, in, H, j.nst, lds, lane);
-            __syncthreads();
-            zero_part();
-            stage_digits(kind, in, emb, H, j.nst, lds, red);
-            __syncthreads();
-            run_stream(j, j.nst);
-            const uint32_t mu = my_units(j.units);
-            if (tid < 16 * mu) {
-                const uint32_t k = tid >> 4, r = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + r;
-                if (row < L.qkv.rows) stc(a.QKV, row * 4, __float_as_uint(part_sum(part, k, 0, r)));
-            }
-            wait_vm();
-        }
-        // ---- attention
-        {
-            if (!grid_sync(g)) {
-                failed = true;
-                break;
-            }
-            const uint32_t nvis = L.window ? min(pos + 1, L.window) : pos + 1;
-            const uint32_t start = pos + 1 - nvis;
-            const uint32_t cmax = a.cmax / L.kv_heads;
-            uint32_t chunks = min(cmax, (nvis + kAttnMinChunk - 1) / kAttnMinChunk);
-            const uint32_t clen = (nvis + chunks - 1) / chunks;
-            chunks = (nvis + clen - 1) / clen;
-            const Job jo = gemv_job(L.o, nullptr);
-            const uint32_t items = L.kv_heads * chunks;
-            if (blockIdx.x < items) {
-                attention_item<GQ>(L, a, pos, blockIdx.x / chunks, blockIdx.x % chunks, chunks, cmax, clen, start,
-                                   lds);
-                wait_vm();
-                __syncthreads();
-            }
-            if (wave != 0) job_prefetch(jo, s, buf, wave, lane);
-        }
-        // ---- o-proj: input = the attention output's digit image
-        {
-            if (!grid_sync(g)) {
-                failed = true;
-                break;
-            }
-            const Job j = gemv_job(L.o, nullptr);
-            Stage in{};
-            in.dig = a.att_img;
-            if (wave == 0) stage_inputs(S_DIGITS, in, L.o.blocks * 32, j.nst, lds, lane);
-            zero_part();
-            __syncthreads();
-            run_stream(j, j.nst);
-            const uint32_t mu = my_units(j.units);
-            if (tid < 16 * mu) {
-                const uint32_t k = tid >> 4, r = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + r;
-                if (row < L.o.rows) stc(a.PROJ, row * 4, __float_as_uint(part_sum(part, k, 0, r)));
-            }
-            wait_vm();
-            const Job jg = gemv_job(L.gate, &L.up);
-            if (wave != 0) job_prefetch(jg, s, buf, wave, lane);
-        }
-        // ---- gate/up: x = rms(proj) post_attn + residual; act = gelu(gate) * up, as digits
-        {
-            if (!grid_sync(g)) {
-                failed = true;
-                break;
-            }
-            const Job j = gemv_job(L.gate, &L.up);
-            Stage in{};
-            InputStage emb{};
-            in.x = a.PROJ;
-            in.res = a.X;
-            in.w_a = L.post_attn;
-            in.eps_a = L.post_attn_eps;
-            in.scale = 1.0f;
-            in.w_n = L.ffn_norm;
-            in.eps_n = L.ffn_eps;
-            in.x_out = a.H;
-            if (wave == 0) stage_inputs(S_RESID, in, H, j.nst, lds, lane);
-            __syncthreads();
-            zero_part();
-            stage_digits(S_RESID, in, emb, H, j.nst, lds, red);
-            __syncthreads();
-            run_stream(j, j.nst);
-            const uint32_t mu = my_units(j.units);
-            if (tid < 32 * mu) {
-                const uint32_t k = tid >> 5, r = tid & 31, t = r >> 4, rr = r & 15;
-                act_l[k][r] = gelu_mul(part_sum(part, k, t, rr), part_sum(part, k, 2 + t, rr));
-            }
-            __syncthreads();
-            if (tid < 4 * mu) {
-                const uint32_t k = tid >> 2, p = tid & 3;
-                float v[8];
+    Ring r{};
+    if (wave != 0) {
+        ring_seek(a, r, 0, n_phases, wave);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = act_l[k][8 * p + e];
-                quad_digits_store(v, a.act_img, L.down.nst, blockIdx.x + k * gridDim.x, p);
-            }
-            wait_vm();
-            const Job jd = gemv_job(L.down, nullptr);
-            if (wave != 0) job_prefetch(jd, s, buf, wave, lane);
+        for (int u = 0; u < kAhead; ++u) ring_issue(a, r, n_phases, lane, buf[u]);
+    } else {
+        phase_pre<GQ>(a, 0, n_phases, pos, lds, lane);
+    }
+
+    for (int32_t ph = 0; ph < n_phases; ++ph) {
+        const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
+        if (ph > 0 && !grid_sync(g)) {
+            failed = true;
+            break;
         }
-        // ---- down: input = the activation's digit image
-        {
-            if (!grid_sync(g)) {
-                failed = true;
-                break;
-            }
-            const Job j = gemv_job(L.down, nullptr);
-            Stage in{};
-            in.dig = a.act_img;
-            if (wave == 0) stage_inputs(S_DIGITS, in, I, j.nst, lds, lane);
-            zero_part();
+        if (kind == P_ATTN) {
+            CLayer& L = layer_at(a, l);
+            const AttnGeo ag = attn_geo(L, pos, a.cmax);
+            const uint32_t item = gridDim.x - 1 - blockIdx.x;
+            if (item < ag.items)
+                attention_item<GQ>(L, a, pos, item / ag.chunks, item % ag.chunks, ag.chunks, ag.cmax, ag.clen, ag.start,
+                                   lds, &att_flag);
             __syncthreads();
-            run_stream(j, j.nst);
-            const uint32_t mu = my_units(j.units);
-            if (tid < 16 * mu) {
-                const uint32_t k = tid >> 4, r = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + r;
-                if (row < L.down.rows) stc(a.D, row * 4, __float_as_uint(part_sum(part, k, 0, r)));
+            stamp(g, M_STORED);
+        } else {
+            const Gemv d = describe(a, l, kind);
+            const uint32_t nst = d.job.nst;
+            if (wave == 0) stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, lds, lane);
+            __syncthreads();
+            stamp(g, M_STAGED);
+            zero_part_lds(part, tid);
+            if (d.in_kind != S_DIGITS) stage_digits(d.in_kind, d.in, d.K, nst, lds, red);
+            __syncthreads();
+            stamp(g, M_DIGITS);
+            // the next phase's LDS writes may start now if they stay above this phase's image
+            const bool pre_now = phase_pre_low<GQ>(a, ph + 1, n_phases) >= (size_t)nst * 640;
+            if (wave != 0) {
+                ring_consume(a, d.job, r, n_phases, buf, reinterpret_cast<const int8_t*>(lds),
+                             reinterpret_cast<const DigitTab*>(lds + (size_t)nst * 512), part, wave, lane);
+            } else {
+                if (blockIdx.x == 0 && d.in_kind != S_DIGITS) {
+                    store_residual(d.in, lds, d.K, nst, lane);
+                    wait_vm();
+                }
+                if (pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
+                stamp(g, M_PRE);
             }
-            wait_vm();
-            if (l + 1 < n_layers) {
-                const Job jn = gemv_job(a.layers[l + 1].qkv, nullptr);
-                if (wave != 0) job_prefetch(jn, s, buf, wave, lane);
+            __syncthreads();
+            stamp(g, M_STREAMED);
+            if (wave == 0) {
+                if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
+                const uint32_t mu = my_units(d.job.units);
+                if (d.y) {
+                    if (tid < 16 * mu) {
+                        const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
+                        if (row < d.rows) stc(d.y, row * 4, __float_as_uint(part_sum(part, k, 0, rr)));
+                    }
+                } else {
+                    if (tid < 32 * mu) {
+                        const uint32_t k = tid >> 5, rr = tid & 31, t = rr >> 4, r16 = rr & 15;
+                        act_l[k][rr] = gelu_mul(part_sum(part, k, t, r16), part_sum(part, k, 2 + t, r16));
+                    }
+                    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // act_l: written and read by wave 0
+                    if (tid < 4 * mu) {
+                        const uint32_t k = tid >> 2, p = tid & 3;
+                        float v[8];
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) v[e] = act_l[k][8 * p + e];
+                        quad_digits_store(v, a.act_img, d.act_nst, blockIdx.x + k * gridDim.x, p);
+                    }
+                }
+                wait_vm();
             }
+            stamp(g, M_STORED);
         }
     }
     grid_exit(g, a.state, a.advance != 0, failed);
+}
+
+uint32_t step_merge_chunks(uint32_t group, size_t lds) {
+    const size_t out = (size_t)group * 256 * 4, per = (size_t)group * 258 * 4;
+    return lds > out ? (uint32_t)((lds - out) / per) : 0u;
 }
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group) {
@@ -783,9 +1037,7 @@ size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t 
     size_t g = nst_h * 640 + (size_t)4 * hidden * 4;  // image + staging of a residual prologue
     g = std::max(g, nst_i * 640);
     g = std::max(g, nst_q * 640);
-    const size_t D = 256, NH = group + 2;
-    const size_t att = 4 * (NH * D + group * D + group * kStepMaxClen + 16 * group * D) + 8 * 8 * NH + 4 * 8 +
-                       4 * 2 * group * kStepMaxChunks + 16;
+    const size_t att = group == 1 ? AttnLds<1>::bytes() : group == 2 ? AttnLds<2>::bytes() : AttnLds<4>::bytes();
     return std::max(g, att);
 }
 

@@ -141,7 +141,9 @@ def main():
         if pn:
             us = 1000.0 * pms / pn
             rate = f"{pb / (us * 1e3):8.1f} GB/s" if pb else ""
-            log(f"    phase {name:10s} x{pn:5d}  avg {us:7.2f} us  {pb / 1e6:8.3f} MB  {rate}")
+            marks = "  ".join(f"{k.split('.')[1]} {1000.0 * v[1] / v[0]:.2f}" for k, v in timings.items()
+                              if k.startswith(name + ".") and v[0])
+            log(f"    phase {name:10s} x{pn:5d}  avg {us:7.2f} us  {pb / 1e6:8.3f} MB  {rate}  [{marks}]")
     log(f"algorithmic bytes per token {per_token_bytes / 1e9:.3f} GB -> roofline {PEAK_GBS * 1e9 / per_token_bytes:.0f} "
         f"tok/s at 8 TB/s; measured {tok_s:.1f} tok/s = {tok_s * per_token_bytes / (PEAK_GBS * 1e9):.3f} of it")
 
