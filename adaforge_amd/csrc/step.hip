@@ -344,7 +344,8 @@ struct AttnLds {
     uint16_t* knew;   // [D] new K row (fp16)
     uint16_t* vnew;   // [D] new V row (fp16)
     // pre
-    double* rope;     // cos [128], sin [128] of pos * inv_freq
+    double* rope;     // cos [128], sin [128] of pos * inv_freq (written after the barrier)
+    double* ifreq;    // [128] the layer's RoPE inverse frequencies
     float* qnw;       // [D] q_norm weights
     float* knw;       // [D] k_norm weights
     uint16_t* kst;    // [stage_clen][D] fp16 K rows of the chunk
@@ -353,7 +354,7 @@ struct AttnLds {
         return 4 * (NH * D + GQ * D + GQ * kStepMaxClen + 16 * GQ * D) + 8 * 8 * NH + 4 * 8 + 2 * 2 * D;
     }
     static constexpr size_t pre_offset() { return (transient_bytes() + 255) / 256 * 256; }
-    static constexpr size_t bytes() { return pre_offset() + 8 * 256 + 4 * 2 * D + 2 * 2 * stage_clen<GQ>() * D; }
+    static constexpr size_t bytes() { return pre_offset() + 8 * 384 + 4 * 2 * D + 2 * 2 * stage_clen<GQ>() * D; }
     __device__ explicit AttnLds(uint8_t* lds) {
         nrm = reinterpret_cast<float*>(lds);
         qs = nrm + NH * D;
@@ -364,7 +365,8 @@ struct AttnLds {
         knew = reinterpret_cast<uint16_t*>(fred + 8);
         vnew = knew + D;
         rope = reinterpret_cast<double*>(lds + pre_offset());
-        qnw = reinterpret_cast<float*>(rope + 256);
+        ifreq = rope + 256;
+        qnw = reinterpret_cast<float*>(ifreq + 128);
         knw = qnw + D;
         kst = reinterpret_cast<uint16_t*>(knw + D);
         vst = kst + stage_clen<GQ>() * D;
@@ -372,12 +374,14 @@ struct AttnLds {
 };
 
 // Wave 0, while the qkv phase streams (nothing here depends on this step's q, k, v): the RoPE
-// angles, the q/k norm weights and the chunk's cached K and V rows, into the "pre" LDS part.
+// inverse frequencies, the q/k norm weights and the chunk's cached K and V rows, copied into
+// the "pre" LDS part.  The copies are waited for with wave 0's next wait (before the barrier).
 template <int GQ>
 __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t h, uint32_t c, uint32_t clen,
                                               uint32_t start, uint8_t* lds, uint32_t lane) {
     AttnLds<GQ> m(lds);
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
+    dma(L.inv_freq, 8 * 128, reinterpret_cast<uint8_t*>(m.ifreq), lane);
     dma(L.q_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.qnw), lane);
     dma(L.k_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.knw), lane);
     if (clen <= stage_clen<GQ>()) {
@@ -391,15 +395,6 @@ __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t 
             }
         }
     }
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const uint32_t f = lane + 64 * i;
-        double sn, cs;
-        sincos((double)pos * gp(L.inv_freq)[f], &sn, &cs);
-        m.rope[f] = cs;
-        m.rope[128 + f] = sn;
-    }
-    wait_vm();
 }
 
 // One attention item.  Only wave 0 touches global memory (the streaming waves' weight loads stay
@@ -430,6 +425,15 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         if (append) {
             dma(a.QKV + L.qn + h * D, 4 * D, reinterpret_cast<uint8_t*>(nrm + GQ * D), lane);
             dma(a.QKV + L.v_off + h * D, 4 * D, reinterpret_cast<uint8_t*>(nrm + (GQ + 1) * D), lane);
+        }
+        // the RoPE angles of this position, while the copies are in flight
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t f = lane + 64 * i;
+            double sn, cs;
+            sincos((double)pos * sh.ifreq[f], &sn, &cs);
+            sh.rope[f] = cs;
+            sh.rope[128 + f] = sn;
         }
         wait_vm();
     }
@@ -486,15 +490,6 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         if (staged) sh.vst[(pos - t0) * D + tid] = v;
     }
     __syncthreads();
-    // the new K/V rows into the cache (read back by later steps only: this step reads them from LDS)
-    const size_t slot = ((size_t)h * ring + pos % ring) * D;
-    if (append && wave == 0) {
-        const v2u* kn = reinterpret_cast<const v2u*>(sh.knew);
-        const v2u* vn = reinterpret_cast<const v2u*>(sh.vnew);
-        *gp(reinterpret_cast<v2u*>(L.kcache + slot) + lane) = kn[lane];
-        *gp(reinterpret_cast<v2u*>(L.vcache + slot) + lane) = vn[lane];
-        wait_vm();
-    }
 
     // scores: 16 lanes per token (16 channels each), 32 token groups; q is re-read from LDS for
     // every token (registers stay free for the weight loads in flight)
@@ -613,6 +608,11 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     __syncthreads();
     float* const head_part = a.part + (size_t)h * cmax * stride;
     if (wave == 0) {
+        if (append) {  // the new K/V rows into the cache (this step reads them from LDS)
+            const size_t slot = ((size_t)h * ring + pos % ring) * D;
+            *gp(reinterpret_cast<v2u*>(L.kcache + slot) + lane) = reinterpret_cast<const v2u*>(sh.knew)[lane];
+            *gp(reinterpret_cast<v2u*>(L.vcache + slot) + lane) = reinterpret_cast<const v2u*>(sh.vnew)[lane];
+        }
         for (uint32_t i = lane; i < stride; i += 64) stc(head_part, (c * stride + i) * 4, __float_as_uint(pst[i]));
         wait_vm();
         if (lane == 0) {
@@ -810,11 +810,11 @@ __device__ __forceinline__ Job phase_job(const StepArgs& a, uint32_t ph) {
 // once with the tile kAhead further on, across phase boundaries, so the next phase's first
 // tiles are in flight while this one finishes and the ring never drains inside the launch.
 struct Ring {
-    Job job;       // the phase being loaded
-    Cur ld;        // its next tile
-    uint32_t fe;   // end of this wave's share
-    uint32_t pad;  // placeholders still to issue after the share
-    int32_t ph;    // the phase (n_phases once every phase is issued)
+    Job job;          // the phase being loaded
+    Cur ld;           // its next tile
+    uint32_t fe;      // end of this wave's share
+    uint32_t pad;     // placeholders still to issue after the share
+    int32_t ph;       // the phase (n_phases once every phase is issued)
 };
 
 __device__ __forceinline__ void ring_seek(const StepArgs& a, Ring& r, int32_t ph, int32_t n_phases, uint32_t wave) {
@@ -892,8 +892,9 @@ __device__ __forceinline__ void ring_consume(const StepArgs& a, const Job& j, Ri
 
 }  // namespace
 
-// Wave 0: work for phase ph that does not depend on the phase before it (norm weights of a
-// residual prologue, or the attention item's RoPE angles, norm weights and cached K/V rows).
+// Wave 0: copies for phase ph that do not depend on the phase before it (norm weights of a
+// residual prologue, or the attention item's RoPE frequencies, norm weights and cached K/V
+// rows).  Issued only: the caller waits (wave 0 waits for everything before its barrier arrival).
 template <int GQ>
 __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t pos, uint8_t* lds,
                                           uint32_t lane) {
@@ -907,7 +908,6 @@ __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t
     } else if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
         preload_norms(d.in.w_a, d.in.w_n, d.K, d.job.nst, lds, lane);
-        wait_vm();
     }
 }
 
@@ -955,6 +955,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         for (int u = 0; u < kAhead; ++u) ring_issue(a, r, n_phases, lane, buf[u]);
     } else {
         phase_pre<GQ>(a, 0, n_phases, pos, lds, lane);
+        wait_vm();
     }
 
     for (int32_t ph = 0; ph < n_phases; ++ph) {
@@ -984,20 +985,17 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             stamp(g, M_DIGITS);
             // the next phase's LDS writes may start now if they stay above this phase's image
             const bool pre_now = phase_pre_low<GQ>(a, ph + 1, n_phases) >= (size_t)nst * 640;
+            // Each role's code up to its last global access of the phase is one branch, so the
+            // compiler's wait model never mixes wave 0's copies into the streaming waves'.
             if (wave != 0) {
                 ring_consume(a, d.job, r, n_phases, buf, reinterpret_cast<const int8_t*>(lds),
                              reinterpret_cast<const DigitTab*>(lds + (size_t)nst * 512), part, wave, lane);
+                __syncthreads();
             } else {
-                if (blockIdx.x == 0 && d.in_kind != S_DIGITS) {
-                    store_residual(d.in, lds, d.K, nst, lane);
-                    wait_vm();
-                }
+                if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, nst, lane);
                 if (pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
-                stamp(g, M_PRE);
-            }
-            __syncthreads();
-            stamp(g, M_STREAMED);
-            if (wave == 0) {
+                __syncthreads();
+                stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = my_units(d.job.units);
                 if (d.y) {
@@ -1020,8 +1018,8 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                     }
                 }
                 wait_vm();
+                stamp(g, M_STORED);
             }
-            stamp(g, M_STORED);
         }
     }
     grid_exit(g, a.state, a.advance != 0, failed);
