@@ -145,7 +145,10 @@ __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance
 // Rows are grouped into units: one 16-row tile (T = 1), or two tiles of two matrices (T = 4:
 // gate tiles 2u, 2u + 1 then up tiles 2u, 2u + 1).  Workgroup b takes units b, b + G, ...
 // (at most kMaxUnits); its super-tile work, flattened as (unit, tile stream, super-tile), is
-// split evenly over the streaming waves.
+// dealt round-robin to the streaming waves: wave w takes w - 1, w - 1 + 7, ...  Every wave thus
+// streams from every row tile of the workgroup (a contiguous split leaves whole matrices, and
+// whatever memory channels they sit on, to single waves, which then finish unevenly), and still
+// visits each row tile in one run, so it leaves one partial row sum per row tile.
 struct Job {
     const uint4* codes[2];
     const uint2* scales[2];
@@ -161,10 +164,12 @@ __device__ __forceinline__ Cur cur_at(uint32_t f, uint32_t nst, uint32_t T) {
     return Cur{f, f - seg * nst, seg % T, seg / T};
 }
 
+// The wave's next super-tile: kStreamWaves further on.
 __device__ __forceinline__ void cur_next(Cur& c, uint32_t nst, uint32_t T) {
-    ++c.f;
-    if (++c.st == nst) {
-        c.st = 0;
+    c.f += kStreamWaves;
+    c.st += kStreamWaves;
+    while (c.st >= nst) {
+        c.st -= nst;
         if (++c.ts == T) {
             c.ts = 0;
             ++c.k;
@@ -176,12 +181,13 @@ __device__ __forceinline__ uint32_t my_units(uint32_t units) {
     return units > blockIdx.x ? min(kMaxUnits, (units - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0u;
 }
 
-// This streaming wave's share [fb, fe) of a job's flattened super-tiles.
-__device__ __forceinline__ void wave_share(const Job& j, uint32_t wave, uint32_t& fb, uint32_t& fe) {
-    const uint32_t F = my_units(j.units) * j.T * j.nst, w = wave - 1;
+// This streaming wave's share of a job's flattened super-tiles: fb, fb + 7, ... below fe, n of
+// them.
+__device__ __forceinline__ void wave_share(const Job& j, uint32_t wave, uint32_t& fb, uint32_t& fe, uint32_t& n) {
     // wave-uniform values: readfirstlane keeps the cursors (and all control flow on them) scalar
-    fb = __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)F * w) / kStreamWaves));
-    fe = __builtin_amdgcn_readfirstlane((uint32_t)(((uint64_t)F * (w + 1)) / kStreamWaves));
+    fe = __builtin_amdgcn_readfirstlane(my_units(j.units) * j.T * j.nst);
+    fb = wave - 1;
+    n = fe > fb ? (fe - fb + kStreamWaves - 1) / kStreamWaves : 0u;
 }
 
 __device__ __forceinline__ void zero_part_lds(float* part, uint32_t tid) {
@@ -809,35 +815,53 @@ __device__ __forceinline__ Job phase_job(const StepArgs& a, uint32_t ph) {
 // in ring slot 0.  Ring slot u holds stream tile u mod kAhead; a consumed slot is refilled at
 // once with the tile kAhead further on, across phase boundaries, so the next phase's first
 // tiles are in flight while this one finishes and the ring never drains inside the launch.
-struct Ring {
-    Job job;          // the phase being loaded
-    Cur ld;           // its next tile
-    uint32_t fe;      // end of this wave's share
-    uint32_t pad;     // placeholders still to issue after the share
-    int32_t ph;       // the phase (n_phases once every phase is issued)
+struct Seek {
+    Job job;   // the phase being loaded
+    Cur ld;    // its next tile
+    uint32_t fe;   // end of this wave's share
+    uint32_t pad;  // placeholders still to issue after the share
+    int32_t ph;    // the phase (n_phases once every phase is issued)
+};
+struct Ring : Seek {
+    Seek nx;      // where the loads go after phase ph (prepared by ring_prepare)
+    int32_t nx_for;  // the ph that nx follows
 };
 
-__device__ __forceinline__ void ring_seek(const StepArgs& a, Ring& r, int32_t ph, int32_t n_phases, uint32_t wave) {
+// The first phase at or after ph with tiles for this wave.  Reads the layer table (scalar loads).
+__device__ __forceinline__ Seek seek_from(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t wave) {
+    Seek s{};
     for (; ph < n_phases; ++ph) {
         if ((uint32_t)ph % kPhases == P_ATTN) continue;
-        r.job = phase_job(a, (uint32_t)ph);
-        uint32_t fb;
-        wave_share(r.job, wave, fb, r.fe);
-        if (fb < r.fe) {
-            r.ld = cur_at(fb, r.job.nst, r.job.T);
-            r.pad = (kAhead - (r.fe - fb) % kAhead) % kAhead;
-            r.ph = __builtin_amdgcn_readfirstlane(ph);
-            return;
+        s.job = phase_job(a, (uint32_t)ph);
+        uint32_t fb, n;
+        wave_share(s.job, wave, fb, s.fe, n);
+        if (n) {
+            s.ld = cur_at(fb, s.job.nst, s.job.T);
+            s.pad = (kAhead - n % kAhead) % kAhead;
+            s.ph = __builtin_amdgcn_readfirstlane(ph);
+            return s;
         }
     }
-    r.ph = n_phases;
-    r.pad = 0;
+    s.ph = n_phases;
+    s.pad = 0;
+    return s;
+}
+
+// Streaming waves, at the start of every GEMV phase (while wave 0 stages the inputs): where the
+// loads go once the current phase's share is issued.  The ring switches to it inside the consume
+// loop with no memory access: a scalar load in flight there would make the next LDS read wait
+// for it (scalar loads may return out of order, so the compiler waits for all of them at once).
+__device__ __forceinline__ void ring_prepare(const StepArgs& a, Ring& r, int32_t n_phases, uint32_t wave) {
+    if (r.nx_for != r.ph) {
+        r.nx = seek_from(a, r.ph + 1, n_phases, wave);
+        r.nx_for = r.ph;
+    }
 }
 
 // Shares are padded to multiples of kAhead and the loads run exactly kAhead tiles ahead, so a
-// round of kAhead refills never crosses a phase boundary: the next phase is sought once per round.
-__device__ __forceinline__ void ring_round(const StepArgs& a, Ring& r, int32_t n_phases, uint32_t wave) {
-    if (r.ph < n_phases && r.ld.f >= r.fe && r.pad == 0) ring_seek(a, r, r.ph + 1, n_phases, wave);
+// round of kAhead refills never crosses a phase boundary: the switch happens once per round.
+__device__ __forceinline__ void ring_round(Ring& r, int32_t n_phases) {
+    if (r.ph < n_phases && r.ld.f >= r.fe && r.pad == 0) static_cast<Seek&>(r) = r.nx;
 }
 
 // Issues the next stream tile into t.  One load pair either way, addresses chosen by selects (a
@@ -861,19 +885,18 @@ __device__ __forceinline__ void ring_issue(const StepArgs& a, Ring& r, int32_t n
 __device__ __forceinline__ void ring_consume(const StepArgs& a, const Job& j, Ring& r, int32_t n_phases,
                                              Q4Tile (&buf)[kAhead], const int8_t* dig, const DigitTab* tab,
                                              float* part, uint32_t wave, uint32_t lane) {
-    uint32_t fb, fe;
-    wave_share(j, wave, fb, fe);
-    if (fb >= fe) return;  // no tiles here, and none in the stream for this phase
+    uint32_t fb, fe, n;
+    wave_share(j, wave, fb, fe, n);
+    if (!n) return;  // no tiles here, and none in the stream for this phase
     Cur cs = cur_at(fb, j.nst, j.T);
-    const uint32_t n = fe - fb;
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
     for (uint32_t base = 0; base < n; base += kAhead) {
-        ring_round(a, r, n_phases, wave);
+        ring_round(r, n_phases);
 #pragma unroll
         for (int u = 0; u < kAhead; ++u) {
             if (base + u < n) {
                 q4_mfma_tile(buf[u], cs.st, dig, tab, lane, acc);
-                if (cs.st == j.nst - 1 || cs.f + 1 == fe) {
+                if (cs.st + kStreamWaves >= j.nst || cs.f + kStreamWaves >= fe) {  // the run's last tile
                     q4_row_sums(acc);
                     if ((lane & 15) == 0) {
                         float* p = part + ((cs.k * kMaxT + cs.ts) * 8 + wave) * 16 + 4 * (lane >> 4);
@@ -950,7 +973,9 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     Q4Tile buf[kAhead];
     Ring r{};
     if (wave != 0) {
-        ring_seek(a, r, 0, n_phases, wave);
+        static_cast<Seek&>(r) = seek_from(a, 0, n_phases, wave);
+        r.nx_for = -1;
+        ring_prepare(a, r, n_phases, wave);
 #pragma unroll
         for (int u = 0; u < kAhead; ++u) ring_issue(a, r, n_phases, lane, buf[u]);
     } else {
@@ -977,6 +1002,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             const Gemv d = describe(a, l, kind);
             const uint32_t nst = d.job.nst;
             if (wave == 0) stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, lds, lane);
+            else ring_prepare(a, r, n_phases, wave);
             __syncthreads();
             stamp(g, M_STAGED);
             zero_part_lds(part, tid);
