@@ -88,6 +88,15 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
+// Sum over a 512-thread block of one double per thread, with one barrier: red holds 8 slots used
+// by this call alone (a second call needs other slots, or a barrier in between).
+__device__ inline double block_sum_once(double v, double* red) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + (red[2] + red[3])) + ((red[4] + red[5]) + (red[6] + red[7]));
+}
+
 // Sum over the block of one double per thread (blockDim a multiple of 64, <= 512).
 __device__ inline double block_sum_d(double v, double* red) {
     v = wave_sum(v);
@@ -129,6 +138,18 @@ __device__ __forceinline__ float norm_apply(float x, double r, float w) {
 
 __device__ __forceinline__ double inv_rms(double sumsq, uint32_t n, float eps) {
     return 1.0 / sqrt(__dadd_rn(sumsq / (double)n, (double)eps));
+}
+
+// 1 / sqrt(sumsq / n + eps) from the hardware estimate and two Newton steps
+// y <- y (1.5 - 0.5 x y^2): each step roughly doubles the correct bits of the ~2^-22-accurate
+// estimate, so the result is within a few double ulps of the division and square root above
+// (the f32 values it scales round identically but in rare ties).
+__device__ __forceinline__ double inv_rms_fast(double sumsq, uint32_t n, float eps) {
+    const double x = __dadd_rn(sumsq / (double)n, (double)eps);
+    double y = __builtin_amdgcn_rsq(x);
+    y = y * __fma_rn(-0.5 * x * y, y, 1.5);
+    y = y * __fma_rn(-0.5 * x * y, y, 1.5);
+    return y;
 }
 
 // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) in double, rounded to f32, times up in f32.
@@ -340,9 +361,20 @@ __device__ __forceinline__ void digit_words(const float (&v)[8], float m, uint32
 __device__ __forceinline__ void digits8(const float (&v)[8], float m, int8_t* dig, uint32_t b, uint32_t p) {
     uint32_t w[4][2];
     digit_words(v, m, w);
+    // plane (i + b) % 4 at store i: the 16 blocks of a wave spread over four LDS bank groups
+    // instead of all starting at bank 0 (blocks are 128 bytes apart)
 #pragma unroll
-    for (int t = 0; t < 4; ++t)
-        *reinterpret_cast<uint2*>(dig + ((size_t)b * 4 + t) * 32 + 8 * p) = make_uint2(w[t][0], w[t][1]);
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t t = (i + b) & 3;
+        uint32_t lo = w[0][0], hi = w[0][1];
+        lo = t == 1 ? w[1][0] : lo;
+        hi = t == 1 ? w[1][1] : hi;
+        lo = t == 2 ? w[2][0] : lo;
+        hi = t == 2 ? w[2][1] : hi;
+        lo = t == 3 ? w[3][0] : lo;
+        hi = t == 3 ? w[3][1] : hi;
+        *reinterpret_cast<uint2*>(dig + ((size_t)b * 4 + t) * 32 + 8 * p) = make_uint2(lo, hi);
+    }
 }
 
 // Block max |x| and sum over the 4 lanes (a quad) that hold a block's 8-element parts.

@@ -250,8 +250,18 @@ __device__ __forceinline__ void store_residual(const Stage& in, const uint8_t* l
     }
 }
 
+__device__ __forceinline__ void ld8(const float* p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+__device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+
 // Digit image of the normalised input (K <= 4096, so one octet per thread), all threads, from
-// LDS only.  The residual sum replaces x in xs[0, K) for store_residual.
+// LDS only (16-byte accesses: 8-float strides read element-wise would hit the same bank from
+// 16 lanes).  The residual sum replaces x in xs[0, K) for store_residual.  red: 16 slots.
 __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t K, uint32_t nst, uint8_t* lds,
                                              double* red) {
     int8_t* dig = reinterpret_cast<int8_t*>(lds);
@@ -259,38 +269,41 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t
     float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
     const uint32_t tid = threadIdx.x, n8 = K / 8, o = tid;
     const bool ok = o < n8;
-    float t[8], v[8];
-    if (kind == S_EMBED) {
+    float t[8], v[8], w[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) t[k] = ok ? xs[8 * o + k] : 0.0f;
+    for (int k = 0; k < 8; ++k) t[k] = w[k] = 0.0f;
+    if (kind == S_EMBED) {
+        if (ok) ld8(xs + 8 * o, t);
     } else {
+        float x[8], r[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = r[k] = 0.0f;
+        if (ok) {
+            ld8(xs + 8 * o, x);
+            ld8(xs + K + 8 * o, r);
+            if (in.w_a) ld8(xs + 2 * K + 8 * o, w);
+        }
         double ra = 1.0;
         if (in.w_a) {
             double sa = 0.0;
-            if (ok) {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) sa += (double)xs[8 * o + k] * xs[8 * o + k];
-            }
-            ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
+            for (int k = 0; k < 8; ++k) sa += (double)x[k] * x[k];
+            ra = inv_rms_fast(block_sum_once(sa, red), K, in.eps_a);
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            if (ok) {
-                const float x = xs[8 * o + k], r = xs[K + 8 * o + k];
-                const float u = in.w_a ? norm_apply(x, ra, xs[2 * K + 8 * o + k]) : x;
-                t[k] = __fmul_rn(__fadd_rn(u, r), in.scale);
-                xs[8 * o + k] = t[k];
-            } else {
-                t[k] = 0.0f;
-            }
+            const float u = in.w_a ? norm_apply(x[k], ra, w[k]) : x[k];
+            t[k] = ok ? __fmul_rn(__fadd_rn(u, r[k]), in.scale) : 0.0f;
         }
+        if (ok) st8(xs + 8 * o, t);
     }
     double ss = 0.0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) ss += (double)t[k] * t[k];
-    const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
+    if (ok) ld8(xs + 3 * K + 8 * o, w);
+    const double rn = inv_rms_fast(block_sum_once(ss, red + 8), K, in.eps_n);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = ok ? norm_apply(t[k], rn, xs[3 * K + 8 * o + k]) : 0.0f;
+    for (int k = 0; k < 8; ++k) v[k] = ok ? norm_apply(t[k], rn, w[k]) : 0.0f;
     float m, sum;
     quad_stats(v, m, sum);
     const uint32_t b = o >> 2, p = o & 3;
@@ -959,7 +972,7 @@ template <int GQ>
 __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float part[kMaxUnits * kMaxT * 8 * 16];
-    __shared__ double red[8];
+    __shared__ double red[16];
     __shared__ int ok_flag, att_flag;
     __shared__ float act_l[kMaxUnits][32];
 
