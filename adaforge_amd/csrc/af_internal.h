@@ -195,6 +195,7 @@ struct StepArgs {
     uint32_t cmax;                  // attention chunks per KV head (at most grid / kv_heads, and
                                     // what the merge can hold in LDS: step_merge_chunks)
     uint32_t advance;               // 1: move ST_POS on at the end (a step without the head)
+    uint32_t xs_off;                // LDS byte offset of the residual prologue's staging (step_xs_offset)
     float* snap;                    // optional: layer outputs [n_layers][hidden] (the last by the head)
     uint64_t* clock;                // optional: [phases][kStepMarks][grid] timestamps (100 MHz), one
                                     // phase per barrier interval (see StepMark)
@@ -211,6 +212,7 @@ constexpr uint32_t kStepMaxUnits = 2;     // GEMV row units per workgroup (16 ro
 constexpr size_t kStepBarBytes = 32 * 10 * 4;
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group);
+uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim);
 uint32_t step_merge_chunks(uint32_t group, size_t lds);  // chunk partials one merge holds in LDS
 hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid);
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s);

@@ -932,6 +932,7 @@ struct af_session {
         a.bar = BAR.as<uint32_t>();
         a.idle = IDLE.as<uint8_t>();
         a.cmax = step_cmax;
+        a.xs_off = step_xs_offset(hidden, intermediate, max_q);
         a.advance = advance ? 1u : 0u;
         a.snap = snap;
         return a;

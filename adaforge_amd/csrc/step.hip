@@ -202,8 +202,10 @@ __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_
     return v;
 }
 
-// Input prologue of a GEMV phase: LDS layout [digit image nst * 640][x K][res K][w_a K][w_n K]
-// (floats).  Wave 0 stages, every thread then builds the digit image.
+// Input prologue of a GEMV phase: LDS layout [digit image nst * 640] ... and, at StepArgs::xs_off
+// (above the largest image of any phase, so the next phase's norm weights can be copied in while
+// this phase's image is in use), [x K][res K][w_a K][w_n K] (floats).  Wave 0 stages, every
+// thread then builds the digit image.
 enum StageKind { S_EMBED = 0, S_RESID = 1, S_DIGITS = 2 };
 
 struct Stage {
@@ -217,9 +219,9 @@ struct Stage {
 // Wave 0, after the barrier: the activation inputs (the norm weights are already in LDS), or
 // the embedding row of the step's token.
 __device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const InputStage& emb, uint32_t K, uint32_t nst,
-                                             uint8_t* lds, uint32_t lane) {
+                                             uint32_t xs_off, uint8_t* lds, uint32_t lane) {
     uint8_t* img = lds;
-    float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
+    float* xs = reinterpret_cast<float*>(lds + xs_off);
     if (kind == S_DIGITS) {
         dma(in.dig, nst * 640, img, lane);
     } else if (kind == S_RESID) {
@@ -232,17 +234,17 @@ __device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const In
 }
 
 // Wave 0: the norm weights (constant) of a residual prologue into their LDS slots.
-__device__ __forceinline__ void preload_norms(const float* w_a, const float* w_n, uint32_t K, uint32_t nst, uint8_t* lds,
-                                              uint32_t lane) {
-    float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
+__device__ __forceinline__ void preload_norms(const float* w_a, const float* w_n, uint32_t K, uint32_t xs_off,
+                                              uint8_t* lds, uint32_t lane) {
+    float* xs = reinterpret_cast<float*>(lds + xs_off);
     if (w_a) dma(w_a, K * 4, reinterpret_cast<uint8_t*>(xs + 2 * K), lane);
     dma(w_n, K * 4, reinterpret_cast<uint8_t*>(xs + 3 * K), lane);
 }
 
 // Wave 0 of workgroup 0: the residual left in xs[0, K) by stage_digits.
-__device__ __forceinline__ void store_residual(const Stage& in, const uint8_t* lds, uint32_t K, uint32_t nst,
+__device__ __forceinline__ void store_residual(const Stage& in, const uint8_t* lds, uint32_t K, uint32_t xs_off,
                                                uint32_t lane) {
-    const v4u* xs = reinterpret_cast<const v4u*>(lds + (size_t)nst * 640);
+    const v4u* xs = reinterpret_cast<const v4u*>(lds + xs_off);
     for (uint32_t i = lane; i < K / 4; i += 64) {
         const v4u v = xs[i];
         stc16(in.x_out, i * 16, v);
@@ -262,11 +264,11 @@ __device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
 // Digit image of the normalised input (K <= 4096, so one octet per thread), all threads, from
 // LDS only (16-byte accesses: 8-float strides read element-wise would hit the same bank from
 // 16 lanes).  The residual sum replaces x in xs[0, K) for store_residual.  red: 16 slots.
-__device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t K, uint32_t nst, uint8_t* lds,
-                                             double* red) {
+__device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t K, uint32_t nst, uint32_t xs_off,
+                                             uint8_t* lds, double* red) {
     int8_t* dig = reinterpret_cast<int8_t*>(lds);
     DigitTab* tab = reinterpret_cast<DigitTab*>(lds + (size_t)nst * 512);
-    float* xs = reinterpret_cast<float*>(lds + (size_t)nst * 640);
+    float* xs = reinterpret_cast<float*>(lds + xs_off);
     const uint32_t tid = threadIdx.x, n8 = K / 8, o = tid;
     const bool ok = o < n8;
     float t[8], v[8], w[8];
@@ -943,7 +945,7 @@ __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t
         if (item < ag.items) attention_pre<GQ>(L, pos, item / ag.chunks, item % ag.chunks, ag.clen, ag.start, lds, lane);
     } else if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
-        preload_norms(d.in.w_a, d.in.w_n, d.K, d.job.nst, lds, lane);
+        preload_norms(d.in.w_a, d.in.w_n, d.K, a.xs_off, lds, lane);
     }
 }
 
@@ -955,7 +957,7 @@ __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, i
     if (kind == P_ATTN) return AttnLds<GQ>::pre_offset();
     if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
-        return (size_t)d.job.nst * 640 + (size_t)8 * d.K;
+        return (size_t)a.xs_off + (size_t)8 * d.K;
     }
     return ~(size_t)0;
 }
@@ -1014,12 +1016,12 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         } else {
             const Gemv d = describe(a, l, kind);
             const uint32_t nst = d.job.nst;
-            if (wave == 0) stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, lds, lane);
+            if (wave == 0) stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, a.xs_off, lds, lane);
             else ring_prepare(a, r, n_phases, wave);
             __syncthreads();
             stamp(g, M_STAGED);
             zero_part_lds(part, tid);
-            if (d.in_kind != S_DIGITS) stage_digits(d.in_kind, d.in, d.K, nst, lds, red);
+            if (d.in_kind != S_DIGITS) stage_digits(d.in_kind, d.in, d.K, nst, a.xs_off, lds, red);
             __syncthreads();
             stamp(g, M_DIGITS);
             // the next phase's LDS writes may start now if they stay above this phase's image
@@ -1031,7 +1033,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                              reinterpret_cast<const DigitTab*>(lds + (size_t)nst * 512), part, wave, lane);
                 __syncthreads();
             } else {
-                if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, nst, lane);
+                if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
                 if (pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 __syncthreads();
                 stamp(g, M_STREAMED);
@@ -1069,11 +1071,14 @@ uint32_t step_merge_chunks(uint32_t group, size_t lds) {
     return lds > out ? (uint32_t)((lds - out) / per) : 0u;
 }
 
+uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim) {
+    const uint32_t nst = std::max({(hidden + 127) / 128, (inter + 127) / 128, (q_dim + 127) / 128});
+    return (nst * 640 + 15) / 16 * 16;  // the largest digit image of any GEMV phase
+}
+
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group) {
-    const size_t nst_h = (hidden + 127) / 128, nst_i = (inter + 127) / 128, nst_q = (q_dim + 127) / 128;
-    size_t g = nst_h * 640 + (size_t)4 * hidden * 4;  // image + staging of a residual prologue
-    g = std::max(g, nst_i * 640);
-    g = std::max(g, nst_q * 640);
+    // images, then the staging of a residual prologue (x, res, two norm weight vectors)
+    const size_t g = step_xs_offset(hidden, inter, q_dim) + (size_t)4 * hidden * 4;
     const size_t att = group == 1 ? AttnLds<1>::bytes() : group == 2 ? AttnLds<2>::bytes() : AttnLds<4>::bytes();
     return std::max(g, att);
 }
