@@ -191,7 +191,8 @@ struct StepArgs {
     float* part;                    // attention chunk partials
     uint32_t* counters;             // attention merge tickets, one per KV head
     uint32_t* bar;                  // grid barrier words (kStepBarBytes, zero between launches)
-    const uint8_t* idle;            // 1152 readable bytes for placeholder weight loads
+    const uint8_t* stream;          // every GEMV weight record of a step, one run per streaming wave
+    const uint64_t* stream_off;     // [grid * kStepStreamWaves + 1] byte offset of each wave's run
     uint32_t cmax;                  // attention chunks per KV head (at most grid / kv_heads, and
                                     // what the merge can hold in LDS: step_merge_chunks)
     uint32_t advance;               // 1: move ST_POS on at the end (a step without the head)
@@ -211,10 +212,37 @@ constexpr uint32_t kStepMaxChunks = 256;  // chunks per KV head
 constexpr uint32_t kStepMaxUnits = 2;     // GEMV row units per workgroup (16 rows, 32 for gate/up)
 constexpr size_t kStepBarBytes = 32 * 10 * 4;
 
+// Weight stream of the step kernel.  A GEMV phase's rows are grouped in units (one 16-row tile;
+// for gate/up, tiles 2u, 2u + 1 of gate then of up: T = 4 tile streams per unit); workgroup b
+// takes units b, b + grid, ... (at most kStepMaxUnits), and its super-tiles, flattened as
+// f = (unit, tile stream, super-tile), go to streaming wave w = 1..7 for f = w - 1, w + 6, ...
+// Each (workgroup, wave) reads one contiguous run of records, every phase of every layer in
+// consume order; a record is one super-tile of one row tile: the 1024 code bytes of the tiled
+// Q4View layout followed by its 128 scale bytes.
+constexpr uint32_t kStepStreamWaves = 7;
+constexpr uint32_t kStepRecord = 1152;
+constexpr uint32_t kStepImg = 576;  // digit image bytes per super-tile: 512 digits + 4 block entries
+constexpr uint32_t kStepStreamPad = 64 * kStepRecord;  // readable bytes after the last run (ring over-read)
+
+__host__ __device__ inline uint32_t step_units(uint32_t units, uint32_t b, uint32_t grid) {
+    if (units <= b) return 0u;
+    const uint32_t n = (units - b + grid - 1) / grid;
+    return n < kStepMaxUnits ? n : kStepMaxUnits;
+}
+// Records of wave w (1..7) of workgroup b in a phase of `units` units, T tile streams, nst super-tiles.
+__host__ __device__ inline uint32_t step_wave_records(uint32_t units, uint32_t T, uint32_t nst, uint32_t b,
+                                                      uint32_t grid, uint32_t w) {
+    const uint32_t fe = step_units(units, b, grid) * T * nst;
+    return fe > w - 1 ? (fe - (w - 1) + kStepStreamWaves - 1) / kStepStreamWaves : 0u;
+}
+
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group);
 uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim);
 uint32_t step_merge_chunks(uint32_t group, size_t lds);  // chunk partials one merge holds in LDS
 hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid);
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s);
+// Fills the weight stream (StepArgs::stream at stream_off) from the layers' tiled Q4View matrices.
+hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint32_t grid, uint8_t* stream,
+                                const uint64_t* stream_off, hipStream_t s);
 
 }  // namespace af

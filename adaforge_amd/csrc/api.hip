@@ -738,7 +738,7 @@ struct af_session {
     uint32_t max_qkv = 0, max_q = 0, cmax = 0, head_blocks = 0;
     DevMem X, H, QKV, ATT, PROJ, ACT, D, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
     // persistent step kernel: layer table, digit images, barrier words
-    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, IDLE;
+    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
     bool use_step = true;     // all layers of a step in one cooperative launch
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
@@ -930,7 +930,8 @@ struct af_session {
         a.part = PART.as<float>();
         a.counters = COUNTERS.as<uint32_t>();
         a.bar = BAR.as<uint32_t>();
-        a.idle = IDLE.as<uint8_t>();
+        a.stream = STREAM.as<uint8_t>();
+        a.stream_off = STREAM_OFF.as<uint64_t>();
         a.cmax = step_cmax;
         a.xs_off = step_xs_offset(hidden, intermediate, max_q);
         a.advance = advance ? 1u : 0u;
@@ -1068,18 +1069,44 @@ int setup_step(af_session& s) {
     }
     int rc;
     if ((rc = dev_upload(s.STEP_LAYERS, table.data(), table.size() * sizeof(StepLayer), "layer table"))) return rc;
-    const size_t att_img = (size_t)((s.max_q / 32 + 3) / 4) * 640, act_img = (size_t)((s.intermediate / 32 + 3) / 4) * 640;
+    const size_t att_img = (size_t)((s.max_q / 32 + 3) / 4) * kStepImg,
+                 act_img = (size_t)((s.intermediate / 32 + 3) / 4) * kStepImg;
     if ((rc = dev_alloc(s.ATT_IMG, att_img, "digit image"))) return rc;
     if ((rc = dev_alloc(s.ACT_IMG, act_img, "digit image"))) return rc;
     if ((rc = dev_alloc(s.BAR, kStepBarBytes, "barrier words"))) return rc;
-    if ((rc = dev_alloc(s.IDLE, 1152, "placeholder tile"))) return rc;
-    HIP_OK(hipMemset(s.IDLE.p, 0, 1152), "placeholder tile clear");
     HIP_OK(hipMemset(s.ATT_IMG.p, 0, att_img), "digit image clear");
     HIP_OK(hipMemset(s.ACT_IMG.p, 0, act_img), "digit image clear");
     HIP_OK(hipMemset(s.BAR.p, 0, kStepBarBytes), "barrier clear");
     const size_t part = (size_t)grid * group * (256 + 2) * 4;
     if (s.PART.bytes < part) {
         if ((rc = dev_alloc(s.PART, part, "attention partials"))) return rc;
+    }
+    // The weight stream: each streaming wave's records, every phase of every layer in order, built
+    // on the device from the tiled matrices, which the step kernel then no longer needs.
+    const uint32_t nw = grid * kStepStreamWaves;
+    std::vector<uint64_t> off((size_t)nw + 1, 0);
+    for (uint32_t i = 0; i < nw; ++i) {
+        const uint32_t b = i / kStepStreamWaves, w = i % kStepStreamWaves + 1;
+        uint64_t recs = 0;
+        for (const LayerDev& L : s.layers) {
+            recs += step_wave_records((L.qkv.rows + 15) / 16, 1, (L.qkv.columns / 32 + 3) / 4, b, grid, w);
+            recs += step_wave_records((L.o.rows + 15) / 16, 1, (L.o.columns / 32 + 3) / 4, b, grid, w);
+            recs += step_wave_records((L.gate.rows + 31) / 32, 4, (L.gate.columns / 32 + 3) / 4, b, grid, w);
+            recs += step_wave_records((L.down.rows + 15) / 16, 1, (L.down.columns / 32 + 3) / 4, b, grid, w);
+        }
+        off[i + 1] = off[i] + recs * kStepRecord;
+    }
+    if ((rc = dev_upload(s.STREAM_OFF, off.data(), off.size() * 8, "weight stream offsets"))) return rc;
+    if ((rc = dev_alloc(s.STREAM, off.back() + kStepStreamPad, "weight stream"))) return rc;
+    HIP_OK(hipMemset(s.STREAM.as<uint8_t>() + off.back(), 0, kStepStreamPad), "weight stream padding");
+    HIP_OK(launch_stream_repack(s.STEP_LAYERS.as<StepLayer>(), (uint32_t)s.layers.size(), grid, s.STREAM.as<uint8_t>(),
+                                s.STREAM_OFF.as<uint64_t>(), nullptr),
+           "weight stream build");
+    HIP_OK(hipDeviceSynchronize(), "weight stream build");
+    for (LayerDev& L : s.layers) {
+        L.qkv.codes.reset(), L.qkv.scales.reset(), L.o.codes.reset(), L.o.scales.reset();
+        L.gate.codes.reset(), L.gate.scales.reset(), L.up.codes.reset(), L.up.scales.reset();
+        L.down.codes.reset(), L.down.scales.reset();
     }
     return AF_OK;
 }

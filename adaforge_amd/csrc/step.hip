@@ -28,9 +28,10 @@ namespace af {
 namespace {
 
 constexpr uint32_t kThreads = 512;
-constexpr uint32_t kStreamWaves = 7;  // waves 1..7 stream weights
-constexpr int kAhead = 8;             // Q4 super-tiles in flight per streaming wave
+constexpr uint32_t kStreamWaves = kStepStreamWaves;  // waves 1..7 stream weights
+constexpr int kRing = 8;              // weight records in flight per streaming wave
 constexpr int kSC1 = 16;              // cache policy: agent-scope coherent access
+constexpr int kNT = 2;                // cache policy: non-temporal (weights are read once per step)
 constexpr int kVmWait = 0x0F70;       // s_waitcnt vmcnt(0) with expcnt / lgkmcnt unconstrained
 constexpr uint32_t kSpinLimit = 1u << 21;
 constexpr uint32_t kMaxUnits = kStepMaxUnits;
@@ -142,53 +143,10 @@ __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance
 
 // ---- GEMV phases --------------------------------------------------------------------------------
 
-// Rows are grouped into units: one 16-row tile (T = 1), or two tiles of two matrices (T = 4:
-// gate tiles 2u, 2u + 1 then up tiles 2u, 2u + 1).  Workgroup b takes units b, b + G, ...
-// (at most kMaxUnits); its super-tile work, flattened as (unit, tile stream, super-tile), is
-// dealt round-robin to the streaming waves: wave w takes w - 1, w - 1 + 7, ...  Every wave thus
-// streams from every row tile of the workgroup (a contiguous split leaves whole matrices, and
-// whatever memory channels they sit on, to single waves, which then finish unevenly), and still
-// visits each row tile in one run, so it leaves one partial row sum per row tile.
-struct Job {
-    const uint4* codes[2];
-    const uint2* scales[2];
-    uint32_t nst, units, T;
+// Shape of a GEMV phase: units of T tile streams of nst super-tiles (StepArgs::stream).
+struct Shape {
+    uint32_t nst, T, units;
 };
-
-struct Cur {
-    uint32_t f, st, ts, k;
-};
-
-__device__ __forceinline__ Cur cur_at(uint32_t f, uint32_t nst, uint32_t T) {
-    const uint32_t seg = f / nst;
-    return Cur{f, f - seg * nst, seg % T, seg / T};
-}
-
-// The wave's next super-tile: kStreamWaves further on.
-__device__ __forceinline__ void cur_next(Cur& c, uint32_t nst, uint32_t T) {
-    c.f += kStreamWaves;
-    c.st += kStreamWaves;
-    while (c.st >= nst) {
-        c.st -= nst;
-        if (++c.ts == T) {
-            c.ts = 0;
-            ++c.k;
-        }
-    }
-}
-
-__device__ __forceinline__ uint32_t my_units(uint32_t units) {
-    return units > blockIdx.x ? min(kMaxUnits, (units - blockIdx.x + gridDim.x - 1) / gridDim.x) : 0u;
-}
-
-// This streaming wave's share of a job's flattened super-tiles: fb, fb + 7, ... below fe, n of
-// them.
-__device__ __forceinline__ void wave_share(const Job& j, uint32_t wave, uint32_t& fb, uint32_t& fe, uint32_t& n) {
-    // wave-uniform values: readfirstlane keeps the cursors (and all control flow on them) scalar
-    fe = __builtin_amdgcn_readfirstlane(my_units(j.units) * j.T * j.nst);
-    fb = wave - 1;
-    n = fe > fb ? (fe - fb + kStreamWaves - 1) / kStreamWaves : 0u;
-}
 
 __device__ __forceinline__ void zero_part_lds(float* part, uint32_t tid) {
     for (uint32_t i = tid; i < kMaxUnits * kMaxT * 8 * 16; i += kThreads) part[i] = 0.0f;
@@ -202,7 +160,198 @@ __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_
     return v;
 }
 
-// Input prologue of a GEMV phase: LDS layout [digit image nst * 640] ... and, at StepArgs::xs_off
+// Digit image of a GEMV input, nst * kStepImg bytes: the digit planes dig[b * 4 + t][32] of
+// block b (nst * 512 bytes), then one entry per block: for x_j = s (q0 + q1 2^-7 + q2 2^-14 +
+// q3 2^-21), s = 2^(ilogb(max |x|) - 5), the scales s 2^-14 and s 2^-21 and -8 sum_j x_j.
+struct alignas(16) BlockTab {
+    float s14, s21, nbias, pad;
+};
+
+__device__ __forceinline__ BlockTab block_tab(float m, float sum) {
+    const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
+    return BlockTab{ldexpf(s, -14), ldexpf(s, -21), -8.0f * sum, 0.0f};
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+template <typename T>
+__device__ __forceinline__ T lds_at(uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((const lds_u8*)p);
+}
+
+// A streaming wave's weight records: a ring of kRing in registers, refilled from the wave's run
+// as each is consumed, across phase (and layer) boundaries: the next phase's first records are
+// in flight while this one finishes and during the barrier and prologue in between.  Slot
+// `slot` holds the next record to consume.
+static_assert(kRing * kStepRecord <= kStepStreamPad, "stream padding below the ring's over-read");
+struct Ring {
+    v4u code[kRing];
+    uint32_t scale[kRing];
+    uint32_t base_lo, base_hi, len;  // the wave's run (wave-uniform)
+    uint32_t soff;                   // byte offset of the next record to request
+    uint32_t slot;
+};
+
+// Buffer view of the wave's run.  Built from readfirstlane values so that the descriptor is known
+// to be wave-uniform (scalar registers); readfirstlane returns int, so each half is taken as
+// unsigned before the halves are joined.  The record offset goes in soffset, which the range
+// check does not cover: the ring's last refills read up to kRing records past the run, which the
+// allocation's padding (kStepStreamPad) keeps inside it.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ring_rsrc(const Ring& r) {
+    const uint64_t p = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(r.base_hi) << 32) |
+                       (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(r.base_lo);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(p), 0, (int)__builtin_amdgcn_readfirstlane(r.len),
+                                             0x00020000);
+}
+
+__device__ __forceinline__ void ring_fill(Ring& r, const __amdgpu_buffer_rsrc_t& rs, int u, uint32_t lane) {
+    r.code[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, lane * 16, r.soff, kNT);
+    r.scale[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, 1024 + lane * 2, r.soff, kNT);
+    r.soff += kStepRecord;
+}
+
+// Rotates the ring so that the next record to consume is in slot 0 (register moves only; the
+// caller has waited for every load in flight).
+template <int S>
+__device__ __forceinline__ void ring_rotate_by(Ring& r) {
+    v4u c[kRing];
+    uint32_t q[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) {
+        c[i] = r.code[(i + S) % kRing];
+        q[i] = r.scale[(i + S) % kRing];
+    }
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) {
+        r.code[i] = c[i];
+        r.scale[i] = q[i];
+    }
+}
+template <int S = 1>
+__device__ __forceinline__ void ring_rotate(Ring& r) {
+    if constexpr (S < kRing) {
+        if (r.slot == S) ring_rotate_by<S>(r);
+        else ring_rotate<S + 1>(r);
+    }
+}
+
+// Per-lane constants of the matrix-core step.  The MFMA computes D = A B with A = the input's
+// digit planes (row m = 4 g + t: digit t of block g of the super-tile; k-group g of lane
+// (m, g) holds the block's 16 digits when g == m / 4, zeros otherwise) and B = the 16 code
+// bytes of (block g, row r) at lane 16 g + r (low nibbles in one MFMA against elements 0..15,
+// high nibbles in a second against 16..31).  Lane l then holds D[4 q + i][r] for digit i of
+// block q = l / 16 and row r = l % 16, which it folds with its one block scale d(r, q).
+struct LaneK {
+    uint32_t aoff;   // active A lanes: byte offset of their digit plane within a super-tile image
+    uint32_t ainc;   // 7 super-tiles of digits for active lanes, 0 for the others
+    uint32_t zero;   // LDS address of 32 zero bytes (inactive A lanes)
+    uint32_t q16;    // block entry of the lane's output block within a super-tile
+    bool aon;
+};
+
+__device__ __forceinline__ LaneK lane_k(uint32_t lane, uint32_t zero) {
+    LaneK k;
+    k.aon = ((lane & 15) >> 2) == (lane >> 4);
+    k.aoff = (lane & 15) * 32;
+    k.ainc = k.aon ? 7u * 512u : 0u;
+    k.zero = zero;
+    k.q16 = (lane >> 4) * 16;
+    return k;
+}
+
+// Flattened super-tile f of a phase -> (super-tile st, tile stream ts, unit k).  rcp =
+// ceil(2^32 / nst), exact for f * nst < 2^32 (f < 2 units * 4 * nst here); T is 1 or 4.
+__device__ __forceinline__ void split_f(uint32_t f, uint32_t nst, uint32_t rcp, uint32_t T, uint32_t& st,
+                                        uint32_t& ts, uint32_t& k) {
+    const uint32_t seg = __umulhi(f, rcp);
+    st = f - seg * nst;
+    ts = seg & (T - 1);
+    k = T == 1 ? seg : seg >> 2;
+}
+
+// Run state of a wave inside a GEMV phase: a run is the wave's super-tiles of one row tile (st,
+// st + 7, ... below nst); f is the flattened index of the next run's first super-tile.
+struct RunState {
+    uint32_t f, n, adig, toff, pidx;
+    float acc;
+};
+
+__device__ __forceinline__ void run_start(RunState& s, uint32_t nst, uint32_t rcp, uint32_t T, uint32_t fe,
+                                          uint32_t img, uint32_t wave, uint32_t lane, const LaneK& lk) {
+    uint32_t st, ts, k;
+    split_f(s.f, nst, rcp, T, st, ts, k);
+    s.n = min((nst - st + 6) / 7, (fe - s.f + 6) / 7);
+    s.f += 7 * s.n;
+    s.adig = lk.aon ? img + st * 512 + lk.aoff : lk.zero;
+    s.toff = img + nst * 512 + st * 64 + lk.q16;
+    s.pidx = ((k * kMaxT + ts) * 8 + wave) * 16 + lane;
+}
+
+// One record: two int8 MFMAs against the digit image, the fold into the row partial, the refill of
+// the slot, and at a run's end the row partials into part.
+__device__ __forceinline__ void consume_record(Ring& r, const __amdgpu_buffer_rsrc_t& rs, int u, RunState& s,
+                                               uint32_t nst, uint32_t rcp, uint32_t T, uint32_t fe, uint32_t img,
+                                               float* part, uint32_t wave, uint32_t lane, const LaneK& lk) {
+    const v4u c = r.code[u];
+    const uint32_t sc = r.scale[u];
+    constexpr uint32_t M = 0x0F0F0F0Fu;
+    const v4i zero4 = {0, 0, 0, 0};
+    const v4i bl = {(int)(c.x & M), (int)(c.y & M), (int)(c.z & M), (int)(c.w & M)};
+    const v4i bh = {(int)((c.x >> 4) & M), (int)((c.y >> 4) & M), (int)((c.z >> 4) & M), (int)((c.w >> 4) & M)};
+    const v4i al = lds_at<v4i>(s.adig), ah = lds_at<v4i>(s.adig + 16);
+    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl, zero4, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh, d, 0, 0, 0);
+    const v4f tb = lds_at<v4f>(s.toff);  // BlockTab: s14, s21, nbias
+    // 2^14 D0 + 2^7 D1 + D2 is exact in int32 (|D_t| <= 32 * 15 * 64)
+    const int I = (d[0] << 14) + (d[1] << 7) + d[2];
+    float in = fmaf((float)I, tb.x, tb.z);
+    in = fmaf((float)d[3], tb.y, in);
+    s.acc = fmaf(h2f((uint16_t)sc), in, s.acc);
+    ring_fill(r, rs, u, lane);  // after the last use of the slot's registers
+    s.adig += lk.ainc;
+    s.toff += 7 * 64;
+    if (--s.n == 0) {  // the run's last super-tile: one partial per row
+        float v = s.acc + __shfl_xor(s.acc, 16);
+        v += __shfl_xor(v, 32);
+        if (lane < 16) part[s.pidx] = v;
+        s.acc = 0.0f;
+        if (s.f < fe) run_start(s, nst, rcp, T, fe, img, wave, lane, lk);
+    }
+}
+
+// Consumes this wave's records of a GEMV phase (fe = the workgroup's flattened super-tiles) and
+// leaves one partial per row, per (unit k, tile stream ts) it visits, in part[(k kMaxT + ts) 8 +
+// wave][16].  img: LDS address of the phase's digit image.  Whole rounds of kRing records run
+// without an exit test (exact waits: slot u's loads are followed by those of the kRing - 1 slots
+// after it), then a tail of fewer than kRing.
+__device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T, uint32_t fe, uint32_t img,
+                                              float* part, uint32_t wave, uint32_t lane, const LaneK& lk) {
+    if (wave - 1 >= fe) return;
+    wait_vm();  // every record in flight was requested before this phase's barrier
+    ring_rotate(r);
+    const __amdgpu_buffer_rsrc_t rs = ring_rsrc(r);
+    r.soff = __builtin_amdgcn_readfirstlane(r.soff);
+    const uint32_t rcp = (uint32_t)((0xFFFFFFFFull + nst) / nst);
+    const uint32_t total = (fe - (wave - 1) + 6) / 7;
+    RunState s;
+    s.f = wave - 1;
+    s.acc = 0.0f;
+    run_start(s, nst, rcp, T, fe, img, wave, lane, lk);
+    for (uint32_t rounds = total / kRing; rounds; --rounds) {
+#pragma unroll
+        for (int u = 0; u < kRing; ++u) consume_record(r, rs, u, s, nst, rcp, T, fe, img, part, wave, lane, lk);
+    }
+    const uint32_t rem = total % kRing;
+#pragma unroll
+    for (int u = 0; u < kRing - 1; ++u)
+        if ((uint32_t)u < rem) consume_record(r, rs, u, s, nst, rcp, T, fe, img, part, wave, lane, lk);
+    r.slot = rem;
+}
+
+// Input prologue of a GEMV phase: LDS layout [digit image nst * kStepImg] ... and, at StepArgs::xs_off
 // (above the largest image of any phase, so the next phase's norm weights can be copied in while
 // this phase's image is in use), [x K][res K][w_a K][w_n K] (floats).  Wave 0 stages, every
 // thread then builds the digit image.
@@ -223,7 +372,7 @@ __device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const In
     uint8_t* img = lds;
     float* xs = reinterpret_cast<float*>(lds + xs_off);
     if (kind == S_DIGITS) {
-        dma(in.dig, nst * 640, img, lane);
+        dma(in.dig, nst * kStepImg, img, lane);
     } else if (kind == S_RESID) {
         dma(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), lane);
         dma(in.res, K * 4, reinterpret_cast<uint8_t*>(xs + K), lane);
@@ -267,7 +416,7 @@ __device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
 __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t K, uint32_t nst, uint32_t xs_off,
                                              uint8_t* lds, double* red) {
     int8_t* dig = reinterpret_cast<int8_t*>(lds);
-    DigitTab* tab = reinterpret_cast<DigitTab*>(lds + (size_t)nst * 512);
+    BlockTab* tab = reinterpret_cast<BlockTab*>(lds + (size_t)nst * 512);
     float* xs = reinterpret_cast<float*>(lds + xs_off);
     const uint32_t tid = threadIdx.x, n8 = K / 8, o = tid;
     const bool ok = o < n8;
@@ -311,7 +460,7 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t
     const uint32_t b = o >> 2, p = o & 3;
     if (b < nst * 4) {
         digits8(v, m, dig, b, p);
-        if (p == 0) digit_tab(tab, b, m, sum);
+        if (p == 0) tab[b] = block_tab(m, sum);
     }
 }
 
@@ -326,14 +475,9 @@ __device__ __forceinline__ void quad_digits_store(const float (&v)[8], int8_t* i
 #pragma unroll
     for (int t = 0; t < 4; ++t) stc8(img, (b * 4 + t) * 32 + 8 * p, v2u{w[t][0], w[t][1]});
     if (p == 0) {
-        DigitTab e[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) e[t] = digit_entry(m, sum, t);
-        const uint32_t base = nst * 512 + b * 32;
-        stc16(img, base, v4u{__float_as_uint(e[0].scale), __float_as_uint(e[0].bias), __float_as_uint(e[1].scale),
-                             __float_as_uint(e[1].bias)});
-        stc16(img, base + 16, v4u{__float_as_uint(e[2].scale), __float_as_uint(e[2].bias),
-                                  __float_as_uint(e[3].scale), __float_as_uint(e[3].bias)});
+        const BlockTab e = block_tab(m, sum);
+        stc16(img, nst * 512 + b * 16,
+              v4u{__float_as_uint(e.s14), __float_as_uint(e.s21), __float_as_uint(e.nbias), 0u});
     }
 }
 
@@ -694,7 +838,7 @@ enum PhaseKind { P_QKV = 0, P_ATTN, P_OPROJ, P_GATEUP, P_DOWN, kPhases };
 
 // One GEMV phase of a layer, read from the layer table.
 struct Gemv {
-    Job job;
+    Shape sh;
     int in_kind;     // S_EMBED, S_RESID or S_DIGITS
     Stage in;
     InputStage emb;  // S_EMBED
@@ -704,45 +848,19 @@ struct Gemv {
     uint32_t act_nst;
 };
 
-__device__ __forceinline__ const void* uniform_ptr(const void* p) {
-    const uint64_t v = reinterpret_cast<uint64_t>(p);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v), hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
-    return reinterpret_cast<const void*>(((uint64_t)hi << 32) | lo);
-}
-
-__device__ __forceinline__ Job make_job(CQ4View& m0, CQ4View* m1) {
-    Job j{};
-    j.codes[0] = reinterpret_cast<const uint4*>(m0.codes);
-    j.scales[0] = reinterpret_cast<const uint2*>(m0.scales);
-    if (m1) {
-        j.codes[1] = reinterpret_cast<const uint4*>(m1->codes);
-        j.scales[1] = reinterpret_cast<const uint2*>(m1->scales);
-        j.units = (m0.rows + 31) / 32;
-        j.T = 4;
-    } else {
-        j.codes[1] = j.codes[0];
-        j.scales[1] = j.scales[0];
-        j.units = (m0.rows + 15) / 16;
-        j.T = 1;
-    }
-    j.nst = m0.nst;
-    // every field is wave-uniform; readfirstlane puts the job in scalar registers so the stream
-    // cursors derived from it, and the branches on them, stay scalar
-    for (int i = 0; i < 2; ++i) {
-        j.codes[i] = reinterpret_cast<const uint4*>(uniform_ptr(j.codes[i]));
-        j.scales[i] = reinterpret_cast<const uint2*>(uniform_ptr(j.scales[i]));
-    }
-    j.units = __builtin_amdgcn_readfirstlane(j.units);
-    j.T = __builtin_amdgcn_readfirstlane(j.T);
-    j.nst = __builtin_amdgcn_readfirstlane(j.nst);
-    return j;
+__device__ __forceinline__ Shape shape_of(CQ4View& m, bool pair) {
+    Shape sh;
+    sh.nst = __builtin_amdgcn_readfirstlane(m.nst);
+    sh.T = pair ? 4u : 1u;
+    sh.units = __builtin_amdgcn_readfirstlane(pair ? (m.rows + 31) / 32 : (m.rows + 15) / 16);
+    return sh;
 }
 
 __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t kind) {
     CLayer& L = layer_at(a, l);
     Gemv d{};
     if (kind == P_QKV) {
-        d.job = make_job(L.qkv, nullptr);
+        d.sh = shape_of(L.qkv, false);
         d.K = a.hidden;
         d.y = a.QKV;
         d.rows = L.qkv.rows;
@@ -766,14 +884,14 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         d.in.eps_n = L.input_eps;
         d.in.x_out = a.X;
     } else if (kind == P_OPROJ) {
-        d.job = make_job(L.o, nullptr);
+        d.sh = shape_of(L.o, false);
         d.in_kind = S_DIGITS;
         d.in.dig = a.att_img;
         d.K = L.o.blocks * 32;
         d.y = a.PROJ;
         d.rows = L.o.rows;
     } else if (kind == P_GATEUP) {
-        d.job = make_job(L.gate, &L.up);
+        d.sh = shape_of(L.gate, true);
         d.in_kind = S_RESID;
         d.in.x = a.PROJ;
         d.in.res = a.X;
@@ -786,7 +904,7 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         d.K = a.hidden;
         d.act_nst = L.down.nst;
     } else {
-        d.job = make_job(L.down, nullptr);
+        d.sh = shape_of(L.down, false);
         d.in_kind = S_DIGITS;
         d.in.dig = a.act_img;
         d.K = a.inter;
@@ -812,120 +930,6 @@ __device__ __forceinline__ AttnGeo attn_geo(CLayer& L, uint32_t pos, uint32_t cm
     g.chunks = (nvis + g.clen - 1) / g.clen;
     g.items = L.kv_heads * g.chunks;
     return g;
-}
-
-// The job of GEMV phase ph.
-__device__ __forceinline__ Job phase_job(const StepArgs& a, uint32_t ph) {
-    ph = __builtin_amdgcn_readfirstlane(ph);  // wave-uniform by construction; say so
-    CLayer& L = layer_at(a, ph / kPhases);
-    const uint32_t kind = ph % kPhases;
-    if (kind == P_QKV) return make_job(L.qkv, nullptr);
-    if (kind == P_OPROJ) return make_job(L.o, nullptr);
-    if (kind == P_GATEUP) return make_job(L.gate, &L.up);
-    return make_job(L.down, nullptr);
-}
-
-// A streaming wave's weight stream over the whole step: its share of every GEMV phase in order,
-// each share padded with placeholder tiles to a multiple of kAhead so that every phase starts
-// in ring slot 0.  Ring slot u holds stream tile u mod kAhead; a consumed slot is refilled at
-// once with the tile kAhead further on, across phase boundaries, so the next phase's first
-// tiles are in flight while this one finishes and the ring never drains inside the launch.
-struct Seek {
-    Job job;   // the phase being loaded
-    Cur ld;    // its next tile
-    uint32_t fe;   // end of this wave's share
-    uint32_t pad;  // placeholders still to issue after the share
-    int32_t ph;    // the phase (n_phases once every phase is issued)
-};
-struct Ring : Seek {
-    Seek nx;      // where the loads go after phase ph (prepared by ring_prepare)
-    int32_t nx_for;  // the ph that nx follows
-};
-
-// The first phase at or after ph with tiles for this wave.  Reads the layer table (scalar loads).
-__device__ __forceinline__ Seek seek_from(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t wave) {
-    Seek s{};
-    for (; ph < n_phases; ++ph) {
-        if ((uint32_t)ph % kPhases == P_ATTN) continue;
-        s.job = phase_job(a, (uint32_t)ph);
-        uint32_t fb, n;
-        wave_share(s.job, wave, fb, s.fe, n);
-        if (n) {
-            s.ld = cur_at(fb, s.job.nst, s.job.T);
-            s.pad = (kAhead - n % kAhead) % kAhead;
-            s.ph = __builtin_amdgcn_readfirstlane(ph);
-            return s;
-        }
-    }
-    s.ph = n_phases;
-    s.pad = 0;
-    return s;
-}
-
-// Streaming waves, at the start of every GEMV phase (while wave 0 stages the inputs): where the
-// loads go once the current phase's share is issued.  The ring switches to it inside the consume
-// loop with no memory access: a scalar load in flight there would make the next LDS read wait
-// for it (scalar loads may return out of order, so the compiler waits for all of them at once).
-__device__ __forceinline__ void ring_prepare(const StepArgs& a, Ring& r, int32_t n_phases, uint32_t wave) {
-    if (r.nx_for != r.ph) {
-        r.nx = seek_from(a, r.ph + 1, n_phases, wave);
-        r.nx_for = r.ph;
-    }
-}
-
-// Shares are padded to multiples of kAhead and the loads run exactly kAhead tiles ahead, so a
-// round of kAhead refills never crosses a phase boundary: the switch happens once per round.
-__device__ __forceinline__ void ring_round(Ring& r, int32_t n_phases) {
-    if (r.ph < n_phases && r.ld.f >= r.fe && r.pad == 0) static_cast<Seek&>(r) = r.nx;
-}
-
-// Issues the next stream tile into t.  One load pair either way, addresses chosen by selects (a
-// placeholder reads the idle buffer, which stays in L2): with no branch around the loads the
-// compiler waits for exactly the slot being consumed.
-__device__ __forceinline__ void ring_issue(const StepArgs& a, Ring& r, int32_t n_phases, uint32_t lane, Q4Tile& t) {
-    const bool real = r.ph < n_phases && r.ld.f < r.fe;
-    const Job& j = r.job;
-    const bool second = j.T == 4 && (r.ld.ts >> 1) != 0;
-    const size_t tile = !real ? 0 : j.T == 4 ? (size_t)(blockIdx.x + r.ld.k * gridDim.x) * 2 + (r.ld.ts & 1)
-                                             : (size_t)(blockIdx.x + r.ld.k * gridDim.x);
-    const uint4* codes = !real ? reinterpret_cast<const uint4*>(a.idle) : second ? j.codes[1] : j.codes[0];
-    const uint2* scales = !real ? reinterpret_cast<const uint2*>(a.idle + 1024) : second ? j.scales[1] : j.scales[0];
-    q4_tile_load(codes, scales, tile, j.nst, real ? r.ld.st : 0u, lane, t);
-    if (real) cur_next(r.ld, j.nst, j.T);
-    else if (r.pad) --r.pad;
-}
-
-// Consumes this wave's share of a GEMV phase from the ring (refilling every slot it visits) and
-// leaves one partial row sum per (unit, tile, wave) in part[(k * kMaxT + ts) * 8 + wave][16].
-__device__ __forceinline__ void ring_consume(const StepArgs& a, const Job& j, Ring& r, int32_t n_phases,
-                                             Q4Tile (&buf)[kAhead], const int8_t* dig, const DigitTab* tab,
-                                             float* part, uint32_t wave, uint32_t lane) {
-    uint32_t fb, fe, n;
-    wave_share(j, wave, fb, fe, n);
-    if (!n) return;  // no tiles here, and none in the stream for this phase
-    Cur cs = cur_at(fb, j.nst, j.T);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t base = 0; base < n; base += kAhead) {
-        ring_round(r, n_phases);
-#pragma unroll
-        for (int u = 0; u < kAhead; ++u) {
-            if (base + u < n) {
-                q4_mfma_tile(buf[u], cs.st, dig, tab, lane, acc);
-                if (cs.st + kStreamWaves >= j.nst || cs.f + kStreamWaves >= fe) {  // the run's last tile
-                    q4_row_sums(acc);
-                    if ((lane & 15) == 0) {
-                        float* p = part + ((cs.k * kMaxT + cs.ts) * 8 + wave) * 16 + 4 * (lane >> 4);
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) p[i] = acc[i];
-                    }
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i] = 0.0f;
-                }
-                cur_next(cs, j.nst, j.T);
-            }
-            ring_issue(a, r, n_phases, lane, buf[u]);
-        }
-    }
 }
 
 }  // namespace
@@ -985,14 +989,22 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     stamp(g, M_START);
     bool failed = false;
     const int32_t n_phases = (int32_t)(kPhases * a.n_layers);
-    Q4Tile buf[kAhead];
-    Ring r{};
+    __shared__ uint4 zero_blk[2];
+    if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);  // read after the first __syncthreads
+    Ring r;
+    const LaneK lk = lane_k(lane, lds_addr(zero_blk));
     if (wave != 0) {
-        static_cast<Seek&>(r) = seek_from(a, 0, n_phases, wave);
-        r.nx_for = -1;
-        ring_prepare(a, r, n_phases, wave);
+        const uint32_t w = blockIdx.x * kStreamWaves + (wave - 1);
+        const uint64_t o0 = a.stream_off[w], o1 = a.stream_off[w + 1];
+        const uint64_t base = reinterpret_cast<uint64_t>(a.stream) + o0;
+        r.base_lo = (uint32_t)base;
+        r.base_hi = (uint32_t)(base >> 32);
+        r.len = (uint32_t)(o1 - o0);
+        r.soff = 0;
+        r.slot = 0;
+        const __amdgpu_buffer_rsrc_t rs = ring_rsrc(r);
 #pragma unroll
-        for (int u = 0; u < kAhead; ++u) ring_issue(a, r, n_phases, lane, buf[u]);
+        for (int u = 0; u < kRing; ++u) ring_fill(r, rs, u, lane);
     } else {
         phase_pre<GQ>(a, 0, n_phases, pos, lds, lane);
         wait_vm();
@@ -1015,9 +1027,8 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             stamp(g, M_STORED);
         } else {
             const Gemv d = describe(a, l, kind);
-            const uint32_t nst = d.job.nst;
+            const uint32_t nst = d.sh.nst;
             if (wave == 0) stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, a.xs_off, lds, lane);
-            else ring_prepare(a, r, n_phases, wave);
             __syncthreads();
             stamp(g, M_STAGED);
             zero_part_lds(part, tid);
@@ -1025,12 +1036,13 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             __syncthreads();
             stamp(g, M_DIGITS);
             // the next phase's LDS writes may start now if they stay above this phase's image
-            const bool pre_now = phase_pre_low<GQ>(a, ph + 1, n_phases) >= (size_t)nst * 640;
+            const bool pre_now = phase_pre_low<GQ>(a, ph + 1, n_phases) >= (size_t)nst * kStepImg;
             // Each role's code up to its last global access of the phase is one branch, so the
             // compiler's wait model never mixes wave 0's copies into the streaming waves'.
             if (wave != 0) {
-                ring_consume(a, d.job, r, n_phases, buf, reinterpret_cast<const int8_t*>(lds),
-                             reinterpret_cast<const DigitTab*>(lds + (size_t)nst * 512), part, wave, lane);
+                const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
+                consume_phase(r, nst, d.sh.T, __builtin_amdgcn_readfirstlane(fe), lds_addr(lds), part, wave, lane,
+                              lk);
                 __syncthreads();
             } else {
                 if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
@@ -1038,7 +1050,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 __syncthreads();
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
-                const uint32_t mu = my_units(d.job.units);
+                const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
                 if (d.y) {
                     if (tid < 16 * mu) {
                         const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
@@ -1066,6 +1078,50 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     grid_exit(g, a.state, a.advance != 0, failed);
 }
 
+// One workgroup per (workgroup b, streaming wave w) of the step grid, block b * 7 + w - 1: copies
+// that wave's records, every GEMV phase of every layer in consume order, from the layers' tiled
+// matrices into its run (a unit past the last row tile reads as zero weights).
+__global__ __launch_bounds__(256) void stream_repack_kernel(const StepLayer* layers, uint32_t n_layers, uint32_t grid,
+                                                            uint8_t* stream, const uint64_t* off) {
+    const uint32_t b = blockIdx.x / kStreamWaves, w = blockIdx.x % kStreamWaves + 1;
+    uint4* dst = reinterpret_cast<uint4*>(stream + off[blockIdx.x]);
+    constexpr uint32_t kChunks = kStepRecord / 16;  // 64 code chunks, then 8 scale chunks
+    constexpr uint32_t kPer = 256 / kChunks;        // records per pass
+    for (uint32_t l = 0; l < n_layers; ++l) {
+        const StepLayer& L = layers[l];
+        for (uint32_t kind = 0; kind < 4; ++kind) {
+            const Q4View& m0 = kind == 0 ? L.qkv : kind == 1 ? L.o : kind == 2 ? L.gate : L.down;
+            const bool pair = kind == 2;
+            const uint32_t nst = m0.nst, T = pair ? 4u : 1u, tiles = (m0.rows + 15) / 16;
+            const uint32_t units = pair ? (m0.rows + 31) / 32 : tiles;
+            const uint32_t n = step_wave_records(units, T, nst, b, grid, w);
+            for (uint32_t j0 = 0; j0 < n; j0 += kPer) {
+                const uint32_t j = j0 + threadIdx.x / kChunks, c = threadIdx.x % kChunks;
+                if (threadIdx.x < kPer * kChunks && j < n) {
+                    const uint32_t f = w - 1 + kStreamWaves * j, seg = f / nst, st = f % nst, ts = seg % T, k = seg / T;
+                    const uint32_t u = b + k * grid;
+                    const Q4View& m = pair && ts >= 2 ? L.up : m0;
+                    const uint32_t tile = pair ? 2 * u + (ts & 1) : u;
+                    const size_t src = (size_t)tile * nst + st;
+                    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+                    if (tile < tiles)
+                        v = c < 64 ? reinterpret_cast<const uint4*>(m.codes)[src * 64 + c]
+                                   : reinterpret_cast<const uint4*>(m.scales)[src * 8 + (c - 64)];
+                    dst[(size_t)j * kChunks + c] = v;
+                }
+            }
+            dst += (size_t)n * kChunks;
+        }
+    }
+}
+
+hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint32_t grid, uint8_t* stream,
+                                const uint64_t* stream_off, hipStream_t s) {
+    hipLaunchKernelGGL(stream_repack_kernel, dim3(grid * kStreamWaves), dim3(256), 0, s, layers, n_layers, grid, stream,
+                       stream_off);
+    return hipGetLastError();
+}
+
 uint32_t step_merge_chunks(uint32_t group, size_t lds) {
     const size_t out = (size_t)group * 256 * 4, per = (size_t)group * 258 * 4;
     return lds > out ? (uint32_t)((lds - out) / per) : 0u;
@@ -1073,7 +1129,7 @@ uint32_t step_merge_chunks(uint32_t group, size_t lds) {
 
 uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim) {
     const uint32_t nst = std::max({(hidden + 127) / 128, (inter + 127) / 128, (q_dim + 127) / 128});
-    return (nst * 640 + 15) / 16 * 16;  // the largest digit image of any GEMV phase
+    return (nst * kStepImg + 15) / 16 * 16;  // the largest digit image of any GEMV phase
 }
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group) {
