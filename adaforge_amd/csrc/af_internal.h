@@ -204,8 +204,10 @@ struct StepArgs {
 
 // Timeline marks of a phase (workgroup's thread 0): start (barrier departure or kernel start),
 // inputs staged, digit image built, weights streamed, outputs stored, arrival at the closing
-// barrier (or kernel end), and the pre-barrier work of the next phase done.
-enum StepMark { M_START = 0, M_STAGED, M_DIGITS, M_STREAMED, M_STORED, M_ARRIVE, M_PRE, kStepMarks = 8 };
+// barrier (or kernel end), the pre-barrier work of the next phase done, and (wave 1) its weight
+// records consumed.  An attention phase marks: q/k/v staged, chunk partial computed, partial
+// published (ticket taken), merge done.
+enum StepMark { M_START = 0, M_STAGED, M_DIGITS, M_STREAMED, M_STORED, M_ARRIVE, M_PRE, M_CONSUMED, kStepMarks = 8 };
 
 constexpr uint32_t kStepMaxClen = 2048;   // tokens per attention chunk
 constexpr uint32_t kStepMaxChunks = 256;  // chunks per KV head

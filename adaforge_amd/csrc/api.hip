@@ -1432,8 +1432,8 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
         HIP_OK(hipMemcpy(clk.data(), s->CLOCK.p, clk.size() * 8, hipMemcpyDeviceToHost), "timeline download");
         const uint32_t G = s->step_grid, nb = s->barriers();
         const double tick_ms = 1e-5;  // 100 MHz
-        static const char* const kMarkNames[kStepMarks] = {"start", "stage", "digits", "stream", "store", "tail", "pre", ""};
-        static const int kOrder[] = {M_START, M_STAGED, M_DIGITS, M_STREAMED, M_STORED, M_PRE, M_ARRIVE};
+        static const char* const kMarkNames[kStepMarks] = {"start", "stage", "digits", "stream", "store", "tail", "pre", "consume"};
+        static const int kOrder[] = {M_START, M_STAGED, M_DIGITS, M_CONSUMED, M_STREAMED, M_STORED, M_PRE, M_ARRIVE};
         auto entry = [&](const std::string& name) -> af_kernel_timing& {
             for (auto& t : extra)
                 if (name == t.name) return t;

@@ -10,11 +10,12 @@
 // barrier, so HBM keeps streaming while the barrier and the next phase's input prologue
 // resolve.
 //
-// Wave roles: vector memory loads of one wave return in issue order, so a wave whose weight
-// prefetch is in flight cannot see an activation load before the prefetch lands.  Wave 0 of
-// every workgroup therefore never prefetches weights: it runs the grid barrier and stages the
-// phase's input vectors into LDS (global->LDS DMA), while waves 1-7 stream the weights.  The
-// input prologue (norms, exact int8 digit planes) then runs on all 512 threads from LDS.
+// Wave roles: wave 0 of every workgroup never streams weights: it runs the grid barrier, the
+// next phase's pre-barrier copies and the output stores, while waves 1-7 stream the weights,
+// each from its own contiguous run of weight records.  After a barrier all eight waves copy the
+// phase's input vectors into LDS (global->LDS DMA; a streaming wave's weight loads still in
+// flight were issued before the barrier), and the input prologue (norms, exact int8 digit
+// planes) runs on all 512 threads from LDS.
 //
 // Coherence: the eight XCDs have private L2 caches.  Activations exchanged between workgroups
 // inside the launch are written and read with agent-scope coherent accesses (sc1), the grid
@@ -70,6 +71,16 @@ __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(kVmWait);
 // waits with wait_vm().
 __device__ __forceinline__ void dma(const void* src, uint32_t bytes, uint8_t* lds, uint32_t lane) {
     for (uint32_t off = 0; off < bytes; off += 1024) {
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + off + lane * 16,
+                                             (lds_ptr)(lds + off), 16, 0, kSC1);
+    }
+}
+
+// The same copy split over the workgroup's 8 waves (wave w takes every 8th KB), so that one
+// wave's issue rate does not bound it; each wave waits for its own part.
+__device__ __forceinline__ void dma_all(const void* src, uint32_t bytes, uint8_t* lds, uint32_t wave, uint32_t lane) {
+    for (uint32_t off = wave * 1024; off < bytes; off += 8 * 1024) {
         if (off + lane * 16 < bytes)
             __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + off + lane * 16,
                                              (lds_ptr)(lds + off), 16, 0, kSC1);
@@ -365,19 +376,20 @@ struct Stage {
     float* snap;          // optional copy of x_out
 };
 
-// Wave 0, after the barrier: the activation inputs (the norm weights are already in LDS), or
-// the embedding row of the step's token.
+// Every wave, after the barrier: the activation inputs (the norm weights are already in LDS), or
+// the embedding row of the step's token.  A streaming wave's weight loads in flight were issued
+// before the barrier, so its wait here costs nothing the next phase would not wait for anyway.
 __device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const InputStage& emb, uint32_t K, uint32_t nst,
-                                             uint32_t xs_off, uint8_t* lds, uint32_t lane) {
+                                             uint32_t xs_off, uint8_t* lds, uint32_t wave, uint32_t lane) {
     uint8_t* img = lds;
     float* xs = reinterpret_cast<float*>(lds + xs_off);
     if (kind == S_DIGITS) {
-        dma(in.dig, nst * kStepImg, img, lane);
+        dma_all(in.dig, nst * kStepImg, img, wave, lane);
     } else if (kind == S_RESID) {
-        dma(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), lane);
-        dma(in.res, K * 4, reinterpret_cast<uint8_t*>(xs + K), lane);
+        dma_all(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), wave, lane);
+        dma_all(in.res, K * 4, reinterpret_cast<uint8_t*>(xs + K), wave, lane);
     } else {
-        embed_row(emb, xs, lane, 64);
+        embed_row(emb, xs, wave * 64 + lane, kThreads);
     }
     wait_vm();
 }
@@ -562,12 +574,14 @@ __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t 
     }
 }
 
-// One attention item.  Only wave 0 touches global memory (the streaming waves' weight loads stay
-// in flight), except for chunks too long to stage, whose K/V rows every wave reads directly.
+// One attention item.  Wave 0 does the item's global accesses (the streaming waves' weight loads
+// stay in flight), except for chunks too long to stage, whose K/V rows every wave reads directly,
+// and the merge's copy of the chunk partials.  Barriers: staged; norms summed; q/k rotated;
+// scores; softmax; values; partial; published (and, merging: partials copied; outputs merged).
 template <int GQ>
 __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uint32_t pos, uint32_t h, uint32_t c,
                                                uint32_t chunks, uint32_t cmax, uint32_t clen, uint32_t start,
-                                               uint8_t* lds, int* flag) {
+                                               uint8_t* lds, int* flag, const Grid& g) {
     constexpr int D = 256, NH = GQ + 2;
     AttnLds<GQ> sh(lds);
     float* nrm = sh.nrm;
@@ -575,14 +589,14 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     float* scores = sh.scores;
     float* vred = sh.vred;
     double* dred = sh.dred;
-    float* fred = sh.fred;
+    float* ml = sh.fred;  // [GQ][2]: max and sum of each query head's softmax
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen), n = t1 - t0;
     const uint32_t ring = L.ring;
     const bool append = t1 == pos + 1;
-    const bool ch = tid < D;
     const bool staged = clen <= stage_clen<GQ>();
+    const int nh = append ? NH : GQ;  // heads normalised here: the queries, and k, v of the new token
 
     // this token's query heads (and k, v when the chunk ends at it), computed by the qkv phase
     if (wave == 0) {
@@ -603,38 +617,57 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         wait_vm();
     }
     __syncthreads();
+    stamp(g, M_STAGED);
 
-    // prologue: RMSNorm of the query heads (and the new K, V), NeoX RoPE
-    float raw[NH];
-#pragma unroll
-    for (int q = 0; q < NH; ++q) raw[q] = ch && (q < GQ || append) ? nrm[q * D + tid] : 0.0f;
-    const double cs = tid < D / 2 ? sh.rope[tid] : 1.0, sn = tid < D / 2 ? sh.rope[128 + tid] : 0.0;
+    // RMSNorm of each head over its 256 channels, then NeoX RoPE on the pairs (i, i + 128): thread
+    // i < 128 (waves 0, 1) holds both channels of pair i of every head, so the rotation needs no
+    // exchange once the two waves' sums of squares are added.
+    const bool pr = tid < D / 2;
+    float x0[NH], x1[NH];
 #pragma unroll
     for (int q = 0; q < NH; ++q) {
-        const double v = wave_sum((double)raw[q] * (double)raw[q]);
-        if (lane == 0) dred[wave * NH + q] = v;
+        x0[q] = pr && q < nh ? nrm[q * D + tid] : 0.0f;
+        x1[q] = pr && q < nh ? nrm[q * D + tid + D / 2] : 0.0f;
     }
-    __syncthreads();
-    if (ch) {
+    if (wave < 2) {
 #pragma unroll
         for (int q = 0; q < NH; ++q) {
-            if (q >= GQ && !append) break;
-            const double ss = (dred[0 * NH + q] + dred[1 * NH + q]) + (dred[2 * NH + q] + dred[3 * NH + q]);
-            float r;
-            if (q < GQ) r = norm_apply(raw[q], inv_rms(ss, D, L.q_eps), sh.qnw[tid]);
-            else if (q == GQ) r = norm_apply(raw[q], inv_rms(ss, D, L.k_eps), sh.knw[tid]);
-            else r = L.v_norm ? (float)__dmul_rn((double)raw[q], inv_rms(ss, D, L.v_eps)) : raw[q];
-            nrm[q * D + tid] = r;
+            const double v = wave_sum((double)x0[q] * (double)x0[q] + (double)x1[q] * (double)x1[q]);
+            if (lane == 0) dred[wave * NH + q] = v;
         }
     }
     __syncthreads();
-    if (tid < D / 2) {
+    if (pr) {
+        const double cs = sh.rope[tid], sn = sh.rope[128 + tid];
 #pragma unroll
-        for (int q = 0; q < GQ + 1; ++q) {
-            if (q == GQ && !append) break;
-            const double x = (double)nrm[q * D + tid], y = (double)nrm[q * D + tid + D / 2];
-            const float r0 = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
-            const float r1 = (float)__dadd_rn(__dmul_rn(x, sn), __dmul_rn(y, cs));
+        for (int q = 0; q < NH; ++q) {
+            if (q >= nh) break;
+            const double ss = dred[q] + dred[NH + q];
+            float y0, y1;
+            if (q < GQ) {
+                const double r = inv_rms_fast(ss, D, L.q_eps);
+                y0 = norm_apply(x0[q], r, sh.qnw[tid]);
+                y1 = norm_apply(x1[q], r, sh.qnw[tid + D / 2]);
+            } else if (q == GQ) {
+                const double r = inv_rms_fast(ss, D, L.k_eps);
+                y0 = norm_apply(x0[q], r, sh.knw[tid]);
+                y1 = norm_apply(x1[q], r, sh.knw[tid + D / 2]);
+            } else {
+                const double r = L.v_norm ? inv_rms_fast(ss, D, L.v_eps) : 1.0;
+                y0 = L.v_norm ? (float)__dmul_rn((double)x0[q], r) : x0[q];
+                y1 = L.v_norm ? (float)__dmul_rn((double)x1[q], r) : x1[q];
+                const uint16_t v0 = f2h(y0), v1 = f2h(y1);
+                sh.vnew[tid] = v0;
+                sh.vnew[tid + D / 2] = v1;
+                if (staged) {
+                    sh.vst[(pos - t0) * D + tid] = v0;
+                    sh.vst[(pos - t0) * D + tid + D / 2] = v1;
+                }
+                break;
+            }
+            const double u = (double)y0, w = (double)y1;
+            const float r0 = (float)__dsub_rn(__dmul_rn(u, cs), __dmul_rn(w, sn));
+            const float r1 = (float)__dadd_rn(__dmul_rn(u, sn), __dmul_rn(w, cs));
             if (q < GQ) {
                 qs[q * D + tid] = r0;
                 qs[q * D + tid + D / 2] = r1;
@@ -648,11 +681,6 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
                 }
             }
         }
-    }
-    if (append && ch) {
-        const uint16_t v = f2h(nrm[(GQ + 1) * D + tid]);
-        sh.vnew[tid] = v;
-        if (staged) sh.vst[(pos - t0) * D + tid] = v;
     }
     __syncthreads();
 
@@ -698,19 +726,23 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     }
     __syncthreads();
 
-    float m[GQ], l[GQ];
-#pragma unroll
-    for (int q = 0; q < GQ; ++q) {
+    // softmax: wave q < GQ normalises query head q's scores on its own (no block reduction)
+    if (wave < (uint32_t)GQ) {
+        float* sc = scores + wave * kStepMaxClen;
         float mx = -INFINITY;
-        for (uint32_t i = tid; i < n; i += kThreads) mx = fmaxf(mx, scores[q * kStepMaxClen + i]);
-        m[q] = block_max_f(mx, fred);
+        for (uint32_t i = lane; i < n; i += 64) mx = fmaxf(mx, sc[i]);
+        mx = wave_max(mx);
         float sum = 0.0f;
-        for (uint32_t i = tid; i < n; i += kThreads) {
-            const float p = expf(scores[q * kStepMaxClen + i] - m[q]);
-            scores[q * kStepMaxClen + i] = p;
+        for (uint32_t i = lane; i < n; i += 64) {
+            const float p = expf(sc[i] - mx);
+            sc[i] = p;
             sum += p;
         }
-        l[q] = block_sum_f(sum, fred);
+        sum = wave_sum(sum);
+        if (lane == 0) {
+            ml[2 * wave] = mx;
+            ml[2 * wave + 1] = sum;
+        }
     }
     __syncthreads();
 
@@ -758,19 +790,12 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         const uint32_t q = i / D, d = i % D;
         float t = 0.0f;
 #pragma unroll
-        for (int g = 0; g < 16; ++g) t += vred[(g * GQ + q) * D + d];
+        for (int g2 = 0; g2 < 16; ++g2) t += vred[(g2 * GQ + q) * D + d];
         pst[q * (D + 2) + d] = t;
     }
-    if (tid < GQ) {
-#pragma unroll
-        for (int q = 0; q < GQ; ++q) {
-            if ((uint32_t)q == tid) {
-                pst[q * (D + 2) + D] = m[q];
-                pst[q * (D + 2) + D + 1] = l[q];
-            }
-        }
-    }
+    if (tid < 2 * GQ) pst[(tid >> 1) * (D + 2) + D + (tid & 1)] = ml[tid];
     __syncthreads();
+    stamp(g, M_DIGITS);
     float* const head_part = a.part + (size_t)h * cmax * stride;
     if (wave == 0) {
         if (append) {  // the new K/V rows into the cache (this step reads them from LDS)
@@ -778,7 +803,9 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
             *gp(reinterpret_cast<v2u*>(L.kcache + slot) + lane) = reinterpret_cast<const v2u*>(sh.knew)[lane];
             *gp(reinterpret_cast<v2u*>(L.vcache + slot) + lane) = reinterpret_cast<const v2u*>(sh.vnew)[lane];
         }
-        for (uint32_t i = lane; i < stride; i += 64) stc(head_part, (c * stride + i) * 4, __float_as_uint(pst[i]));
+        // stride * 4 bytes per chunk is a multiple of 16 (GQ * 1032)
+        const v4u* ps = reinterpret_cast<const v4u*>(pst);
+        for (uint32_t i = lane; i < stride / 4; i += 64) stc16(head_part, (c * stride + 4 * i) * 4, ps[i]);
         wait_vm();
         if (lane == 0) {
             const uint32_t ticket =
@@ -788,16 +815,15 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         wait_vm();
     }
     __syncthreads();
+    stamp(g, M_STREAMED);
     if (!__builtin_amdgcn_readfirstlane(*flag)) return;
 
     // merge (last chunk of this head): M = max_c m_c, w_c = exp(m_c - M), output
     // sum_c w_c o_c / sum_c w_c l_c, in chunk order
     float* mrg = reinterpret_cast<float*>(lds);  // [chunks][stride]
     float* outv = mrg + chunks * stride;        // [GQ][D]
-    if (wave == 0) {
-        dma(head_part, chunks * stride * 4, lds, lane);
-        wait_vm();
-    }
+    dma_all(head_part, chunks * stride * 4, lds, wave, lane);
+    wait_vm();
     __syncthreads();
     for (uint32_t i = tid; i < GQ * D; i += kThreads) {
         const uint32_t q = i / D, d = i % D;
@@ -966,14 +992,14 @@ __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, i
     return ~(size_t)0;
 }
 
-// Wave roles.  Waves 1-7 issue no vector memory instruction but their weight loads: the
-// compiler then waits for exactly the ring slot being consumed, and no activation or staging
-// access ever queues behind the weight loads in flight.  Wave 0 does every other global access
-// (barrier, staging DMA, stores), and every wave-0 block that issues one waits for it before the
-// block ends.  A GEMV phase: barrier; wave 0 stages the inputs; all build the digit image from
-// LDS; waves 1-7 consume their weight stream (refilling the ring with the next phase's tiles)
-// while wave 0 stores the residual and prepares the next phase when its LDS is free; wave 0
-// stores the outputs.  Every phase's code appears once in the loop over (layer, phase).
+// Wave roles.  Inside a phase, waves 1-7 issue no vector memory instruction but their weight
+// loads: the compiler then waits for exactly the ring slot being consumed.  Wave 0 does every
+// other global access of the phase (barrier, pre-copies, stores), and every wave-0 block that
+// issues one waits for it before the block ends.  A GEMV phase: barrier; all waves stage the
+// inputs; all build the digit image from LDS; waves 1-7 consume their weight stream (refilling
+// the ring with the next phase's records) while wave 0 stores the residual and prepares the next
+// phase when its LDS is free; wave 0 stores the outputs.  Every phase's code appears once in the
+// loop over (layer, phase).
 template <int GQ>
 __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -1022,13 +1048,13 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             const uint32_t item = gridDim.x - 1 - blockIdx.x;
             if (item < ag.items)
                 attention_item<GQ>(L, a, pos, item / ag.chunks, item % ag.chunks, ag.chunks, ag.cmax, ag.clen, ag.start,
-                                   lds, &att_flag);
+                                   lds, &att_flag, g);
             __syncthreads();
             stamp(g, M_STORED);
         } else {
             const Gemv d = describe(a, l, kind);
             const uint32_t nst = d.sh.nst;
-            if (wave == 0) stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, a.xs_off, lds, lane);
+            stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, a.xs_off, lds, wave, lane);
             __syncthreads();
             stamp(g, M_STAGED);
             zero_part_lds(part, tid);
@@ -1043,6 +1069,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
                 consume_phase(r, nst, d.sh.T, __builtin_amdgcn_readfirstlane(fe), lds_addr(lds), part, wave, lane,
                               lk);
+                if (wave == 1) stamp_at(g, g.k, M_CONSUMED);
                 __syncthreads();
             } else {
                 if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
