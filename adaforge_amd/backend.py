@@ -186,10 +186,10 @@ class HipGenerationSession:
         pa, pp = _ids(prompt)
         out = np.zeros(max(int(max_new), 1), np.uint32)
         n = N.sz()
-        t = (N.KernelTiming * 128)()
+        t = (N.KernelTiming * 256)()
         nt = N.sz()
         check(N.lib().af_session_profile(self._h, pp, pa.size, int(max_new), out.ctypes.data_as(N.u32p),
-                                         ctypes.byref(n), t, 128, ctypes.byref(nt)))
+                                         ctypes.byref(n), t, 256, ctypes.byref(nt)))
         return out[:n.value].tolist(), {t[i].name.decode(): (t[i].launches, t[i].total_ms, t[i].bytes_per_launch)
                                         for i in range(nt.value)}
 

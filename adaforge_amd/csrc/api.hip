@@ -1476,6 +1476,24 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
                     e.total_ms += (double)(t - prev) * tick_ms;
                     prev = t;
                 }
+                // each mark's mean offset from the workgroup's own phase start ("<phase>.<mark>@")
+                for (int mk = M_STAGED; mk < kStepMarks; ++mk) {
+                    if (mk == M_ARRIVE) continue;
+                    double sum = 0;
+                    uint32_t cnt = 0;
+                    for (uint32_t b = 0; b < G; ++b) {
+                        const uint64_t t0 = ev(p, M_START, b), t = ev(p, mk, b);
+                        if (t && t >= t0) {
+                            sum += (double)(t - t0);
+                            ++cnt;
+                        }
+                    }
+                    if (cnt) {
+                        af_kernel_timing& e = entry(base + "." + kMarkNames[mk] + "@");
+                        e.launches += 1;
+                        e.total_ms += sum / cnt * tick_ms;
+                    }
+                }
                 // the same split averaged over every workgroup ("<phase>.<mark>~")
                 for (uint32_t b = 0; b < G; ++b) {
                     uint64_t pv = ev(p, M_START, b);

@@ -1074,6 +1074,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             } else {
                 if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
                 if (pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
+                stamp(g, M_PRE);
                 __syncthreads();
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
