@@ -334,26 +334,38 @@ __device__ __forceinline__ uint2 ld_stream(const uint2* p) {
 }
 
 // Digit words of 8 consecutive elements v of a block whose max |x| is m: w[t] holds the 8
-// int8 digits of plane t.
+// int8 digits of plane t.  With s = 2^(ilogb(m) - 5), U = rint(v 2^21 / s) is an integer with
+// |U| <= 2^27 (|v| < 2^(ilogb(m) + 1), and scaling by a power of two is exact), and its signed
+// radix-2^7 digits q0..q3 (q_t = round(r_t / 2^(21 - 7t)) on the remainders, |q_t| <= 64) satisfy
+// U = 2^21 q0 + 2^14 q1 + 2^7 q2 + q3, so v = s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) to within
+// half of s 2^-21.  Integer adds and shifts only, then v_perm packs the low bytes.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+    // byte i of the result = low byte of the i-th argument
+    const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);  // [a0, b0, 0, 0]
+    const uint32_t hi = __builtin_amdgcn_perm((uint32_t)d, (uint32_t)c, 0x0C0C0400u);  // [c0, d0, 0, 0]
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);                                 // [a0, b0, c0, d0]
+}
+
 __device__ __forceinline__ void digit_words(const float (&v)[8], float m, uint32_t (&w)[4][2]) {
     const int e = m > 0.0f ? ilogbf(m) : 0;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) w[t][0] = w[t][1] = 0u;
+    int q[4][8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        const float u = m > 0.0f ? ldexpf(v[k], 5 - e) : 0.0f;  // |u| < 64, exact
-        const float q0 = rintf(u);
-        float r = (u - q0) * 128.0f;
-        const float q1 = rintf(r);
-        r = (r - q1) * 128.0f;
-        const float q2 = rintf(r);
-        r = (r - q2) * 128.0f;
-        const float q3 = rintf(r);
-        const int sh = 8 * (k & 3);
-        w[0][k >> 2] |= ((uint32_t)(int)q0 & 0xFFu) << sh;
-        w[1][k >> 2] |= ((uint32_t)(int)q1 & 0xFFu) << sh;
-        w[2][k >> 2] |= ((uint32_t)(int)q2 & 0xFFu) << sh;
-        w[3][k >> 2] |= ((uint32_t)(int)q3 & 0xFFu) << sh;
+        const int U = m > 0.0f ? (int)rintf(ldexpf(v[k], 26 - e)) : 0;
+        const int q0 = (U + (1 << 20)) >> 21;
+        const int r0 = U - q0 * (1 << 21);
+        const int q1 = (r0 + (1 << 13)) >> 14;
+        const int r1 = r0 - q1 * (1 << 14);
+        const int q2 = (r1 + (1 << 6)) >> 7;
+        q[0][k] = q0;
+        q[1][k] = q1;
+        q[2][k] = q2;
+        q[3][k] = r1 - q2 * (1 << 7);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        w[t][0] = pack4(q[t][0], q[t][1], q[t][2], q[t][3]);
+        w[t][1] = pack4(q[t][4], q[t][5], q[t][6], q[t][7]);
     }
 }
 

@@ -364,7 +364,7 @@ __device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T,
 
 // Input prologue of a GEMV phase: LDS layout [digit image nst * kStepImg] ... and, at StepArgs::xs_off
 // (above the largest image of any phase, so the next phase's norm weights can be copied in while
-// this phase's image is in use), [x K][res K][w_a K][w_n K] (floats).  Wave 0 stages, every
+// this phase's image is in use), [x K][res K][w_a K][w_n K] (floats).  Every wave stages, every
 // thread then builds the digit image.
 enum StageKind { S_EMBED = 0, S_RESID = 1, S_DIGITS = 2 };
 
@@ -422,9 +422,14 @@ __device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
     reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
 }
 
-// Digit image of the normalised input (K <= 4096, so one octet per thread), all threads, from
-// LDS only (16-byte accesses: 8-float strides read element-wise would hit the same bank from
-// 16 lanes).  The residual sum replaces x in xs[0, K) for store_residual.  red: 16 slots.
+// Digit image of the input before its RMSNorm row factor (K <= 4096, so one octet per thread), all
+// threads, from LDS only (16-byte accesses: 8-float strides read element-wise would hit the same
+// bank from 16 lanes).  The GEMV input is f32(t rn w_n) with t the residual sum and rn =
+// rms(t)^-1; the image holds u = f32(t w_n) instead, and the phase's row sums are scaled by rn
+// (norm_factor), so the digits need not wait for the sum of squares of t, whose wave sums this
+// leaves in red[8, 16) for norm_factor to add after the caller's barrier.  (The difference is the
+// f32 rounding of each input element, about 2^-24 of it.)  The residual sum replaces x in xs[0, K)
+// for store_residual.  red: 16 slots.
 __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t K, uint32_t nst, uint32_t xs_off,
                                              uint8_t* lds, double* red) {
     int8_t* dig = reinterpret_cast<int8_t*>(lds);
@@ -463,10 +468,11 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t
     double ss = 0.0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) ss += (double)t[k] * t[k];
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[8 + (tid >> 6)] = ss;
     if (ok) ld8(xs + 3 * K + 8 * o, w);
-    const double rn = inv_rms_fast(block_sum_once(ss, red + 8), K, in.eps_n);
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = ok ? norm_apply(t[k], rn, w[k]) : 0.0f;
+    for (int k = 0; k < 8; ++k) v[k] = ok ? __fmul_rn(t[k], w[k]) : 0.0f;
     float m, sum;
     quad_stats(v, m, sum);
     const uint32_t b = o >> 2, p = o & 3;
@@ -474,6 +480,13 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t
         digits8(v, m, dig, b, p);
         if (p == 0) tab[b] = block_tab(m, sum);
     }
+}
+
+// The RMSNorm row factor of a residual prologue, from the wave sums stage_digits left in red
+// (after a barrier), in block_sum_once's order.
+__device__ __forceinline__ double norm_factor(const double* red, uint32_t K, float eps) {
+    const double ss = ((red[8] + red[9]) + (red[10] + red[11])) + ((red[12] + red[13]) + (red[14] + red[15]));
+    return inv_rms_fast(ss, K, eps);
 }
 
 // Digit image words of one 32-element block held by a quad (8 values per lane), stored
@@ -1079,15 +1092,20 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
+                // a residual prologue's row factor (1 for an input given as a digit image)
+                const double rn = d.in_kind != S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
                 if (d.y) {
                     if (tid < 16 * mu) {
                         const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
-                        if (row < d.rows) stc(d.y, row * 4, __float_as_uint(part_sum(part, k, 0, rr)));
+                        const float y = (float)(rn * (double)part_sum(part, k, 0, rr));
+                        if (row < d.rows) stc(d.y, row * 4, __float_as_uint(y));
                     }
                 } else {
                     if (tid < 32 * mu) {
                         const uint32_t k = tid >> 5, rr = tid & 31, t = rr >> 4, r16 = rr & 15;
-                        act_l[k][rr] = gelu_mul(part_sum(part, k, t, r16), part_sum(part, k, 2 + t, r16));
+                        const float gt = (float)(rn * (double)part_sum(part, k, t, r16));
+                        const float up = (float)(rn * (double)part_sum(part, k, 2 + t, r16));
+                        act_l[k][rr] = gelu_mul(gt, up);
                     }
                     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");  // act_l: written and read by wave 0
                     if (tid < 4 * mu) {
