@@ -87,6 +87,16 @@ __device__ __forceinline__ void dma_all(const void* src, uint32_t bytes, uint8_t
     }
 }
 
+// The same copy split into 1 KB stripes over n waves (this one is number i < n).
+__device__ __forceinline__ void dma_part(const void* src, uint32_t bytes, uint8_t* lds, uint32_t i, uint32_t n,
+                                         uint32_t lane) {
+    for (uint32_t off = i * 1024; off < bytes; off += n * 1024) {
+        if (off + lane * 16 < bytes)
+            __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + off + lane * 16,
+                                             (lds_ptr)(lds + off), 16, 0, kSC1);
+    }
+}
+
 // ---- grid barrier -------------------------------------------------------------------------------
 
 struct Grid {
@@ -107,9 +117,11 @@ __device__ __forceinline__ void stamp(const Grid& g, uint32_t mark) {
 }
 
 // All threads call it.  Returns false (in every thread) if the barrier did not complete within
-// the spin limit, which only a launch without co-resident workgroups could cause.
-__device__ __forceinline__ bool grid_sync(Grid& g) {
-    __syncthreads();
+// the spin limit, which only a launch without co-resident workgroups could cause.  With `lead`
+// the workgroup first waits for all its waves (their stores are waited for before they arrive);
+// without it, wave 0 alone has published the phase's outputs and arrives for the workgroup.
+__device__ __forceinline__ bool grid_sync(Grid& g, bool lead) {
+    if (lead) __syncthreads();
     if (threadIdx.x == 0) {
         stamp_at(g, g.k, M_ARRIVE);
         const uint32_t per = gridDim.x / 8, grp = blockIdx.x & 7, k = g.k + 1;
@@ -159,8 +171,12 @@ struct Shape {
     uint32_t nst, T, units;
 };
 
+// Row partials of a GEMV phase in LDS: part[(k kMaxT + ts) 8 + wave][16 rows], a wave's sums over
+// its super-tiles of tile stream ts of unit k.
+constexpr uint32_t kPart = kMaxUnits * kMaxT * 8 * 16;
+
 __device__ __forceinline__ void zero_part_lds(float* part, uint32_t tid) {
-    for (uint32_t i = tid; i < kMaxUnits * kMaxT * 8 * 16; i += kThreads) part[i] = 0.0f;
+    for (uint32_t i = tid; i < kPart; i += kThreads) part[i] = 0.0f;
 }
 
 __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_t ts, uint32_t r) {
@@ -169,6 +185,15 @@ __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_
 #pragma unroll
     for (int w = 2; w < 8; ++w) v += p[16 * w];
     return v;
+}
+
+// Sum over the four lanes of a row (l % 16 equal), left in every lane: the 32-lane halves, then
+// the 16-lane rows, swapped in registers (v_permlane32_swap / v_permlane16_swap).
+__device__ __forceinline__ float row_total(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float w = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 // Digit image of a GEMV input, nst * kStepImg bytes: the digit planes dig[b * 4 + t][32] of
@@ -256,110 +281,151 @@ __device__ __forceinline__ void ring_rotate(Ring& r) {
 // high nibbles in a second against 16..31).  Lane l then holds D[4 q + i][r] for digit i of
 // block q = l / 16 and row r = l % 16, which it folds with its one block scale d(r, q).
 struct LaneK {
-    uint32_t aoff;   // active A lanes: byte offset of their digit plane within a super-tile image
-    uint32_t ainc;   // 7 super-tiles of digits for active lanes, 0 for the others
-    uint32_t zero;   // LDS address of 32 zero bytes (inactive A lanes)
-    uint32_t q16;    // block entry of the lane's output block within a super-tile
+    uint32_t aoff;  // active A lanes: byte offset of their digit plane within a super-tile image
+    uint32_t q16;   // block entry of the lane's output block within a super-tile
     bool aon;
 };
 
-__device__ __forceinline__ LaneK lane_k(uint32_t lane, uint32_t zero) {
+__device__ __forceinline__ LaneK lane_k(uint32_t lane) {
     LaneK k;
     k.aon = ((lane & 15) >> 2) == (lane >> 4);
     k.aoff = (lane & 15) * 32;
-    k.ainc = k.aon ? 7u * 512u : 0u;
-    k.zero = zero;
     k.q16 = (lane >> 4) * 16;
     return k;
 }
 
-// Flattened super-tile f of a phase -> (super-tile st, tile stream ts, unit k).  rcp =
-// ceil(2^32 / nst), exact for f * nst < 2^32 (f < 2 units * 4 * nst here); T is 1 or 4.
-__device__ __forceinline__ void split_f(uint32_t f, uint32_t nst, uint32_t rcp, uint32_t T, uint32_t& st,
-                                        uint32_t& ts, uint32_t& k) {
-    const uint32_t seg = __umulhi(f, rcp);
-    st = f - seg * nst;
-    ts = seg & (T - 1);
-    k = T == 1 ? seg : seg >> 2;
-}
-
-// Run state of a wave inside a GEMV phase: a run is the wave's super-tiles of one row tile (st,
-// st + 7, ... below nst); f is the flattened index of the next run's first super-tile.
-struct RunState {
-    uint32_t f, n, adig, toff, pidx;
-    float acc;
+// LDS byte addresses of a phase's record operands for this lane: the digit planes of super-tile st
+// at a0 + st * am (am = 0 and a0 = the zero block for inactive A lanes) and the lane's BlockTab
+// entry at t0 + 64 st.
+struct LaneAddr {
+    uint32_t a0, am, t0;
 };
 
-__device__ __forceinline__ void run_start(RunState& s, uint32_t nst, uint32_t rcp, uint32_t T, uint32_t fe,
-                                          uint32_t img, uint32_t wave, uint32_t lane, const LaneK& lk) {
-    uint32_t st, ts, k;
-    split_f(s.f, nst, rcp, T, st, ts, k);
-    s.n = min((nst - st + 6) / 7, (fe - s.f + 6) / 7);
-    s.f += 7 * s.n;
-    s.adig = lk.aon ? img + st * 512 + lk.aoff : lk.zero;
-    s.toff = img + nst * 512 + st * 64 + lk.q16;
-    s.pidx = ((k * kMaxT + ts) * 8 + wave) * 16 + lane;
+__device__ __forceinline__ LaneAddr lane_addr(const uint8_t* img, const v4i* zero, uint32_t nst, const LaneK& lk) {
+    LaneAddr a;
+    a.a0 = lk.aon ? lds_addr(img) + lk.aoff : lds_addr(zero);
+    a.am = lk.aon ? 512u : 0u;
+    a.t0 = lds_addr(img) + nst * 512 + lk.q16;
+    return a;
 }
 
-// One record: two int8 MFMAs against the digit image, the fold into the row partial, the refill of
-// the slot, and at a run's end the row partials into part.
-__device__ __forceinline__ void consume_record(Ring& r, const __amdgpu_buffer_rsrc_t& rs, int u, RunState& s,
-                                               uint32_t nst, uint32_t rcp, uint32_t T, uint32_t fe, uint32_t img,
-                                               float* part, uint32_t wave, uint32_t lane, const LaneK& lk) {
-    const v4u c = r.code[u];
-    const uint32_t sc = r.scale[u];
+__device__ __forceinline__ void split_codes(const v4u c, v4i& bl, v4i& bh) {
     constexpr uint32_t M = 0x0F0F0F0Fu;
+    bl = v4i{(int)(c.x & M), (int)(c.y & M), (int)(c.z & M), (int)(c.w & M)};
+    bh = v4i{(int)((c.x >> 4) & M), (int)((c.y >> 4) & M), (int)((c.z >> 4) & M), (int)((c.w >> 4) & M)};
+}
+
+// Position of a wave's next record in a GEMV phase (wave-uniform).  The wave's super-tiles are f =
+// wave - 1, wave + 6, ... (flattened over unit k, tile stream ts, super-tile st) below fe; a run is
+// its super-tiles of one (k, ts).  A step of 7 super-tiles (7 = dseg nst + dst) advances st by dst
+// and the run by dseg, or by dseg + 1 when st wraps; the run's row sums go to part[prow + r].
+struct Cursor {
+    uint32_t st, prow;      // super-tile, part offset of the run
+    uint32_t nst, dst;
+    uint32_t pstep0, pstep1;  // prow advance without / with a wrap
+    bool end0;                // a step without a wrap leaves the run (nst < 7)
+};
+
+__device__ __forceinline__ Cursor cursor_start(uint32_t nst, uint32_t T, uint32_t wave) {
+    Cursor c;
+    const uint32_t f = wave - 1, seg = f / nst, dseg = 7 / nst;
+    const uint32_t pstep = T == 1 ? kMaxT * 8 * 16 : 8 * 16;  // one (k, ts) further; T is 1 or 4
+    c.nst = nst;
+    c.dst = 7 % nst;
+    c.pstep0 = dseg * pstep;
+    c.pstep1 = (dseg + 1) * pstep;
+    c.end0 = dseg != 0;
+    c.st = f - seg * nst;
+    c.prow = seg * pstep + wave * 16;
+    return c;
+}
+
+// One record of slot u: two int8 MFMAs against the digit image, the fold into the lane's partial,
+// the refill of the slot (with Fill), and at the run's end its row sums into part (a uniform
+// branch: every lane of a row writes the same value) and a fresh partial.
+template <bool Fill = true>
+__device__ __forceinline__ void consume_one(Ring& r, const __amdgpu_buffer_rsrc_t& rs, int u, Cursor& c, float& acc,
+                                            const LaneAddr& la, float* part, uint32_t lane) {
+    const uint32_t s1 = c.st + c.dst, s2 = s1 - c.nst;
+    const bool wrap = s1 >= c.nst;
+    const bool last = wrap || c.end0;  // the run's last record (the phase's last: see consume_phase)
+    const uint32_t pa = la.a0 + c.st * la.am;
+    const v4i a0 = lds_at<v4i>(pa), a1 = lds_at<v4i>(pa + 16);
+    const v4f tb = lds_at<v4f>(la.t0 + c.st * 64);  // BlockTab: s14, s21, nbias
     const v4i zero4 = {0, 0, 0, 0};
-    const v4i bl = {(int)(c.x & M), (int)(c.y & M), (int)(c.z & M), (int)(c.w & M)};
-    const v4i bh = {(int)((c.x >> 4) & M), (int)((c.y >> 4) & M), (int)((c.z >> 4) & M), (int)((c.w >> 4) & M)};
-    const v4i al = lds_at<v4i>(s.adig), ah = lds_at<v4i>(s.adig + 16);
-    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(al, bl, zero4, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, bh, d, 0, 0, 0);
-    const v4f tb = lds_at<v4f>(s.toff);  // BlockTab: s14, s21, nbias
+    v4i bl, bh;
+    split_codes(r.code[u], bl, bh);
+    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bl, zero4, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh, d, 0, 0, 0);
     // 2^14 D0 + 2^7 D1 + D2 is exact in int32 (|D_t| <= 32 * 15 * 64)
     const int I = (d[0] << 14) + (d[1] << 7) + d[2];
     float in = fmaf((float)I, tb.x, tb.z);
     in = fmaf((float)d[3], tb.y, in);
-    s.acc = fmaf(h2f((uint16_t)sc), in, s.acc);
-    ring_fill(r, rs, u, lane);  // after the last use of the slot's registers
-    s.adig += lk.ainc;
-    s.toff += 7 * 64;
-    if (--s.n == 0) {  // the run's last super-tile: one partial per row
-        float v = s.acc + __shfl_xor(s.acc, 16);
-        v += __shfl_xor(v, 32);
-        if (lane < 16) part[s.pidx] = v;
-        s.acc = 0.0f;
-        if (s.f < fe) run_start(s, nst, rcp, T, fe, img, wave, lane, lk);
+    acc = fmaf(h2f((uint16_t)r.scale[u]), in, acc);
+    if constexpr (Fill) ring_fill(r, rs, u, lane);  // after the last use of the slot's registers
+    if (last) {
+        part[c.prow + (lane & 15)] = row_total(acc);
+        acc = 0.0f;
     }
+    c.prow += wrap ? c.pstep1 : c.pstep0;
+    c.st = wrap ? s2 : s1;
 }
 
-// Consumes this wave's records of a GEMV phase (fe = the workgroup's flattened super-tiles) and
-// leaves one partial per row, per (unit k, tile stream ts) it visits, in part[(k kMaxT + ts) 8 +
-// wave][16].  img: LDS address of the phase's digit image.  Whole rounds of kRing records run
-// without an exit test (exact waits: slot u's loads are followed by those of the kRing - 1 slots
-// after it), then a tail of fewer than kRing.
-__device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T, uint32_t fe, uint32_t img,
-                                              float* part, uint32_t wave, uint32_t lane, const LaneK& lk) {
+// The phase's last record ends its run whether or not the next step wraps: its row sums, unless
+// that record already wrote them (acc was reset).  c has advanced past the record.
+__device__ __forceinline__ void flush_last(float acc, const Cursor& c, float* part, uint32_t lane) {
+    // the run of the last record: prow before the step (no wrap: pstep0 was added)
+    if (c.st >= c.dst && !c.end0) part[c.prow + (lane & 15)] = row_total(acc);
+}
+
+// A streaming wave's partials are all in part: +64 on the workgroup's LDS counter (every lane adds
+// one), ordered after the wave's LDS writes.
+__device__ __forceinline__ void signal_done(uint32_t* done) {
+    __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Consumes this wave's records of a GEMV phase (fe = the workgroup's flattened super-tiles), leaves
+// its partials in part and signals `done`.  img: the phase's digit image in LDS.
+// * When the ring holds every record of the phase, they are consumed first and the slots are
+//   refilled after the signal: a refill cannot issue while the memory system is saturated, and
+//   that wait then delays neither the records nor the phase's epilogue.
+// * Otherwise whole rounds of kRing records run without an exit test (exact waits: slot u's loads
+//   are followed by those of the kRing - 1 slots after it), then a tail of fewer than kRing.
+__device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T, uint32_t fe, const uint8_t* img,
+                                              const v4i* zero, float* part, uint32_t wave, uint32_t lane,
+                                              const LaneK& lk, uint32_t* done) {
     if (wave - 1 >= fe) return;
     wait_vm();  // every record in flight was requested before this phase's barrier
     ring_rotate(r);
     const __amdgpu_buffer_rsrc_t rs = ring_rsrc(r);
     r.soff = __builtin_amdgcn_readfirstlane(r.soff);
-    const uint32_t rcp = (uint32_t)((0xFFFFFFFFull + nst) / nst);
     const uint32_t total = (fe - (wave - 1) + 6) / 7;
-    RunState s;
-    s.f = wave - 1;
-    s.acc = 0.0f;
-    run_start(s, nst, rcp, T, fe, img, wave, lane, lk);
-    for (uint32_t rounds = total / kRing; rounds; --rounds) {
+    const LaneAddr la = lane_addr(img, zero, nst, lk);
+    Cursor c = cursor_start(nst, T, wave);
+    float acc = 0.0f;
+    if (total <= kRing) {
 #pragma unroll
-        for (int u = 0; u < kRing; ++u) consume_record(r, rs, u, s, nst, rcp, T, fe, img, part, wave, lane, lk);
+        for (int u = 0; u < kRing; ++u)
+            if ((uint32_t)u < total) consume_one<false>(r, rs, u, c, acc, la, part, lane);
+        flush_last(acc, c, part, lane);
+        signal_done(done);
+#pragma unroll
+        for (int u = 0; u < kRing; ++u)
+            if ((uint32_t)u < total) ring_fill(r, rs, u, lane);
+        r.slot = total % kRing;
+        return;
+    }
+    for (uint32_t i = total / kRing; i; --i) {
+#pragma unroll
+        for (int u = 0; u < kRing; ++u) consume_one(r, rs, u, c, acc, la, part, lane);
     }
     const uint32_t rem = total % kRing;
 #pragma unroll
     for (int u = 0; u < kRing - 1; ++u)
-        if ((uint32_t)u < rem) consume_record(r, rs, u, s, nst, rcp, T, fe, img, part, wave, lane, lk);
+        if ((uint32_t)u < rem) consume_one(r, rs, u, c, acc, la, part, lane);
     r.slot = rem;
+    flush_last(acc, c, part, lane);
+    signal_done(done);
 }
 
 // Input prologue of a GEMV phase: LDS layout [digit image nst * kStepImg] ... and, at StepArgs::xs_off
@@ -992,6 +1058,21 @@ __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t
     }
 }
 
+// The norm weights of GEMV phase ph (qkv, gate/up), copied by the streaming waves once their records
+// are consumed: waves 1-7 each take every 7th KB.  Returns false for other phases (left to
+// phase_pre on wave 0).
+__device__ __forceinline__ bool norms_pre_part(const StepArgs& a, int32_t ph, int32_t n_phases, uint8_t* lds,
+                                               uint32_t wave, uint32_t lane) {
+    if (ph >= n_phases) return false;
+    const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
+    if (kind != P_QKV && kind != P_GATEUP) return false;
+    const Gemv d = describe(a, l, kind);
+    float* xs = reinterpret_cast<float*>(lds + a.xs_off);
+    if (d.in.w_a) dma_part(d.in.w_a, d.K * 4, reinterpret_cast<uint8_t*>(xs + 2 * d.K), wave - 1, kStreamWaves, lane);
+    dma_part(d.in.w_n, d.K * 4, reinterpret_cast<uint8_t*>(xs + 3 * d.K), wave - 1, kStreamWaves, lane);
+    return true;
+}
+
 // Lowest LDS byte phase_pre writes for phase ph (no write: ~0).
 template <int GQ>
 __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, int32_t n_phases) {
@@ -1016,9 +1097,10 @@ __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, i
 template <int GQ>
 __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ float part[kMaxUnits * kMaxT * 8 * 16];
+    __shared__ float part[kPart];
     __shared__ double red[16];
     __shared__ int ok_flag, att_flag;
+    __shared__ uint32_t done_cnt;  // streaming waves done with a GEMV phase, 64 per wave
     __shared__ float act_l[kMaxUnits][32];
 
     if (a.state[ST_STOP]) return;  // uniform: written only before the launch
@@ -1030,8 +1112,9 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     const int32_t n_phases = (int32_t)(kPhases * a.n_layers);
     __shared__ uint4 zero_blk[2];
     if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);  // read after the first __syncthreads
+    if (tid == 0) done_cnt = 0;
     Ring r;
-    const LaneK lk = lane_k(lane, lds_addr(zero_blk));
+    const LaneK lk = lane_k(lane);
     if (wave != 0) {
         const uint32_t w = blockIdx.x * kStreamWaves + (wave - 1);
         const uint64_t o0 = a.stream_off[w], o1 = a.stream_off[w + 1];
@@ -1051,7 +1134,8 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
 
     for (int32_t ph = 0; ph < n_phases; ++ph) {
         const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
-        if (ph > 0 && !grid_sync(g)) {
+        // after a GEMV phase wave 0 has waited for the streaming waves (done_cnt) and for its stores
+        if (ph > 0 && !grid_sync(g, (uint32_t)(ph - 1) % kPhases == P_ATTN)) {
             failed = true;
             break;
         }
@@ -1080,15 +1164,22 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             // compiler's wait model never mixes wave 0's copies into the streaming waves'.
             if (wave != 0) {
                 const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
-                consume_phase(r, nst, d.sh.T, __builtin_amdgcn_readfirstlane(fe), lds_addr(lds), part, wave, lane,
-                              lk);
+                consume_phase(r, nst, d.sh.T, __builtin_amdgcn_readfirstlane(fe), lds,
+                              reinterpret_cast<const v4i*>(zero_blk), part, wave, lane, lk, &done_cnt);
+                // waited for by the next phase's staging (wait_vm) before its barrier
+                if (pre_now) norms_pre_part(a, ph + 1, n_phases, lds, wave, lane);
                 if (wave == 1) stamp_at(g, g.k, M_CONSUMED);
-                __syncthreads();
             } else {
                 if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
-                if (pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
+                if (pre_now && (ph + 1 >= n_phases || (uint32_t)(ph + 1) % kPhases == P_ATTN))
+                    phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 stamp(g, M_PRE);
-                __syncthreads();
+                // the streaming waves with records (wave - 1 < fe) have left their partials in part
+                const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
+                const uint32_t want = 64u * min(kStreamWaves, fe);
+                while (__hip_atomic_load(&done_cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < want)
+                    __builtin_amdgcn_s_sleep(1);
+                done_cnt = 0;  // next incremented after the next grid barrier
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
