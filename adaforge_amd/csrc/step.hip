@@ -67,6 +67,15 @@ __device__ __forceinline__ void stc16(void* base, uint32_t off, v4u v) {
 }
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(kVmWait); }
 
+// threadIdx.x through an empty asm, read once per phase: the per-lane values derived from it are
+// then computed inside the phase that uses them.  Hoisted out of the phase loop (the thread index
+// is loop-invariant) they would hold registers through every phase, the weight ring's included.
+__device__ __forceinline__ uint32_t tix() {
+    uint32_t t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // Wave-level global -> LDS copy of `bytes` (a multiple of 16) with coherent loads; the caller
 // waits with wait_vm().
 __device__ __forceinline__ void dma(const void* src, uint32_t bytes, uint8_t* lds, uint32_t lane) {
@@ -501,7 +510,7 @@ __device__ __forceinline__ void stage_digits(int kind, const Stage& in, uint32_t
     int8_t* dig = reinterpret_cast<int8_t*>(lds);
     BlockTab* tab = reinterpret_cast<BlockTab*>(lds + (size_t)nst * 512);
     float* xs = reinterpret_cast<float*>(lds + xs_off);
-    const uint32_t tid = threadIdx.x, n8 = K / 8, o = tid;
+    const uint32_t tid = tix(), n8 = K / 8, o = tid;
     const bool ok = o < n8;
     float t[8], v[8], w[8];
 #pragma unroll
@@ -670,7 +679,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     double* dred = sh.dred;
     float* ml = sh.fred;  // [GQ][2]: max and sum of each query head's softmax
 
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t tid = tix(), lane = tid & 63, wave = wave_id();
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen), n = t1 - t0;
     const uint32_t ring = L.ring;
     const bool append = t1 == pos + 1;
@@ -1114,7 +1123,6 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);  // read after the first __syncthreads
     if (tid == 0) done_cnt = 0;
     Ring r;
-    const LaneK lk = lane_k(lane);
     if (wave != 0) {
         const uint32_t w = blockIdx.x * kStreamWaves + (wave - 1);
         const uint64_t o0 = a.stream_off[w], o1 = a.stream_off[w + 1];
@@ -1133,6 +1141,8 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     }
 
     for (int32_t ph = 0; ph < n_phases; ++ph) {
+        const uint32_t tid = tix(), lane = tid & 63;
+        const LaneK lk = lane_k(lane);
         const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
         // after a GEMV phase wave 0 has waited for the streaming waves (done_cnt) and for its stores
         if (ph > 0 && !grid_sync(g, (uint32_t)(ph - 1) % kPhases == P_ATTN)) {
