@@ -461,20 +461,21 @@ __device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const In
     if (kind == S_DIGITS) {
         dma_all(in.dig, nst * kStepImg, img, wave, lane);
     } else if (kind == S_RESID) {
-        dma_all(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), wave, lane);
-        dma_all(in.res, K * 4, reinterpret_cast<uint8_t*>(xs + K), wave, lane);
+        dma_all(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), wave, lane);  // the residual is in xs + K
     } else {
         embed_row(emb, xs, wave * 64 + lane, kThreads);
     }
     wait_vm();
 }
 
-// Wave 0: the norm weights (constant) of a residual prologue into their LDS slots.
-__device__ __forceinline__ void preload_norms(const float* w_a, const float* w_n, uint32_t K, uint32_t xs_off,
-                                              uint8_t* lds, uint32_t lane) {
+// Wave 0: what a residual prologue reads that the phase before it does not change, into its LDS
+// slots: the residual (written two phases earlier) and the norm weights.
+__device__ __forceinline__ void preload_norms(int kind, const Stage& in, uint32_t K, uint32_t xs_off, uint8_t* lds,
+                                              uint32_t lane) {
     float* xs = reinterpret_cast<float*>(lds + xs_off);
-    if (w_a) dma(w_a, K * 4, reinterpret_cast<uint8_t*>(xs + 2 * K), lane);
-    dma(w_n, K * 4, reinterpret_cast<uint8_t*>(xs + 3 * K), lane);
+    if (kind == S_RESID) dma(in.res, K * 4, reinterpret_cast<uint8_t*>(xs + K), lane);
+    if (in.w_a) dma(in.w_a, K * 4, reinterpret_cast<uint8_t*>(xs + 2 * K), lane);
+    dma(in.w_n, K * 4, reinterpret_cast<uint8_t*>(xs + 3 * K), lane);
 }
 
 // Wave 0 of workgroup 0: the residual left in xs[0, K) by stage_digits.
@@ -1063,12 +1064,12 @@ __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t
         if (item < ag.items) attention_pre<GQ>(L, pos, item / ag.chunks, item % ag.chunks, ag.clen, ag.start, lds, lane);
     } else if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
-        preload_norms(d.in.w_a, d.in.w_n, d.K, a.xs_off, lds, lane);
+        preload_norms(d.in_kind, d.in, d.K, a.xs_off, lds, lane);
     }
 }
 
-// The norm weights of GEMV phase ph (qkv, gate/up), copied by the streaming waves once their records
-// are consumed: waves 1-7 each take every 7th KB.  Returns false for other phases (left to
+// The residual and norm weights of GEMV phase ph (qkv, gate/up), copied by the streaming waves once
+// their records are consumed: waves 1-7 each take every 7th KB.  Returns false for other phases (left to
 // phase_pre on wave 0).
 __device__ __forceinline__ bool norms_pre_part(const StepArgs& a, int32_t ph, int32_t n_phases, uint8_t* lds,
                                                uint32_t wave, uint32_t lane) {
@@ -1077,6 +1078,8 @@ __device__ __forceinline__ bool norms_pre_part(const StepArgs& a, int32_t ph, in
     if (kind != P_QKV && kind != P_GATEUP) return false;
     const Gemv d = describe(a, l, kind);
     float* xs = reinterpret_cast<float*>(lds + a.xs_off);
+    if (d.in_kind == S_RESID)
+        dma_part(d.in.res, d.K * 4, reinterpret_cast<uint8_t*>(xs + d.K), wave - 1, kStreamWaves, lane);
     if (d.in.w_a) dma_part(d.in.w_a, d.K * 4, reinterpret_cast<uint8_t*>(xs + 2 * d.K), wave - 1, kStreamWaves, lane);
     dma_part(d.in.w_n, d.K * 4, reinterpret_cast<uint8_t*>(xs + 3 * d.K), wave - 1, kStreamWaves, lane);
     return true;
@@ -1090,7 +1093,7 @@ __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, i
     if (kind == P_ATTN) return AttnLds<GQ>::pre_offset();
     if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
-        return (size_t)a.xs_off + (size_t)8 * d.K;
+        return (size_t)a.xs_off + (size_t)4 * d.K;  // from the residual's slot
     }
     return ~(size_t)0;
 }
