@@ -45,7 +45,16 @@ struct Q6View {
     const uint16_t* d;
     uint32_t rows;
     uint32_t units;  // columns / 64
+    const uint8_t* t;  // head records: [ceil(rows / 16)][columns / 256][kQ6Rec] (upload_q6)
 };
+
+// A head record: 16 rows x one 256-weight super-block.  Lane l = 16 g + r (row r of the tile,
+// 16-element group g of a 64-weight k-block kb) owns 12 code dwords (3 per kb: L0, L1, H) at
+// [p = q / 4][l][q % 4] for dword q, its sub-block scales sc[r][4 kb + g] at 3072 + 4 l (byte kb),
+// and the row's d at 3328 + 2 r.  L0 byte b = c_b | c_{4+b} << 4 (low nibbles), L1 byte b =
+// c_{8+b} | c_{12+b} << 4, H byte b = the high bit pairs of c_b, c_{4+b}, c_{8+b}, c_{12+b}, where
+// c_j is the 6-bit code of weight 64 kb + 16 g + j.
+constexpr uint32_t kQ6Rec = 3360;
 
 // ---- input stages (the GEMV prologue builds the fp32 input vector in LDS) -------------------
 enum InputKind : int {

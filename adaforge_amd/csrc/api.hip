@@ -251,13 +251,62 @@ int upload_q4(Q4Dev& d, const std::vector<af_matrix>& parts) {
 }
 
 struct Q6Dev {
-    DevMem a, b, h, s, d;
+    DevMem a, b, h, s, d, t;
     uint32_t rows = 0, columns = 0;
     Q6View view() const {
         return Q6View{a.as<uint8_t>(), b.as<uint8_t>(), h.as<uint8_t>(), s.as<uint32_t>(), d.as<uint16_t>(), rows,
-                      columns / 64};
+                      columns / 64, t.as<uint8_t>()};
     }
 };
+
+// Head records (kQ6Rec) from GGUF Q6_K super-blocks: rows padded to a multiple of 16 with zero
+// codes and scales.  Weight e of a super-block (q6.rs layout): low nibble of ql[64 (e / 128) +
+// 32 (e / 32 % 2) + e % 32] (the high nibble when e % 128 >= 64), high bits (qh[32 (e / 128) +
+// e % 32] >> 2 (e % 128 / 32)) & 3, scale sc[e / 16], d at byte 208.
+std::vector<uint8_t> q6_head_records(const uint8_t* src, uint32_t columns, uint32_t rows) {
+    const uint64_t sblocks = columns / 256, tiles = (rows + 15) / 16;
+    std::vector<uint8_t> T(tiles * sblocks * kQ6Rec, 0);
+    parallel_rows(tiles * sblocks, [&](uint64_t b0, uint64_t e0) {
+        for (uint64_t i = b0; i < e0; ++i) {
+            const uint64_t tile = i / sblocks, sbk = i % sblocks;
+            uint8_t* rec = &T[i * kQ6Rec];
+            for (uint32_t r = 0; r < 16; ++r) {
+                const uint64_t row = tile * 16 + r;
+                if (row >= rows) continue;
+                const uint8_t* blk = src + (row * sblocks + sbk) * 210;
+                const uint8_t *ql = blk, *qh = blk + 128, *sc = blk + 192;
+                rec[3328 + 2 * r] = blk[208];
+                rec[3329 + 2 * r] = blk[209];
+                for (uint32_t g = 0; g < 4; ++g) {
+                    const uint32_t lane = 16 * g + r;
+                    for (uint32_t kb = 0; kb < 4; ++kb) {
+                        uint8_t c[16];
+                        for (uint32_t j = 0; j < 16; ++j) {
+                            const uint32_t e = 64 * kb + 16 * g + j, l = e % 128;
+                            const uint8_t lo = ql[64 * (e / 128) + 32 * (l / 32 % 2) + l % 32];
+                            const uint8_t nib = l >= 64 ? (uint8_t)(lo >> 4) : (uint8_t)(lo & 15);
+                            const uint8_t hi = (uint8_t)((qh[32 * (e / 128) + l % 32] >> (2 * (l / 32))) & 3);
+                            c[j] = (uint8_t)(nib | (hi << 4));
+                        }
+                        uint8_t w[12];
+                        for (uint32_t b = 0; b < 4; ++b) {
+                            w[b] = (uint8_t)((c[b] & 15) | ((c[4 + b] & 15) << 4));
+                            w[4 + b] = (uint8_t)((c[8 + b] & 15) | ((c[12 + b] & 15) << 4));
+                            w[8 + b] = (uint8_t)((c[b] >> 4) | ((c[4 + b] >> 4) << 2) | ((c[8 + b] >> 4) << 4) |
+                                                 ((c[12 + b] >> 4) << 6));
+                        }
+                        for (uint32_t q = 0; q < 3; ++q) {  // dwords 3 kb .. 3 kb + 2 of the lane
+                            const uint32_t dw = 3 * kb + q;
+                            std::memcpy(rec + (dw / 4) * 1024 + lane * 16 + (dw % 4) * 4, w + 4 * q, 4);
+                        }
+                        rec[3072 + lane * 4 + kb] = sc[4 * kb + g];
+                    }
+                }
+            }
+        }
+    });
+    return T;
+}
 
 int upload_q6(Q6Dev& dv, const uint8_t* src, uint32_t columns, uint32_t rows) {
     const uint64_t units = columns / 64, sblocks = columns / 256;
@@ -287,6 +336,8 @@ int upload_q6(Q6Dev& dv, const uint8_t* src, uint32_t columns, uint32_t rows) {
     if ((rc = dev_upload(dv.h, H.data(), H.size(), "Q6_K upload"))) return rc;
     if ((rc = dev_upload(dv.s, S.data(), S.size() * 4, "Q6_K upload"))) return rc;
     if ((rc = dev_upload(dv.d, D.data(), D.size() * 2, "Q6_K upload"))) return rc;
+    const std::vector<uint8_t> T = q6_head_records(src, columns, rows);
+    if ((rc = dev_upload(dv.t, T.data(), T.size(), "Q6_K upload"))) return rc;
     dv.rows = rows;
     dv.columns = columns;
     return AF_OK;

@@ -131,6 +131,15 @@ __device__ inline float block_max_f(float v, float* red) {
     return t;
 }
 
+// Sum over the four lanes of a row (l % 16 equal), left in every lane: the 32-lane halves, then
+// the 16-lane rows, swapped in registers (v_permlane32_swap / v_permlane16_swap).
+__device__ __forceinline__ float row_total(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float w = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // f32(x * r * w) with the products in double, as the FP64 RMSNorm oracle rounds its output.
 __device__ __forceinline__ float norm_apply(float x, double r, float w) {
     return (float)__dmul_rn(__dmul_rn((double)x, r), (double)w);
@@ -318,6 +327,17 @@ __device__ inline void input_stage(const InputStage& in, float* xs, uint32_t K, 
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// LDS access by 32-bit byte address (ds_* with a VGPR address and no 64-bit arithmetic).
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+template <typename T>
+__device__ __forceinline__ T lds_at(uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
+}
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)reinterpret_cast<uintptr_t>((const lds_u8*)p);
+}
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
 
 // Streaming loads of weights (read once per step): non-temporal hint, global address space

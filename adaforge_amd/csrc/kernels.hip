@@ -132,123 +132,169 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
     return v > bv || (v == bv && i < bi);
 }
 
-template <int R>
-struct Q6Rows {
-    uint4 a[R], b[R], h[R];
-    uint32_t s[R];
-    uint16_t d[R];
+// ---- Q6_K head on the int8 matrix cores --------------------------------------------------------
+//
+// The table is read as records of 16 rows x one 256-weight super-block (Q6View::t, kQ6Rec bytes,
+// built at upload).  Per record, four v_mfma_i32_16x16x64_i8 over its 64-weight k-blocks: A = the
+// input's digit planes (row 4 g + t: digit t of 16-element group g; the 16 lanes whose k-group is
+// g read them, the others a zero block), B = the codes of (group g, row r) at lane 16 g + r, as
+// the lane's 16 unsigned 6-bit codes.  Lane 16 g + r then holds D[4 g + t][r] for t = 0..3, which
+// it folds with the group's plane scales and its sub-block scale, and with the row's d once per
+// record.  Input x_j = s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) per 16-element group, exactly.
+
+constexpr int kHeadRing = 6;  // records in flight per wave
+
+// A wave's head state: its ring of records and its position in its tile sequence.
+struct HeadRing {
+    v4u code[kHeadRing][3];  // the lane's 12 code dwords per record (3 per k-block)
+    uint32_t sc[kHeadRing];  // the lane's 4 sub-block scales (int8, one per k-block)
+    uint32_t d[kHeadRing];   // the lane's row d (fp16 in the low half)
 };
 
-template <int R>
-__device__ __forceinline__ void q6_load(Q6Rows<R>& o, const Q6View& w, uint32_t r0, uint32_t u, bool act) {
-    const uint32_t sblocks = w.units / 4;
+// 16 unsigned 6-bit codes from a lane's dwords L0, L1 (low nibbles of codes b and 4 + b in byte b,
+// and of codes 8 + b, 12 + b) and H (high bit pairs of codes b, 4 + b, 8 + b, 12 + b in byte b).
+__device__ __forceinline__ v4i q6_unpack(uint32_t l0, uint32_t l1, uint32_t h) {
+    constexpr uint32_t M = 0x0F0F0F0Fu, M3 = 0x30303030u;
+    return v4i{(int)((l0 & M) | ((h << 4) & M3)), (int)(((l0 >> 4) & M) | ((h << 2) & M3)),
+               (int)((l1 & M) | (h & M3)), (int)(((l1 >> 4) & M) | ((h >> 2) & M3))};
+}
+
+__device__ __forceinline__ void head_fill(HeadRing& hr, int u, const __amdgpu_buffer_rsrc_t& rs, uint32_t rec,
+                                          uint32_t lane) {
+    const int off = (int)(rec * kQ6Rec);
 #pragma unroll
-    for (int i = 0; i < R; ++i) {
-        const uint32_t row = r0 + i;
-        const bool ok = act && row < w.rows;
-        const size_t off = ((size_t)row * w.units + u) * 16;
-        o.a[i] = ok ? *reinterpret_cast<const uint4*>(w.a + off) : make_uint4(0, 0, 0, 0);
-        o.b[i] = ok ? *reinterpret_cast<const uint4*>(w.b + off) : make_uint4(0, 0, 0, 0);
-        o.h[i] = ok ? *reinterpret_cast<const uint4*>(w.h + off) : make_uint4(0, 0, 0, 0);
-        o.s[i] = ok ? w.s[(size_t)row * w.units + u] : 0u;
-        o.d[i] = ok ? w.d[(size_t)row * sblocks + (u >> 2)] : (uint16_t)0;
-    }
+    for (int p = 0; p < 3; ++p) hr.code[u][p] = __builtin_amdgcn_raw_buffer_load_b128(rs, p * 1024 + lane * 16, off, 2);
+    hr.sc[u] = __builtin_amdgcn_raw_buffer_load_b32(rs, 3072 + lane * 4, off, 2);
+    hr.d[u] = __builtin_amdgcn_raw_buffer_load_b16(rs, 3328 + (lane & 15) * 2, off, 2);
 }
 
 template <int IN>
-__global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
-    constexpr int R = kHeadRows;
-    extern __shared__ float xs[];
-    __shared__ double red[8];
-    __shared__ float wv[256];
-    __shared__ uint32_t wi[256], wb[256];
+__global__ __launch_bounds__(512) void q6_head_kernel(HeadArgs a) {
+    extern __shared__ __align__(16) uint8_t hl[];  // xs [K] f32, digit planes [K / 16][4][16], tab [K / 16]
+    __shared__ double red[16];
+    __shared__ float wv[8];
+    __shared__ uint32_t wi[8], wb[8];
     __shared__ bool last;
+    __shared__ uint4 zero_blk[2];
 
     if (a.state && a.state[ST_STOP]) return;
-    const uint32_t units = a.w.units, K = units * 64;
-    const int lane = threadIdx.x & 63, wave = (int)wave_id();
-    const bool act = (uint32_t)lane < units;
-    const uint32_t u = act ? (uint32_t)lane : 0;
-    const uint32_t rows = a.w.rows;
-    const uint32_t stride = gridDim.x * 4 * R;
-    uint32_t r0 = (blockIdx.x * 4 + wave) * R;
-    Q6Rows<R> cur;
-    q6_load(cur, a.w, r0, u, act);  // weights first: their latency overlaps the input stage
+    const uint32_t K = a.w.units * 64, sb = K / 256, rows = a.w.rows, ntiles = (rows + 15) / 16;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t nw = gridDim.x * (blockDim.x / 64), gw = blockIdx.x * (blockDim.x / 64) + wave;
+    float* xs = reinterpret_cast<float*>(hl);
+    uint8_t* dig = hl + (size_t)K * 4;
+    float4* tab = reinterpret_cast<float4*>(dig + (size_t)K * 4);
+    if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);
+
+    // the wave's records: tiles gw, gw + nw, ... below ntiles, sb records each
+    const uint32_t my_tiles = gw < ntiles ? (ntiles - gw + nw - 1) / nw : 0;
+    const uint32_t total = my_tiles * sb;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w.t), 0, (int)(ntiles * sb * kQ6Rec), 0x00020000);
+    HeadRing hr;
+    uint32_t ft = gw, fs = 0;  // next record to request: tile ft, super-block fs (past the end: record 0)
+    auto fill = [&](int u) {
+        const uint32_t rec = ft < ntiles ? ft * sb + fs : 0u;
+        head_fill(hr, u, rs, rec, lane);
+        if (++fs == sb) {
+            fs = 0;
+            ft += nw;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < kHeadRing; ++u) fill(u);  // weights first: their latency overlaps the input stage
 
     if constexpr (IN == IN_PLAIN) {
         const float4* src = reinterpret_cast<const float4*>(a.in.x);
         float4* dst = reinterpret_cast<float4*>(xs);
-        for (uint32_t i = threadIdx.x; i < K / 4; i += blockDim.x) dst[i] = src[i];
+        for (uint32_t i = tid; i < K / 4; i += blockDim.x) dst[i] = src[i];
         __syncthreads();
     } else {
         input_stage<IN>(a.in, xs, K, red);
     }
-    const uint32_t base = (u >> 2) * 256 + ((u >> 1) & 1) * 128 + (u & 1) * 16;
-    float x[4][16], bias[4];
+    // digit image: thread i < K / 16 takes group i
+    if (tid < K / 16) {
+        float v0[8], v1[8], m = 0.0f, sum = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        float t = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            x[q][j] = act ? xs[base + q * 32 + j] : 0.0f;
-            t += x[q][j];
+        for (int k = 0; k < 8; ++k) {
+            v0[k] = xs[16 * tid + k];
+            v1[k] = xs[16 * tid + 8 + k];
+            m = fmaxf(m, fmaxf(fabsf(v0[k]), fabsf(v1[k])));
+            sum += v0[k] + v1[k];
         }
-        bias[q] = 32.0f * t;
+        uint32_t w0[4][2], w1[4][2];
+        digit_words(v0, m, w0);
+        digit_words(v1, m, w1);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            reinterpret_cast<uint4*>(dig)[tid * 4 + t] = make_uint4(w0[t][0], w0[t][1], w1[t][0], w1[t][1]);
+        const float sc = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
+        tab[tid] = make_float4(ldexpf(sc, -14), ldexpf(sc, -21), -32.0f * sum, 0.0f);
     }
+    __syncthreads();
 
-    float bv = -INFINITY;
+    const uint32_t g = lane >> 4, r = lane & 15;
+    const bool aon = (r >> 2) == g;
+    const uint32_t a0 = aon ? lds_addr(dig) + r * 16 : lds_addr(zero_blk), am = aon ? 256u : 0u;
+    const uint32_t t0 = lds_addr(tab) + g * 16;
+    float bv = -INFINITY, acc = 0.0f;
     uint32_t bi = 0xFFFFFFFFu, bad = 0;
-    while (r0 < rows) {
-        const uint32_t nr = r0 + stride;
-        Q6Rows<R> nxt;
-        q6_load(nxt, a.w, nr, u, act && nr < rows);
-        float acc[R];
+    uint32_t ct = gw, cs = 0;  // record being consumed
+    auto record = [&](int u) {
+        float sbacc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-            const uint32_t av[4] = {cur.a[i].x, cur.a[i].y, cur.a[i].z, cur.a[i].w};
-            const uint32_t bw[4] = {cur.b[i].x, cur.b[i].y, cur.b[i].z, cur.b[i].w};
-            const uint32_t hv[4] = {cur.h[i].x, cur.h[i].y, cur.h[i].z, cur.h[i].w};
-            const float d = h2f(cur.d[i]);
-            float t = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                float sq = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const uint32_t c = q6_codes(av[k], bw[k], hv[k], q);
-                    sq = fmaf((float)(c & 0xFFu), x[q][4 * k + 0], sq);
-                    sq = fmaf((float)((c >> 8) & 0xFFu), x[q][4 * k + 1], sq);
-                    sq = fmaf((float)((c >> 16) & 0xFFu), x[q][4 * k + 2], sq);
-                    sq = fmaf((float)(c >> 24), x[q][4 * k + 3], sq);
-                }
-                const float ds = d * (float)(int8_t)(cur.s[i] >> (8 * q));
-                t = fmaf(ds, sq - bias[q], t);
-            }
-            acc[i] = wave_sum(t);
+        for (int kb = 0; kb < 4; ++kb) {
+            const uint32_t wl0 = hr.code[u][(3 * kb) / 4][(3 * kb) % 4];
+            const uint32_t wl1 = hr.code[u][(3 * kb + 1) / 4][(3 * kb + 1) % 4];
+            const uint32_t wh = hr.code[u][(3 * kb + 2) / 4][(3 * kb + 2) % 4];
+            const uint32_t blk = cs * 4 + kb;  // k-block of the row
+            const v4i av = lds_at<v4i>(a0 + blk * am);
+            const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, q6_unpack(wl0, wl1, wh), v4i{0, 0, 0, 0}, 0, 0, 0);
+            const v4f tb = lds_at<v4f>(t0 + blk * 64);
+            // 2^14 D0 + 2^7 D1 + D2 is exact in int32 (|D_t| <= 16 * 63 * 64)
+            const int I = (d[0] << 14) + (d[1] << 7) + d[2];
+            float in = fmaf((float)I, tb.x, tb.z);
+            in = fmaf((float)d[3], tb.y, in);
+            sbacc = fmaf((float)(int8_t)(hr.sc[u] >> (8 * kb)), in, sbacc);
         }
-        if (lane == 0) {
-#pragma unroll
-            for (int i = 0; i < R; ++i) {
-                const uint32_t row = r0 + i;
-                if (row < rows) {
-                    const float v = acc[i];
-                    if (!isfinite(v)) bad = 1;
-                    else if (better(v, row, bv, bi)) {
-                        bv = v;
-                        bi = row;
-                    }
+        acc = fmaf(h2f((uint16_t)hr.d[u]), sbacc, acc);
+        fill(u);  // after the last use of the slot's registers
+        if (++cs == sb) {  // the tile's last record: its 16 rows
+            const float v = row_total(acc);
+            acc = 0.0f;
+            const uint32_t row = ct * 16 + r;
+            if (lane < 16 && row < rows) {
+                if (a.logits) a.logits[row] = v;
+                if (!isfinite(v)) bad = 1;
+                else if (better(v, row, bv, bi)) {
+                    bv = v;
+                    bi = row;
                 }
             }
+            cs = 0;
+            ct += nw;
         }
-        if (a.logits) {
-            float v = acc[0];
+    };
+    for (uint32_t i = total / kHeadRing; i; --i) {
 #pragma unroll
-            for (int i = 1; i < R; ++i)
-                if (lane == i) v = acc[i];
-            if (lane < R && r0 + lane < rows) a.logits[r0 + lane] = v;
+        for (int u = 0; u < kHeadRing; ++u) record(u);
+    }
+    const uint32_t rem = total % kHeadRing;
+#pragma unroll
+    for (int u = 0; u < kHeadRing - 1; ++u)
+        if ((uint32_t)u < rem) record(u);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the ring's last requests (past the end) before exit
+
+    // wave, then workgroup, then grid: the greatest value, smallest id on ties, any non-finite
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const uint32_t oi = __shfl_xor(bi, o);
+        if (better(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
         }
-        cur = nxt;
-        r0 = nr;
+        bad |= __shfl_xor(bad, o);
     }
     if (lane == 0) {
         wv[wave] = bv;
@@ -257,7 +303,7 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w) {
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) {
             if (better(wv[w], wi[w], bv, bi)) {
                 bv = wv[w];
                 bi = wi[w];
@@ -283,23 +329,31 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
         }
         flag |= p.z;
     }
-    wv[threadIdx.x] = v;
-    wi[threadIdx.x] = id;
-    wb[threadIdx.x] = flag;
-    __syncthreads();
-    for (uint32_t h = blockDim.x / 2; h > 0; h >>= 1) {
-        if (threadIdx.x < h) {
-            const uint32_t o = threadIdx.x + h;
-            if (better(wv[o], wi[o], wv[threadIdx.x], wi[threadIdx.x])) {
-                wv[threadIdx.x] = wv[o];
-                wi[threadIdx.x] = wi[o];
-            }
-            wb[threadIdx.x] |= wb[o];
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float ov = __shfl_xor(v, o);
+        const uint32_t oi = __shfl_xor(id, o);
+        if (better(ov, oi, v, id)) {
+            v = ov;
+            id = oi;
         }
-        __syncthreads();
+        flag |= __shfl_xor(flag, o);
     }
+    if (lane == 0) {
+        wv[wave] = v;
+        wi[wave] = id;
+        wb[wave] = flag;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        const uint32_t best = wi[0], flagged = wb[0] || best >= rows;
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) {
+            if (better(wv[w], wi[w], v, id)) {
+                v = wv[w];
+                id = wi[w];
+            }
+            flag |= wb[w];
+        }
+        const uint32_t best = id, flagged = flag || best >= rows;
         if (a.result) {
             a.result[0] = best;
             a.result[1] = flagged;
@@ -314,31 +368,31 @@ __global__ __launch_bounds__(256) void q6_head_kernel(HeadArgs a) {
             if (stop) a.state[ST_STOP] = 1u;
             a.state[ST_POS] = pos + 1;
             if (a.records) {
-                StepRecord r;
-                r.id = best;
-                r.bad = flagged;
-                r.stop = stop;
-                r.done = 1u;
-                a.records[pos + 1] = r;
+                StepRecord rc;
+                rc.id = best;
+                rc.bad = flagged;
+                rc.stop = stop;
+                rc.done = 1u;
+                a.records[pos + 1] = rc;
             }
         }
         *a.counter = 0u;
     }
 }
 
-// Persistent grid: at most three workgroups per CU, each wave striding over row groups.
+// One workgroup of 8 waves per CU (at most), each wave striding over 16-row tiles.
 uint32_t head_grid(uint32_t rows) {
-    uint32_t per_block = 4 * kHeadRows;
-    uint32_t g = (rows + per_block - 1) / per_block;
-    return g > 768 ? 768 : g;
+    const uint32_t tiles = (rows + 15) / 16;
+    const uint32_t g = (tiles + 7) / 8;
+    return g > 256 ? 256 : g;
 }
 
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s) {
-    const size_t lds = (size_t)a.w.units * 64 * sizeof(float);
+    const size_t K = (size_t)a.w.units * 64, lds = K * 4 + K * 4 + K;  // xs, digit planes, tab
     switch (in_kind) {
-        case IN_PLAIN: hipLaunchKernelGGL(q6_head_kernel<IN_PLAIN>, dim3(grid), dim3(256), lds, s, a); break;
-        case IN_NORM: hipLaunchKernelGGL(q6_head_kernel<IN_NORM>, dim3(grid), dim3(256), lds, s, a); break;
-        case IN_RESID: hipLaunchKernelGGL(q6_head_kernel<IN_RESID>, dim3(grid), dim3(256), lds, s, a); break;
+        case IN_PLAIN: hipLaunchKernelGGL(q6_head_kernel<IN_PLAIN>, dim3(grid), dim3(512), lds, s, a); break;
+        case IN_NORM: hipLaunchKernelGGL(q6_head_kernel<IN_NORM>, dim3(grid), dim3(512), lds, s, a); break;
+        case IN_RESID: hipLaunchKernelGGL(q6_head_kernel<IN_RESID>, dim3(grid), dim3(512), lds, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();

@@ -196,14 +196,6 @@ __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_
     return v;
 }
 
-// Sum over the four lanes of a row (l % 16 equal), left in every lane: the 32-lane halves, then
-// the 16-lane rows, swapped in registers (v_permlane32_swap / v_permlane16_swap).
-__device__ __forceinline__ float row_total(float v) {
-    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    const float w = __uint_as_float(h[0]) + __uint_as_float(h[1]);
-    const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(w), __float_as_uint(w), false, false);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
 
 // Digit image of a GEMV input, nst * kStepImg bytes: the digit planes dig[b * 4 + t][32] of
 // block b (nst * 512 bytes), then one entry per block: for x_j = s (q0 + q1 2^-7 + q2 2^-14 +
@@ -217,15 +209,6 @@ __device__ __forceinline__ BlockTab block_tab(float m, float sum) {
     return BlockTab{ldexpf(s, -14), ldexpf(s, -21), -8.0f * sum, 0.0f};
 }
 
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
-template <typename T>
-__device__ __forceinline__ T lds_at(uint32_t addr) {
-    return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
-}
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)reinterpret_cast<uintptr_t>((const lds_u8*)p);
-}
 
 // A streaming wave's weight records: a ring of kRing in registers, refilled from the wave's run
 // as each is consumed, across phase (and layer) boundaries: the next phase's first records are
