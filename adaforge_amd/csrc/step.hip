@@ -758,12 +758,16 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
 
     // scores: 16 lanes per token (16 channels each), 32 token groups; q is re-read from LDS for
     // every token (registers stay free for the weight loads in flight)
-    {
+    // The K and V rows come from LDS (staged chunk, or the new token) or from the cache; the two
+    // kinds of chunk run separate loops, so a staged chunk's loops hold no global load, and the
+    // compiler has no reason to wait for a streaming wave's weight loads in flight.
+    auto score_rows = [&](auto staged_c) {
+        constexpr bool ST = decltype(staged_c)::value;
         const uint32_t grp = tid >> 4, j = tid & 15;
         for (uint32_t t = t0 + grp; t < t1; t += 32) {
             v4u k0, k1;
-            if (staged || t == pos) {
-                const uint16_t* kr = staged ? sh.kst + (t - t0) * D : sh.knew;
+            if (ST || t == pos) {
+                const uint16_t* kr = ST ? sh.kst + (t - t0) * D : sh.knew;
                 const v4u* kp = reinterpret_cast<const v4u*>(kr + 16 * j);
                 k0 = kp[0];
                 k1 = kp[1];
@@ -795,7 +799,11 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
                 if (j == 0) scores[q * kStepMaxClen + (t - t0)] = d * L.scale;
             }
         }
-    }
+    };
+    // scores: 16 lanes per token (16 channels each), 32 token groups; q is re-read from LDS for
+    // every token (registers stay free for the weight loads in flight)
+    if (staged) score_rows(std::true_type{});
+    else score_rows(std::false_type{});
     __syncthreads();
 
     // softmax: wave q < GQ normalises query head q's scores on its own (no block reduction)
@@ -819,7 +827,8 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     __syncthreads();
 
     // values: 32 lanes per token row (8 channels each), 16 token groups
-    {
+    auto value_rows = [&](auto staged_c) {
+        constexpr bool ST = decltype(staged_c)::value;
         const uint32_t tg = tid >> 5, dl = tid & 31;
         float acc[GQ][8];
 #pragma unroll
@@ -828,8 +837,8 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
             for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
         for (uint32_t t = t0 + tg; t < t1; t += 16) {
             v4u vv;
-            if (staged || t == pos) {
-                const uint16_t* vr = staged ? sh.vst + (t - t0) * D : sh.vnew;
+            if (ST || t == pos) {
+                const uint16_t* vr = ST ? sh.vst + (t - t0) * D : sh.vnew;
                 vv = *reinterpret_cast<const v4u*>(vr + 8 * dl);
             } else {
                 vv = *gp(reinterpret_cast<const v4u*>(L.vcache + ((size_t)h * ring + t % ring) * D + 8 * dl));
@@ -852,7 +861,9 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         for (int q = 0; q < GQ; ++q)
 #pragma unroll
             for (int e = 0; e < 8; ++e) vred[(tg * GQ + q) * D + 8 * dl + e] = acc[q][e];
-    }
+    };
+    if (staged) value_rows(std::true_type{});
+    else value_rows(std::false_type{});
     __syncthreads();
 
     // chunk partial o[q][d] (unnormalised), m[q], l[q], staged in LDS and stored by wave 0
@@ -1162,8 +1173,11 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
                 consume_phase(r, nst, d.sh.T, __builtin_amdgcn_readfirstlane(fe), lds,
                               reinterpret_cast<const v4i*>(zero_blk), part, wave, lane, lk, &done_cnt);
-                // waited for by the next phase's staging (wait_vm) before its barrier
+                // waited for here, so that no LDS copy is pending at the loop's back edge: the
+                // compiler would otherwise wait for every load in flight (this wave's weight ring
+                // included) before the next phase's first LDS read
                 if (pre_now) norms_pre_part(a, ph + 1, n_phases, lds, wave, lane);
+                wait_vm();
                 if (wave == 1) stamp_at(g, g.k, M_CONSUMED);
             } else {
                 if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
