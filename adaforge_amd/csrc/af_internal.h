@@ -112,7 +112,10 @@ struct Q4Args {
 // stop flag (set by the head when it selects a stop id or sees non-finite logits;
 // every kernel of a decode step returns immediately while it is set), and the
 // number of stop ids.
-enum { ST_POS = 0, ST_BAD = 1, ST_STOP = 2, ST_NSTOP = 3, ST_WORDS = 4 };
+// Session state words on the device.  The host uploads the first ST_HOST_WORDS; ST_EPOCH counts
+// the step kernel's launches (the last workgroup out advances it) and tags the vectors that
+// the step kernel publishes without a grid barrier.
+enum { ST_POS = 0, ST_BAD = 1, ST_STOP = 2, ST_NSTOP = 3, ST_EPOCH = 4, ST_HOST_WORDS = 4, ST_WORDS = 5 };
 constexpr uint32_t kMaxStopIds = 256;
 
 // Per-step record the head writes to mapped host memory: id, non-finite flag, stop flag.
@@ -196,6 +199,7 @@ struct StepArgs {
     const uint32_t* ids;
     uint32_t* state;
     float *X, *H, *QKV, *PROJ, *D;  // activations exchanged inside the launch
+    uint32_t *PROJT, *DT;           // o-proj and down outputs as (value, tag) word pairs, [hidden][2]
     int8_t *att_img, *act_img;      // digit images of the o-proj and down inputs
     float* part;                    // attention chunk partials
     uint32_t* counters;             // attention merge tickets, one per KV head

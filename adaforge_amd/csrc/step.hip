@@ -111,18 +111,19 @@ __device__ __forceinline__ void dma_part(const void* src, uint32_t bytes, uint8_
 struct Grid {
     uint32_t* bar;
     uint32_t k;       // barriers passed in this launch
+    uint32_t p;       // phase (of the timeline) the workgroup is in
     int* ok;          // LDS flag
     uint64_t* clock;  // optional timeline (StepArgs::clock)
 };
 
-// Thread 0 only.  Phase = barriers passed so far.
+// Thread 0 only.
 __device__ __forceinline__ void stamp_at(const Grid& g, uint32_t phase, uint32_t mark) {
     if (g.clock) g.clock[((size_t)phase * kStepMarks + mark) * gridDim.x + blockIdx.x] = wall_clock64();
 }
 // Wave 0 stores (every lane the same value to the same word): a branch on the wave index is
 // uniform, where one on the thread index would make the phase loop's control flow divergent.
 __device__ __forceinline__ void stamp(const Grid& g, uint32_t mark) {
-    if (wave_id() == 0) stamp_at(g, g.k, mark);
+    if (wave_id() == 0) stamp_at(g, g.p, mark);
 }
 
 // All threads call it.  Returns false (in every thread) if the barrier did not complete within
@@ -132,7 +133,7 @@ __device__ __forceinline__ void stamp(const Grid& g, uint32_t mark) {
 __device__ __forceinline__ bool grid_sync(Grid& g, bool lead) {
     if (lead) __syncthreads();
     if (threadIdx.x == 0) {
-        stamp_at(g, g.k, M_ARRIVE);
+        stamp_at(g, g.p, M_ARRIVE);
         const uint32_t per = gridDim.x / 8, grp = blockIdx.x & 7, k = g.k + 1;
         const uint32_t old =
             __hip_atomic_fetch_add(g.bar + 32 * (1 + grp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -147,11 +148,22 @@ __device__ __forceinline__ bool grid_sync(Grid& g, bool lead) {
             }
         }
         *g.ok = ok;
-        stamp_at(g, g.k + 1, M_START);
+        stamp_at(g, g.p + 1, M_START);
     }
     __syncthreads();
     ++g.k;
+    ++g.p;
     return __builtin_amdgcn_readfirstlane(*g.ok) != 0;  // uniform: keeps the phase loop scalar
+}
+
+// A phase boundary without a grid barrier: the next phase's input carries its own tags
+// (poll_tagged).  Only the timeline moves on.
+__device__ __forceinline__ void tagged_boundary(Grid& g) {
+    if (wave_id() == 0) {
+        stamp_at(g, g.p, M_ARRIVE);
+        stamp_at(g, g.p + 1, M_START);
+    }
+    ++g.p;
 }
 
 // Last workgroup out resets the barrier words for the next launch; with `advance` it also moves
@@ -159,7 +171,7 @@ __device__ __forceinline__ bool grid_sync(Grid& g, bool lead) {
 __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance, bool failed) {
     __syncthreads();
     if (threadIdx.x == 0) {
-        stamp_at(g, g.k, M_ARRIVE);
+        stamp_at(g, g.p, M_ARRIVE);
         if (failed) {
             __hip_atomic_store(state + ST_BAD, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(state + ST_STOP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -169,6 +181,7 @@ __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance
             for (uint32_t i = 0; i < 10; ++i)
                 __hip_atomic_store(g.bar + 32 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (advance) state[ST_POS] += 1u;
+            state[ST_EPOCH] += 1u;  // read by the next launch, which the end of this one orders
         }
     }
 }
@@ -427,28 +440,69 @@ __device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T,
 enum StageKind { S_EMBED = 0, S_RESID = 1, S_DIGITS = 2 };
 
 struct Stage {
-    const float *x, *res, *w_a, *w_n;
+    const float *res, *w_a, *w_n;
+    const uint32_t* xt;   // S_RESID: the input as (value, tag) word pairs (poll_tagged)
+    uint32_t tag;         // the tag of the input's current values
     float eps_a, eps_n, scale;
     const int8_t* dig;    // S_DIGITS
     float* x_out;         // S_EMBED / S_RESID: the residual, written by workgroup 0
     float* snap;          // optional copy of x_out
 };
 
-// Every wave, after the barrier: the activation inputs (the norm weights are already in LDS), or
-// the embedding row of the step's token.  A streaming wave's weight loads in flight were issued
-// before the barrier, so its wait here costs nothing the next phase would not wait for anyway.
-__device__ __forceinline__ void stage_inputs(int kind, const Stage& in, const InputStage& emb, uint32_t K, uint32_t nst,
+// A vector handed from one GEMV phase to the next without a grid barrier: element i is the word
+// pair (value, tag) at 8 i, stored by its producer with one 8-byte store, and tag identifies the
+// launch and layer that wrote it.  Every thread reads 16-byte pieces tid, tid + 512, .. (K <= 4096:
+// at most 4) and re-reads the pieces whose tags are not yet `tag`; a current piece's two values
+// go to xs.  A pair is never overwritten before every workgroup has read it: the grid barriers
+// between its consumer phase and its producer's next turn order the two.  Returns false (in the
+// whole wave) if the wave's pieces did not all become current within the spin limit.
+constexpr uint32_t kPollLimit = 1u << 20;
+
+__device__ __forceinline__ bool poll_tagged(const uint32_t* src, uint32_t K, uint32_t tag, float* xs, uint32_t tid) {
+    const __amdgpu_buffer_rsrc_t rs = rsrc(src);
+    const uint32_t n = K / 2;
+    uint32_t need = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        if (tid + kThreads * i < n) need |= 1u << i;
+    for (uint32_t spins = 0;; ++spins) {
+        v4u v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            v[i] = v4u{0u, 0u, 0u, 0u};
+            if (need >> i & 1) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + kThreads * i) * 16, 0, kSC1);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            if ((need >> i & 1) && v[i].y == tag && v[i].w == tag) {
+                reinterpret_cast<v2u*>(xs)[tid + kThreads * i] = v2u{v[i].x, v[i].z};
+                need &= ~(1u << i);
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(need != 0) == 0) return true;
+        if (spins >= kPollLimit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+// Every wave, after the phase boundary: the activation inputs (the norm weights are already in
+// LDS), or the embedding row of the step's token.  A streaming wave's weight loads in flight were
+// issued before the boundary, so its wait here costs nothing the next phase would not wait for
+// anyway.  Returns false (in the whole wave) if a tagged input did not become current.
+__device__ __forceinline__ bool stage_inputs(int kind, const Stage& in, const InputStage& emb, uint32_t K, uint32_t nst,
                                              uint32_t xs_off, uint8_t* lds, uint32_t wave, uint32_t lane) {
     uint8_t* img = lds;
     float* xs = reinterpret_cast<float*>(lds + xs_off);
+    bool ok = true;
     if (kind == S_DIGITS) {
         dma_all(in.dig, nst * kStepImg, img, wave, lane);
     } else if (kind == S_RESID) {
-        dma_all(in.x, K * 4, reinterpret_cast<uint8_t*>(xs), wave, lane);  // the residual is in xs + K
+        ok = poll_tagged(in.xt, K, in.tag, xs, wave * 64 + lane);  // the residual is in xs + K
     } else {
         embed_row(emb, xs, wave * 64 + lane, kThreads);
     }
     wait_vm();
+    return ok;
 }
 
 // Wave 0: what a residual prologue reads that the phase before it does not change, into its LDS
@@ -952,7 +1006,9 @@ struct Gemv {
     Stage in;
     InputStage emb;  // S_EMBED
     uint32_t K;      // input width
-    float* y;        // outputs (null for gate/up, whose output is the down input's digit image)
+    float* y;        // outputs (qkv, and the last layer's down, read by the head)
+    uint32_t* yt;    // outputs as (value, tag) pairs (o-proj, down): the next phase polls them
+    uint32_t ytag;
     uint32_t rows;
     uint32_t act_nst;
 };
@@ -965,7 +1021,8 @@ __device__ __forceinline__ Shape shape_of(CQ4View& m, bool pair) {
     return sh;
 }
 
-__device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t kind) {
+// tag0: the tag of layer 0's handed-over vectors in this launch (layer l: tag0 + l).
+__device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t kind, uint32_t tag0 = 0) {
     CLayer& L = layer_at(a, l);
     Gemv d{};
     if (kind == P_QKV) {
@@ -982,7 +1039,8 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         } else {
             CLayer& P = layer_at(a, l - 1);
             d.in_kind = S_RESID;
-            d.in.x = a.D;
+            d.in.xt = a.DT;
+            d.in.tag = tag0 + l - 1;
             d.in.res = a.H;
             d.in.w_a = P.post_ffn;
             d.in.eps_a = P.post_ffn_eps;
@@ -997,12 +1055,14 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         d.in_kind = S_DIGITS;
         d.in.dig = a.att_img;
         d.K = L.o.blocks * 32;
-        d.y = a.PROJ;
+        d.yt = a.PROJT;
+        d.ytag = tag0 + l;
         d.rows = L.o.rows;
     } else if (kind == P_GATEUP) {
         d.sh = shape_of(L.gate, true);
         d.in_kind = S_RESID;
-        d.in.x = a.PROJ;
+        d.in.xt = a.PROJT;
+        d.in.tag = tag0 + l;
         d.in.res = a.X;
         d.in.w_a = L.post_attn;
         d.in.eps_a = L.post_attn_eps;
@@ -1017,7 +1077,12 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         d.in_kind = S_DIGITS;
         d.in.dig = a.act_img;
         d.K = a.inter;
-        d.y = a.D;
+        if (l + 1 < a.n_layers) {
+            d.yt = a.DT;
+            d.ytag = tag0 + l;
+        } else {
+            d.y = a.D;
+        }
         d.rows = L.down.rows;
     }
     return d;
@@ -1105,20 +1170,22 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float part[kPart];
     __shared__ double red[16];
-    __shared__ int ok_flag, att_flag;
+    __shared__ int ok_flag, att_flag, poll_bad;
     __shared__ uint32_t done_cnt;  // streaming waves done with a GEMV phase, 64 per wave
     __shared__ float act_l[kMaxUnits][32];
 
     if (a.state[ST_STOP]) return;  // uniform: written only before the launch
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t pos = a.state[ST_POS];
-    Grid g{a.bar, 0u, &ok_flag, a.clock};
+    const uint32_t tag0 = a.state[ST_EPOCH] * a.n_layers + 1u;  // never 0, the tag of a cleared pair
+    Grid g{a.bar, 0u, 0u, &ok_flag, a.clock};
     stamp(g, M_START);
     bool failed = false;
     const int32_t n_phases = (int32_t)(kPhases * a.n_layers);
     __shared__ uint4 zero_blk[2];
     if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);  // read after the first __syncthreads
     if (tid == 0) done_cnt = 0;
+    if (tid == 0) poll_bad = 0;
     Ring r;
     if (wave != 0) {
         const uint32_t w = blockIdx.x * kStreamWaves + (wave - 1);
@@ -1141,10 +1208,17 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         const uint32_t tid = tix(), lane = tid & 63;
         const LaneK lk = lane_k(lane);
         const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
-        // after a GEMV phase wave 0 has waited for the streaming waves (done_cnt) and for its stores
-        if (ph > 0 && !grid_sync(g, (uint32_t)(ph - 1) % kPhases == P_ATTN)) {
-            failed = true;
-            break;
+        // The input of gate/up (o-proj's outputs) and of qkv after layer 0 (down's outputs) is
+        // handed over by tags; every other phase opens with a grid barrier.  After a GEMV phase
+        // wave 0 has waited for the streaming waves (done_cnt) and for its stores.
+        const bool tagged = kind == P_GATEUP || (kind == P_QKV && l > 0);
+        if (ph > 0) {
+            if (tagged) {
+                tagged_boundary(g);
+            } else if (!grid_sync(g, (uint32_t)(ph - 1) % kPhases == P_ATTN)) {
+                failed = true;
+                break;
+            }
         }
         if (kind == P_ATTN) {
             CLayer& L = layer_at(a, l);
@@ -1156,10 +1230,14 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             __syncthreads();
             stamp(g, M_STORED);
         } else {
-            const Gemv d = describe(a, l, kind);
+            const Gemv d = describe(a, l, kind, tag0);
             const uint32_t nst = d.sh.nst;
-            stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, a.xs_off, lds, wave, lane);
+            if (!stage_inputs(d.in_kind, d.in, d.emb, d.K, nst, a.xs_off, lds, wave, lane)) poll_bad = 1;
             __syncthreads();
+            if (__builtin_amdgcn_readfirstlane(poll_bad)) {
+                failed = true;
+                break;
+            }
             stamp(g, M_STAGED);
             zero_part_lds(part, tid);
             if (d.in_kind != S_DIGITS) stage_digits(d.in_kind, d.in, d.K, nst, a.xs_off, lds, red);
@@ -1178,7 +1256,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 // included) before the next phase's first LDS read
                 if (pre_now) norms_pre_part(a, ph + 1, n_phases, lds, wave, lane);
                 wait_vm();
-                if (wave == 1) stamp_at(g, g.k, M_CONSUMED);
+                if (wave == 1) stamp_at(g, g.p, M_CONSUMED);
             } else {
                 if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
                 if (pre_now && (ph + 1 >= n_phases || (uint32_t)(ph + 1) % kPhases == P_ATTN))
@@ -1195,11 +1273,16 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
                 // a residual prologue's row factor (1 for an input given as a digit image)
                 const double rn = d.in_kind != S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
-                if (d.y) {
+                if (d.y || d.yt) {
                     if (tid < 16 * mu) {
                         const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
                         const float y = (float)(rn * (double)part_sum(part, k, 0, rr));
-                        if (row < d.rows) stc(d.y, row * 4, __float_as_uint(y));
+                        if (row < d.rows) {
+                            if (d.yt)
+                                stc8(d.yt, row * 8, v2u{__float_as_uint(y), d.ytag});
+                            else
+                                stc(d.y, row * 4, __float_as_uint(y));
+                        }
                     }
                 } else {
                     if (tid < 32 * mu) {
