@@ -199,7 +199,7 @@ struct StepArgs {
     const uint32_t* ids;
     uint32_t* state;
     float *X, *H, *QKV, *PROJ, *D;  // activations exchanged inside the launch
-    uint32_t *PROJT, *DT;           // o-proj and down outputs as (value, tag) word pairs, [hidden][2]
+    uint32_t *QKVT, *PROJT, *DT;    // qkv, o-proj and down outputs as (value, tag) word pairs
     int8_t *att_img, *act_img;      // digit images of the o-proj and down inputs
     float* part;                    // attention chunk partials
     uint32_t* counters;             // attention merge tickets, one per KV head

@@ -787,7 +787,7 @@ struct af_session {
     float final_eps = 0, emb_scale = 1, cap = 0;
     uint32_t hidden = 0, intermediate = 0, vocabulary = 0, capacity = 0;
     uint32_t max_qkv = 0, max_q = 0, cmax = 0, head_blocks = 0;
-    DevMem X, H, QKV, ATT, PROJ, ACT, D, PROJT, DT, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
+    DevMem X, H, QKV, ATT, PROJ, ACT, D, QKVT, PROJT, DT, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
     // persistent step kernel: layer table, digit images, barrier words
     DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
@@ -976,6 +976,7 @@ struct af_session {
         a.QKV = QKV.as<float>();
         a.PROJ = PROJ.as<float>();
         a.D = D.as<float>();
+        a.QKVT = QKVT.as<uint32_t>();
         a.PROJT = PROJT.as<uint32_t>();
         a.DT = DT.as<uint32_t>();
         a.att_img = ATT_IMG.as<int8_t>();
@@ -1267,7 +1268,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         {&s->PROJ, (size_t)hidden * 4, true},
         {&s->ACT, (size_t)inter * 4, true},
         {&s->D, (size_t)hidden * 4, true},
-        {&s->PROJT, (size_t)hidden * 8, true},  // (value, tag) pairs: tag 0 is never current
+        {&s->QKVT, (size_t)s->max_qkv * 8, true},  // (value, tag) pairs: tag 0 is never current
+        {&s->PROJT, (size_t)hidden * 8, true},
         {&s->DT, (size_t)hidden * 8, true},
         {&s->LOGITS, (size_t)hm.rows * 4, false},
         {&s->PART, (size_t)max_kv * s->cmax * max_group * (256 + 2) * 4, false},

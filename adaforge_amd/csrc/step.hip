@@ -707,7 +707,7 @@ __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t 
 template <int GQ>
 __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uint32_t pos, uint32_t h, uint32_t c,
                                                uint32_t chunks, uint32_t cmax, uint32_t clen, uint32_t start,
-                                               uint8_t* lds, int* flag, const Grid& g) {
+                                               uint32_t tag, uint8_t* lds, int* flag, int* bad, const Grid& g) {
     constexpr int D = 256, NH = GQ + 2;
     AttnLds<GQ> sh(lds);
     float* nrm = sh.nrm;
@@ -724,25 +724,62 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     const bool staged = clen <= stage_clen<GQ>();
     const int nh = append ? NH : GQ;  // heads normalised here: the queries, and k, v of the new token
 
-    // this token's query heads (and k, v when the chunk ends at it), computed by the qkv phase
+    // This token's query heads (and k, v when the chunk ends at it), computed by the qkv phase and
+    // handed over as (value, tag) pairs (poll_tagged): 16-byte piece p (two values) of the item
+    // is copied to vred + 16 p, and re-copied until both its tags are current; nrm[2 p, 2 p + 2)
+    // then takes its values.  Piece j 64 + lane of copy instruction j.
     if (wave == 0) {
-        dma(a.QKV + (size_t)h * GQ * D, 4 * GQ * D, reinterpret_cast<uint8_t*>(nrm), lane);
-        if (append) {
-            dma(a.QKV + L.qn + h * D, 4 * D, reinterpret_cast<uint8_t*>(nrm + GQ * D), lane);
-            dma(a.QKV + L.v_off + h * D, 4 * D, reinterpret_cast<uint8_t*>(nrm + (GQ + 1) * D), lane);
-        }
-        // the RoPE angles of this position, while the copies are in flight
+        constexpr int J = 2 * NH;  // copy instructions for every head (D / 2 pieces = 2 x 64 each)
+        const uint32_t P = (uint32_t)nh * (D / 2);
+        uint8_t* stg = reinterpret_cast<uint8_t*>(vred);
+        auto src = [&](int j) -> const uint32_t* {  // element of piece j 64 + lane
+            const uint32_t p = (uint32_t)j * 64 + lane, q = p / (D / 2), e = 2 * (p % (D / 2));
+            const uint32_t base = q < GQ ? (h * GQ + q) * D : (q == GQ ? L.qn : L.v_off) + h * D;
+            return a.QKVT + 2 * (size_t)(base + e);
+        };
+        uint32_t need = 0;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const uint32_t f = lane + 64 * i;
-            double sn, cs;
-            sincos((double)pos * sh.ifreq[f], &sn, &cs);
-            sh.rope[f] = cs;
-            sh.rope[128 + f] = sn;
+        for (int j = 0; j < J; ++j)
+            if ((uint32_t)j * 64 + lane < P) need |= 1u << j;
+        bool ok = true;
+        for (uint32_t spins = 0;; ++spins) {
+#pragma unroll
+            for (int j = 0; j < J; ++j)
+                if (need >> j & 1)
+                    __builtin_amdgcn_global_load_lds(src(j), (lds_ptr)(stg + j * 1024), 16, 0, kSC1);
+            if (spins == 0) {
+                // the RoPE angles of this position, while the first copies are in flight
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const uint32_t f = lane + 64 * i;
+                    double sn, cs;
+                    sincos((double)pos * sh.ifreq[f], &sn, &cs);
+                    sh.rope[f] = cs;
+                    sh.rope[128 + f] = sn;
+                }
+            }
+            wait_vm();
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                if (need >> j & 1) {
+                    const v4u v = *reinterpret_cast<const v4u*>(stg + j * 1024 + lane * 16);
+                    if (v.y == tag && v.w == tag) {
+                        reinterpret_cast<v2u*>(nrm)[j * 64 + lane] = v2u{v.x, v.z};
+                        need &= ~(1u << j);
+                    }
+                }
+            }
+            if (__builtin_amdgcn_ballot_w64(need != 0) == 0) break;
+            if (spins >= kPollLimit) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
-        wait_vm();
+        if (!ok) *bad = 1;
     }
     __syncthreads();
+    if (__builtin_amdgcn_readfirstlane(*bad)) return;
     stamp(g, M_STAGED);
 
     // RMSNorm of each head over its 256 channels, then NeoX RoPE on the pairs (i, i + 128): thread
@@ -1028,7 +1065,8 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
     if (kind == P_QKV) {
         d.sh = shape_of(L.qkv, false);
         d.K = a.hidden;
-        d.y = a.QKV;
+        d.yt = a.QKVT;
+        d.ytag = tag0 + l;
         d.rows = L.qkv.rows;
         if (l == 0) {
             d.in_kind = S_EMBED;
@@ -1208,10 +1246,10 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         const uint32_t tid = tix(), lane = tid & 63;
         const LaneK lk = lane_k(lane);
         const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
-        // The input of gate/up (o-proj's outputs) and of qkv after layer 0 (down's outputs) is
-        // handed over by tags; every other phase opens with a grid barrier.  After a GEMV phase
-        // wave 0 has waited for the streaming waves (done_cnt) and for its stores.
-        const bool tagged = kind == P_GATEUP || (kind == P_QKV && l > 0);
+        // The inputs of attention (qkv's outputs), gate/up (o-proj's outputs) and qkv after layer 0
+        // (down's outputs) are handed over by tags; o-proj and down open with a grid barrier.
+        // After a GEMV phase wave 0 has waited for the streaming waves (done_cnt) and its stores.
+        const bool tagged = kind != P_OPROJ && kind != P_DOWN;
         if (ph > 0) {
             if (tagged) {
                 tagged_boundary(g);
@@ -1226,8 +1264,12 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             const uint32_t item = gridDim.x - 1 - blockIdx.x;
             if (item < ag.items)
                 attention_item<GQ>(L, a, pos, item / ag.chunks, item % ag.chunks, ag.chunks, ag.cmax, ag.clen, ag.start,
-                                   lds, &att_flag, g);
+                                   tag0 + l, lds, &att_flag, &poll_bad, g);
             __syncthreads();
+            if (__builtin_amdgcn_readfirstlane(poll_bad)) {
+                failed = true;
+                break;
+            }
             stamp(g, M_STORED);
         } else {
             const Gemv d = describe(a, l, kind, tag0);
