@@ -200,7 +200,7 @@ struct StepArgs {
     uint32_t* state;
     float *X, *H, *QKV, *PROJ, *D;  // activations exchanged inside the launch
     uint32_t *QKVT, *PROJT, *DT;    // qkv, o-proj and down outputs as (value, tag) word pairs
-    int8_t *att_img, *act_img;      // digit images of the o-proj and down inputs
+    int8_t *att_img, *act_img;      // digit images of the o-proj (as tagged pieces) and down inputs
     float* part;                    // attention chunk partials
     uint32_t* counters;             // attention merge tickets, one per KV head
     uint32_t* bar;                  // grid barrier words (kStepBarBytes, zero between launches)

@@ -1123,7 +1123,8 @@ int setup_step(af_session& s) {
     }
     int rc;
     if ((rc = dev_upload(s.STEP_LAYERS, table.data(), table.size() * sizeof(StepLayer), "layer table"))) return rc;
-    const size_t att_img = (size_t)((s.max_q / 32 + 3) / 4) * kStepImg,
+    // the o-proj input image is handed over as tagged pieces: 16 bytes per 8-byte image word
+    const size_t att_img = (size_t)((s.max_q / 32 + 3) / 4) * kStepImg * 2,
                  act_img = (size_t)((s.intermediate / 32 + 3) / 4) * kStepImg;
     if ((rc = dev_alloc(s.ATT_IMG, att_img, "digit image"))) return rc;
     if ((rc = dev_alloc(s.ACT_IMG, act_img, "digit image"))) return rc;

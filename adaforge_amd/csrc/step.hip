@@ -437,11 +437,12 @@ __device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T,
 // (above the largest image of any phase, so the next phase's norm weights can be copied in while
 // this phase's image is in use), [x K][res K][w_a K][w_n K] (floats).  Every wave stages, every
 // thread then builds the digit image.
-enum StageKind { S_EMBED = 0, S_RESID = 1, S_DIGITS = 2 };
+enum StageKind { S_EMBED = 0, S_RESID = 1, S_DIGITS = 2, S_TDIGITS = 3 };  // S_TDIGITS: tagged (poll_image)
 
 struct Stage {
     const float *res, *w_a, *w_n;
-    const uint32_t* xt;   // S_RESID: the input as (value, tag) word pairs (poll_tagged)
+    const uint32_t* xt;   // S_RESID: the input as (value, tag) word pairs (poll_tagged); S_TDIGITS: the
+                          // tagged digit image (poll_image)
     uint32_t tag;         // the tag of the input's current values
     float eps_a, eps_n, scale;
     const int8_t* dig;    // S_DIGITS
@@ -485,6 +486,37 @@ __device__ __forceinline__ bool poll_tagged(const uint32_t* src, uint32_t K, uin
     }
 }
 
+// A digit image handed over without a grid barrier: its 8-byte word i (bytes lo, hi) is the
+// 16-byte piece (lo, tag, hi, tag) at 16 i of the tagged image.  Wave w copies the pieces of copy
+// chunks j = w, w + 8, .. (64 pieces each) into LDS staging stg + 1024 j, re-copies the chunks'
+// pieces whose tags are not yet current, and writes a current piece's word to the image in LDS.
+// Returns false (in the whole wave) if its pieces did not become current within the spin limit.
+__device__ __forceinline__ bool poll_image(const uint32_t* src, uint32_t bytes, uint32_t tag, uint8_t* img, uint8_t* stg,
+                                           uint32_t wave, uint32_t lane) {
+    const uint32_t n = bytes / 8, nj = (n + 63) / 64;
+    uint32_t need = 0;
+    for (uint32_t i = 0, j = wave; j < nj; ++i, j += 8)
+        if (j * 64 + lane < n) need |= 1u << i;
+    for (uint32_t spins = 0;; ++spins) {
+        for (uint32_t i = 0, j = wave; j < nj; ++i, j += 8)
+            if (need >> i & 1)
+                __builtin_amdgcn_global_load_lds(src + 4 * (j * 64 + lane), (lds_ptr)(stg + j * 1024), 16, 0, kSC1);
+        wait_vm();
+        for (uint32_t i = 0, j = wave; j < nj; ++i, j += 8) {
+            if (need >> i & 1) {
+                const v4u v = *reinterpret_cast<const v4u*>(stg + j * 1024 + lane * 16);
+                if (v.y == tag && v.w == tag) {
+                    *reinterpret_cast<v2u*>(img + (j * 64 + lane) * 8) = v2u{v.x, v.z};
+                    need &= ~(1u << i);
+                }
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(need != 0) == 0) return true;
+        if (spins >= kPollLimit) return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
 // Every wave, after the phase boundary: the activation inputs (the norm weights are already in
 // LDS), or the embedding row of the step's token.  A streaming wave's weight loads in flight were
 // issued before the boundary, so its wait here costs nothing the next phase would not wait for
@@ -496,6 +528,8 @@ __device__ __forceinline__ bool stage_inputs(int kind, const Stage& in, const In
     bool ok = true;
     if (kind == S_DIGITS) {
         dma_all(in.dig, nst * kStepImg, img, wave, lane);
+    } else if (kind == S_TDIGITS) {
+        ok = poll_image(in.xt, nst * kStepImg, in.tag, img, img + nst * kStepImg, wave, lane);  // step_xs_offset
     } else if (kind == S_RESID) {
         ok = poll_tagged(in.xt, K, in.tag, xs, wave * 64 + lane);  // the residual is in xs + K
     } else {
@@ -616,6 +650,22 @@ __device__ __forceinline__ void quad_digits_store(const float (&v)[8], int8_t* i
         const BlockTab e = block_tab(m, sum);
         stc16(img, nst * 512 + b * 16,
               v4u{__float_as_uint(e.s14), __float_as_uint(e.s21), __float_as_uint(e.nbias), 0u});
+    }
+}
+
+// The same words as tagged pieces (poll_image) of a tagged image.
+__device__ __forceinline__ void quad_digits_store_tagged(const float (&v)[8], uint32_t* img, uint32_t nst, uint32_t b,
+                                                         uint32_t p, uint32_t tag) {
+    float m, sum;
+    quad_stats(v, m, sum);
+    uint32_t w[4][2];
+    digit_words(v, m, w);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) stc16(img, 2 * ((b * 4 + t) * 32 + 8 * p), v4u{w[t][0], tag, w[t][1], tag});
+    if (p == 0) {
+        const BlockTab e = block_tab(m, sum);
+        stc16(img, 2 * (nst * 512 + b * 16), v4u{__float_as_uint(e.s14), tag, __float_as_uint(e.s21), tag});
+        stc16(img, 2 * (nst * 512 + b * 16) + 16, v4u{__float_as_uint(e.nbias), tag, 0u, tag});
     }
 }
 
@@ -1023,7 +1073,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
                 float v[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) v[k] = outv[blk * 32 + 8 * p + k];
-                quad_digits_store(v, a.att_img, nst_att, h * GQ * 8 + blk, p);
+                quad_digits_store_tagged(v, reinterpret_cast<uint32_t*>(a.att_img), nst_att, h * GQ * 8 + blk, p, tag);
             }
         }
         if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1039,7 +1089,7 @@ enum PhaseKind { P_QKV = 0, P_ATTN, P_OPROJ, P_GATEUP, P_DOWN, kPhases };
 // One GEMV phase of a layer, read from the layer table.
 struct Gemv {
     Shape sh;
-    int in_kind;     // S_EMBED, S_RESID or S_DIGITS
+    int in_kind;     // StageKind
     Stage in;
     InputStage emb;  // S_EMBED
     uint32_t K;      // input width
@@ -1090,8 +1140,9 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         d.in.x_out = a.X;
     } else if (kind == P_OPROJ) {
         d.sh = shape_of(L.o, false);
-        d.in_kind = S_DIGITS;
-        d.in.dig = a.att_img;
+        d.in_kind = S_TDIGITS;
+        d.in.xt = reinterpret_cast<const uint32_t*>(a.att_img);
+        d.in.tag = tag0 + l;
         d.K = L.o.blocks * 32;
         d.yt = a.PROJT;
         d.ytag = tag0 + l;
@@ -1246,10 +1297,11 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         const uint32_t tid = tix(), lane = tid & 63;
         const LaneK lk = lane_k(lane);
         const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
-        // The inputs of attention (qkv's outputs), gate/up (o-proj's outputs) and qkv after layer 0
-        // (down's outputs) are handed over by tags; o-proj and down open with a grid barrier.
-        // After a GEMV phase wave 0 has waited for the streaming waves (done_cnt) and its stores.
-        const bool tagged = kind != P_OPROJ && kind != P_DOWN;
+        // The inputs of attention (qkv's outputs), o-proj (the attention image), gate/up (o-proj's
+        // outputs) and qkv after layer 0 (down's outputs) are handed over by tags; down opens with a
+        // grid barrier.  After a GEMV phase wave 0 has waited for the streaming waves (done_cnt)
+        // and for its stores.
+        const bool tagged = kind != P_DOWN;
         if (ph > 0) {
             if (tagged) {
                 tagged_boundary(g);
@@ -1282,7 +1334,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             }
             stamp(g, M_STAGED);
             zero_part_lds(part, tid);
-            if (d.in_kind != S_DIGITS) stage_digits(d.in_kind, d.in, d.K, nst, a.xs_off, lds, red);
+            if (d.in_kind < S_DIGITS) stage_digits(d.in_kind, d.in, d.K, nst, a.xs_off, lds, red);
             __syncthreads();
             stamp(g, M_DIGITS);
             // the next phase's LDS writes may start now if they stay above this phase's image
@@ -1300,7 +1352,12 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 wait_vm();
                 if (wave == 1) stamp_at(g, g.p, M_CONSUMED);
             } else {
-                if (blockIdx.x == 0 && d.in_kind != S_DIGITS) store_residual(d.in, lds, d.K, a.xs_off, lane);
+                // waited for before the outputs are stored: a phase that reads the residual may be
+                // ordered after this one only through the outputs' tags
+                if (blockIdx.x == 0 && d.in_kind < S_DIGITS) {
+                    store_residual(d.in, lds, d.K, a.xs_off, lane);
+                    wait_vm();
+                }
                 if (pre_now && (ph + 1 >= n_phases || (uint32_t)(ph + 1) % kPhases == P_ATTN))
                     phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 stamp(g, M_PRE);
@@ -1314,7 +1371,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
                 // a residual prologue's row factor (1 for an input given as a digit image)
-                const double rn = d.in_kind != S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
+                const double rn = d.in_kind < S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
                 if (d.y || d.yt) {
                     if (tid < 16 * mu) {
                         const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
@@ -1401,7 +1458,9 @@ uint32_t step_merge_chunks(uint32_t group, size_t lds) {
 
 uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim) {
     const uint32_t nst = std::max({(hidden + 127) / 128, (inter + 127) / 128, (q_dim + 127) / 128});
-    return (nst * kStepImg + 15) / 16 * 16;  // the largest digit image of any GEMV phase
+    // the o-proj image and, above it, the staging of its tagged pieces (poll_image: 1 KB per 64)
+    const uint32_t o_img = (q_dim + 127) / 128 * kStepImg, o_stage = (o_img / 8 + 63) / 64 * 1024;
+    return (std::max(nst * kStepImg, o_img + o_stage) + 15) / 16 * 16;  // the largest digit image of any GEMV phase
 }
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group) {
