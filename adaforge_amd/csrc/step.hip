@@ -1363,6 +1363,9 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 stamp(g, M_PRE);
                 // the streaming waves with records (wave - 1 < fe) have left their partials in part
                 const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
+                // a residual prologue's row factor (1 for an input given as a digit image), while the
+                // streaming waves consume: the wave sums it adds are in red since the digits barrier
+                const double rn = d.in_kind < S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
                 const uint32_t want = 64u * min(kStreamWaves, fe);
                 while (__hip_atomic_load(&done_cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < want)
                     __builtin_amdgcn_s_sleep(1);
@@ -1370,8 +1373,6 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
-                // a residual prologue's row factor (1 for an input given as a digit image)
-                const double rn = d.in_kind < S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
                 if (d.y || d.yt) {
                     if (tid < 16 * mu) {
                         const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
