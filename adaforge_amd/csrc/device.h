@@ -356,9 +356,12 @@ __device__ __forceinline__ uint2 ld_stream(const uint2* p) {
 // Digit words of 8 consecutive elements v of a block whose max |x| is m: w[t] holds the 8
 // int8 digits of plane t.  With s = 2^(ilogb(m) - 5), U = rint(v 2^21 / s) is an integer with
 // |U| <= 2^27 (|v| < 2^(ilogb(m) + 1), and scaling by a power of two is exact), and its signed
-// radix-2^7 digits q0..q3 (q_t = round(r_t / 2^(21 - 7t)) on the remainders, |q_t| <= 64) satisfy
-// U = 2^21 q0 + 2^14 q1 + 2^7 q2 + q3, so v = s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) to within
-// half of s 2^-21.  Integer adds and shifts only, then v_perm packs the low bytes.
+// radix-2^7 digits satisfy U = 2^21 q0 + 2^14 q1 + 2^7 q2 + q3, so v = s (q0 + q1 2^-7 + q2 2^-14
+// + q3 2^-21) to within half of s 2^-21.  The digits are signed 7-bit fields: q3 = sext(U[0, 7)),
+// so U - q3 = 2^7 floor((U + 64) / 2^7); q2 = sext((U + 64)[7, 14)); q1 = sext((U + 8256)[14, 21));
+// q0 = floor((U + 1056832) / 2^21), with 8256 = 64 (1 + 2^7) and 1056832 = 64 (1 + 2^7 + 2^14).
+// q1..q3 lie in [-64, 63] and q0 in [-64, 64].  One bitfield extract (and one add) per digit,
+// then v_perm packs the low bytes.
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
     // byte i of the result = low byte of the i-th argument
     const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b, (uint32_t)a, 0x0C0C0400u);  // [a0, b0, 0, 0]
@@ -372,15 +375,10 @@ __device__ __forceinline__ void digit_words(const float (&v)[8], float m, uint32
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int U = m > 0.0f ? (int)rintf(ldexpf(v[k], 26 - e)) : 0;
-        const int q0 = (U + (1 << 20)) >> 21;
-        const int r0 = U - q0 * (1 << 21);
-        const int q1 = (r0 + (1 << 13)) >> 14;
-        const int r1 = r0 - q1 * (1 << 14);
-        const int q2 = (r1 + (1 << 6)) >> 7;
-        q[0][k] = q0;
-        q[1][k] = q1;
-        q[2][k] = q2;
-        q[3][k] = r1 - q2 * (1 << 7);
+        q[0][k] = (U + 1056832) >> 21;
+        q[1][k] = __builtin_amdgcn_sbfe(U + 8256, 14, 7);
+        q[2][k] = __builtin_amdgcn_sbfe(U + 64, 7, 7);
+        q[3][k] = __builtin_amdgcn_sbfe(U, 0, 7);
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
