@@ -692,7 +692,7 @@ struct AttnLds {
     float* qs;        // [GQ][D] rotated queries
     float* scores;    // [GQ][kStepMaxClen]
     float* vred;      // [16][GQ][D]
-    double* dred;     // [8][NH]
+    double* dred;     // [8][NH] (the q/k/v norms use [NH][2])
     float* fred;      // [8]
     uint16_t* knew;   // [D] new K row (fp16)
     uint16_t* vnew;   // [D] new V row (fp16)
@@ -832,65 +832,57 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     if (__builtin_amdgcn_readfirstlane(*bad)) return;
     stamp(g, M_STAGED);
 
-    // RMSNorm of each head over its 256 channels, then NeoX RoPE on the pairs (i, i + 128): thread
-    // i < 128 (waves 0, 1) holds both channels of pair i of every head, so the rotation needs no
-    // exchange once the two waves' sums of squares are added.
-    const bool pr = tid < D / 2;
-    float x0[NH], x1[NH];
-#pragma unroll
-    for (int q = 0; q < NH; ++q) {
-        x0[q] = pr && q < nh ? nrm[q * D + tid] : 0.0f;
-        x1[q] = pr && q < nh ? nrm[q * D + tid + D / 2] : 0.0f;
-    }
-    if (wave < 2) {
-#pragma unroll
-        for (int q = 0; q < NH; ++q) {
-            const double v = wave_sum((double)x0[q] * (double)x0[q] + (double)x1[q] * (double)x1[q]);
-            if (lane == 0) dred[wave * NH + q] = v;
-        }
+    // RMSNorm of each head over its 256 channels, then NeoX RoPE on the pairs (i, i + 128): head q
+    // runs on waves 2 (q % 4) and 2 (q % 4) + 1, whose lane l holds both channels of pair l (even
+    // wave) or 64 + l (odd wave), so a head's sum of squares is its two waves' sums, added in pair
+    // order, and the rotation needs no exchange.  Heads q and q + 4 share waves (GQ = 4).
+    const uint32_t pi = tid & (D / 2 - 1);
+    for (uint32_t q = tid >> 7; q < (uint32_t)nh; q += 4) {  // wave-uniform
+        const float x0 = nrm[q * D + pi], x1 = nrm[q * D + pi + D / 2];
+        const double v = wave_sum((double)x0 * (double)x0 + (double)x1 * (double)x1);
+        if (lane == 0) dred[2 * q + (wave & 1)] = v;
     }
     __syncthreads();
-    if (pr) {
-        const double cs = sh.rope[tid], sn = sh.rope[128 + tid];
-#pragma unroll
-        for (int q = 0; q < NH; ++q) {
-            if (q >= nh) break;
-            const double ss = dred[q] + dred[NH + q];
+    {
+        const double cs = sh.rope[pi], sn = sh.rope[128 + pi];
+        for (uint32_t q = tid >> 7; q < (uint32_t)nh; q += 4) {
+            const float x0 = nrm[q * D + pi], x1 = nrm[q * D + pi + D / 2];
+            const double ss = dred[2 * q] + dred[2 * q + 1];
             float y0, y1;
             if (q < GQ) {
                 const double r = inv_rms_fast(ss, D, L.q_eps);
-                y0 = norm_apply(x0[q], r, sh.qnw[tid]);
-                y1 = norm_apply(x1[q], r, sh.qnw[tid + D / 2]);
+                y0 = norm_apply(x0, r, sh.qnw[pi]);
+                y1 = norm_apply(x1, r, sh.qnw[pi + D / 2]);
             } else if (q == GQ) {
                 const double r = inv_rms_fast(ss, D, L.k_eps);
-                y0 = norm_apply(x0[q], r, sh.knw[tid]);
-                y1 = norm_apply(x1[q], r, sh.knw[tid + D / 2]);
+                y0 = norm_apply(x0, r, sh.knw[pi]);
+                y1 = norm_apply(x1, r, sh.knw[pi + D / 2]);
             } else {
                 const double r = L.v_norm ? inv_rms_fast(ss, D, L.v_eps) : 1.0;
-                y0 = L.v_norm ? (float)__dmul_rn((double)x0[q], r) : x0[q];
-                y1 = L.v_norm ? (float)__dmul_rn((double)x1[q], r) : x1[q];
+                y0 = L.v_norm ? (float)__dmul_rn((double)x0, r) : x0;
+                y1 = L.v_norm ? (float)__dmul_rn((double)x1, r) : x1;
                 const uint16_t v0 = f2h(y0), v1 = f2h(y1);
-                sh.vnew[tid] = v0;
-                sh.vnew[tid + D / 2] = v1;
+                sh.vnew[pi] = v0;
+                sh.vnew[pi + D / 2] = v1;
                 if (staged) {
-                    sh.vst[(pos - t0) * D + tid] = v0;
-                    sh.vst[(pos - t0) * D + tid + D / 2] = v1;
+                    sh.vst[(pos - t0) * D + pi] = v0;
+                    sh.vst[(pos - t0) * D + pi + D / 2] = v1;
                 }
-                break;
+                continue;
             }
             const double u = (double)y0, w = (double)y1;
             const float r0 = (float)__dsub_rn(__dmul_rn(u, cs), __dmul_rn(w, sn));
             const float r1 = (float)__dadd_rn(__dmul_rn(u, sn), __dmul_rn(w, cs));
             if (q < GQ) {
-                qs[q * D + tid] = r0;
-                qs[q * D + tid + D / 2] = r1;
+                qs[q * D + pi] = r0;
+                qs[q * D + pi + D / 2] = r1;
             } else {
                 const uint16_t k0 = f2h(r0), k1 = f2h(r1);
-                sh.knew[tid] = k0;
-                sh.knew[tid + D / 2] = k1;
+                sh.knew[pi] = k0;
+                sh.knew[pi + D / 2] = k1;
                 if (staged) {
-                    sh.kst[(pos - t0) * D + tid] = k0;
-                    sh.kst[(pos - t0) * D + tid + D / 2] = k1;
+                    sh.kst[(pos - t0) * D + pi] = k0;
+                    sh.kst[(pos - t0) * D + pi + D / 2] = k1;
                 }
             }
         }
