@@ -791,7 +791,7 @@ struct af_session {
     // persistent step kernel: layer table, digit images, barrier words
     DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
-    bool use_step = true;     // all layers of a step in one cooperative launch
+    bool use_step = true;     // all layers of a step in one persistent launch
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
     size_t step_lds = 0;
     uint32_t max_kv_rows = 0;

@@ -1,13 +1,13 @@
-// Persistent decode step for gfx950 (MI355X): all layers of one decode step in one cooperative
-// launch of one 512-thread workgroup per CU.  Per layer it runs five phases separated by grid
-// barriers: qkv GEMV (residual + RMSNorm prologue), GQA attention over the fp16 KV cache
-// (split-K, merged by the last chunk of each KV head), o-proj GEMV, fused gate/up GEMV with
-// tanh-GELU, down GEMV.
+// Persistent decode step for gfx950 (MI355X): all layers of one decode step in one launch of one
+// 512-thread workgroup per CU.  Per layer it runs five phases: qkv GEMV (residual + RMSNorm
+// prologue), GQA attention over the fp16 KV cache (split-K, merged by the last chunk of each KV
+// head), o-proj GEMV, fused gate/up GEMV with tanh-GELU, down GEMV.  Down opens with a grid
+// barrier; the other phases poll their inputs, which their producers store with tags.
 //
 // Why one launch: a layer's five dependent kernels each pay a dispatch, a ramp and a drain,
 // and their weight streams cannot start before the previous kernel ends.  Here the weights of
-// the next phase, which do not depend on any activation, are requested before each grid
-// barrier, so HBM keeps streaming while the barrier and the next phase's input prologue
+// the next phase, which do not depend on any activation, are requested before each phase
+// boundary, so HBM keeps streaming while the boundary and the next phase's input prologue
 // resolve.
 //
 // Wave roles: wave 0 of every workgroup never streams weights: it runs the grid barrier, the
@@ -20,7 +20,7 @@
 // Coherence: the eight XCDs have private L2 caches.  Activations exchanged between workgroups
 // inside the launch are written and read with agent-scope coherent accesses (sc1), the grid
 // barrier uses agent-scope atomics, and a store is waited for (s_waitcnt vmcnt(0)) before the
-// barrier arrival that publishes it.  Weights, norm vectors and the KV cache rows read here
+// barrier arrival that publishes it; a tagged value carries its tag in the same store.  Weights, norm vectors and the KV cache rows read here
 // were written before the launch began.
 #include "device.h"
 
@@ -1463,14 +1463,18 @@ size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t 
     return std::max(g, att);
 }
 
+// A plain launch: the grid is the occupancy API's co-resident maximum (step_max_grid, one
+// workgroup per CU), so every workgroup of the grid barriers is resident; a grid that were not
+// would end in the barriers' spin limit, reported as a failed step, not in a hang.  The
+// cooperative launch API gives the same residency and costs about 12 us more per launch.
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s) {
-    void* args[] = {const_cast<StepArgs*>(&a)};
     switch (group) {
-        case 1: return hipLaunchCooperativeKernel((const void*)decode_step_kernel<1>, dim3(grid), dim3(kThreads), args, lds, s);
-        case 2: return hipLaunchCooperativeKernel((const void*)decode_step_kernel<2>, dim3(grid), dim3(kThreads), args, lds, s);
-        case 4: return hipLaunchCooperativeKernel((const void*)decode_step_kernel<4>, dim3(grid), dim3(kThreads), args, lds, s);
+        case 1: hipLaunchKernelGGL(decode_step_kernel<1>, dim3(grid), dim3(kThreads), lds, s, a); break;
+        case 2: hipLaunchKernelGGL(decode_step_kernel<2>, dim3(grid), dim3(kThreads), lds, s, a); break;
+        case 4: hipLaunchKernelGGL(decode_step_kernel<4>, dim3(grid), dim3(kThreads), lds, s, a); break;
         default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
 }
 
 hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid) {
