@@ -11,17 +11,17 @@
 // resolve.
 //
 // Wave roles: wave 0 of every workgroup never streams weights: it runs the grid barrier, the
-// next phase's pre-barrier copies and the output stores, while waves 1-7 stream the weights,
-// each from its own contiguous run of weight records.  After a barrier all eight waves copy the
-// phase's input vectors into LDS (global->LDS DMA; a streaming wave's weight loads still in
-// flight were issued before the barrier), and the input prologue (norms, exact int8 digit
-// planes) runs on all 512 threads from LDS.
+// next phase's early copies and the output stores, while waves 1-7 stream the weights, each
+// from its own contiguous run of weight records.  At a phase start all eight waves poll or copy
+// the phase's input into LDS (a streaming wave's weight loads still in flight were issued
+// before), and the input prologue (norms, exact int8 digit planes) runs on all 512 threads
+// from LDS.
 //
 // Coherence: the eight XCDs have private L2 caches.  Activations exchanged between workgroups
 // inside the launch are written and read with agent-scope coherent accesses (sc1), the grid
 // barrier uses agent-scope atomics, and a store is waited for (s_waitcnt vmcnt(0)) before the
-// barrier arrival that publishes it; a tagged value carries its tag in the same store.  Weights, norm vectors and the KV cache rows read here
-// were written before the launch began.
+// barrier arrival that publishes it; a tagged value carries its tag in the same store.
+// Weights, norm vectors and the KV cache rows read here were written before the launch began.
 #include "device.h"
 
 namespace af {
@@ -225,7 +225,7 @@ __device__ __forceinline__ BlockTab block_tab(float m, float sum) {
 
 // A streaming wave's weight records: a ring of kRing in registers, refilled from the wave's run
 // as each is consumed, across phase (and layer) boundaries: the next phase's first records are
-// in flight while this one finishes and during the barrier and prologue in between.  Slot
+// in flight while this one finishes and during the boundary and prologue in between.  Slot
 // `slot` holds the next record to consume.
 static_assert(kRing * kStepRecord <= kStepStreamPad, "stream padding below the ring's over-read");
 struct Ring {
@@ -400,7 +400,7 @@ __device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T,
                                               const v4i* zero, float* part, uint32_t wave, uint32_t lane,
                                               const LaneK& lk, uint32_t* done) {
     if (wave - 1 >= fe) return;
-    wait_vm();  // every record in flight was requested before this phase's barrier
+    wait_vm();  // every record in flight was requested before this phase began
     ring_rotate(r);
     const __amdgpu_buffer_rsrc_t rs = ring_rsrc(r);
     r.soff = __builtin_amdgcn_readfirstlane(r.soff);
@@ -674,7 +674,7 @@ __device__ __forceinline__ void quad_digits_store_tagged(const float (&v)[8], ui
 // Work item (KV head h, chunk c) of the visible range runs with all 512 threads; the last chunk
 // of a head to finish merges the head's partials and writes the digit image of its query heads'
 // outputs for the o-proj GEMV.  Chunks of at most stage_clen tokens have their cached K and V
-// rows staged in LDS before the barrier that opens the attention phase.
+// rows staged in LDS before the attention phase opens.
 template <int GQ>
 constexpr uint32_t stage_clen() {
     return GQ == 4 ? 32u : 64u;
@@ -682,7 +682,7 @@ constexpr uint32_t stage_clen() {
 
 // LDS of an attention item.  The "pre" part (RoPE angles, q/k norm weights, staged K/V rows) is
 // written by wave 0 while the qkv phase streams its weights, so it lies above that phase's
-// digit image; the "transient" part is written after the barrier.  The merge reuses the space
+// digit image; the "transient" part is written after the phase opens.  The merge reuses the space
 // from offset 0: the head's chunk partials, then the merged outputs.
 template <int GQ>
 struct AttnLds {
@@ -697,7 +697,7 @@ struct AttnLds {
     uint16_t* knew;   // [D] new K row (fp16)
     uint16_t* vnew;   // [D] new V row (fp16)
     // pre
-    double* rope;     // cos [128], sin [128] of pos * inv_freq (written after the barrier)
+    double* rope;     // cos [128], sin [128] of pos * inv_freq (written after the phase opens)
     double* ifreq;    // [128] the layer's RoPE inverse frequencies
     float* qnw;       // [D] q_norm weights
     float* knw;       // [D] k_norm weights
@@ -728,7 +728,7 @@ struct AttnLds {
 
 // Wave 0, while the qkv phase streams (nothing here depends on this step's q, k, v): the RoPE
 // inverse frequencies, the q/k norm weights and the chunk's cached K and V rows, copied into
-// the "pre" LDS part.  The copies are waited for with wave 0's next wait (before the barrier).
+// the "pre" LDS part.  The copies are waited for with wave 0's next wait (in its qkv epilogue).
 template <int GQ>
 __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t h, uint32_t c, uint32_t clen,
                                               uint32_t start, uint8_t* lds, uint32_t lane) {
@@ -1191,7 +1191,7 @@ __device__ __forceinline__ AttnGeo attn_geo(CLayer& L, uint32_t pos, uint32_t cm
 
 // Wave 0: copies for phase ph that do not depend on the phase before it (norm weights of a
 // residual prologue, or the attention item's RoPE frequencies, norm weights and cached K/V
-// rows).  Issued only: the caller waits (wave 0 waits for everything before its barrier arrival).
+// rows).  Issued only: the caller waits (wave 0 waits for everything at the end of its epilogue).
 template <int GQ>
 __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t pos, uint8_t* lds,
                                           uint32_t lane) {
@@ -1241,11 +1241,11 @@ __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, i
 // Wave roles.  Inside a phase, waves 1-7 issue no vector memory instruction but their weight
 // loads: the compiler then waits for exactly the ring slot being consumed.  Wave 0 does every
 // other global access of the phase (barrier, pre-copies, stores), and every wave-0 block that
-// issues one waits for it before the block ends.  A GEMV phase: barrier; all waves stage the
-// inputs; all build the digit image from LDS; waves 1-7 consume their weight stream (refilling
-// the ring with the next phase's records) while wave 0 stores the residual and prepares the next
-// phase when its LDS is free; wave 0 stores the outputs.  Every phase's code appears once in the
-// loop over (layer, phase).
+// issues one waits for it before the block ends.  A GEMV phase: its boundary (grid barrier or
+// tagged input); all waves stage the inputs; all build the digit image from LDS; waves 1-7
+// consume their weight stream (refilling the ring with the next phase's records) while wave 0
+// stores the residual and prepares the next phase when its LDS is free; wave 0 stores the
+// outputs.  Every phase's code appears once in the loop over (layer, phase).
 template <int GQ>
 __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
@@ -1361,7 +1361,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 const uint32_t want = 64u * min(kStreamWaves, fe);
                 while (__hip_atomic_load(&done_cnt, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < want)
                     __builtin_amdgcn_s_sleep(1);
-                done_cnt = 0;  // next incremented after the next grid barrier
+                done_cnt = 0;  // next incremented after the next phase's stage barrier
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
