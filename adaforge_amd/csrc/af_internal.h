@@ -213,6 +213,9 @@ struct StepArgs {
     float* snap;                    // optional: layer outputs [n_layers][hidden] (the last by the head)
     uint64_t* clock;                // optional: [phases][kStepMarks][grid] timestamps (100 MHz), one
                                     // phase per barrier interval (see StepMark)
+    uint32_t fail_phase;            // a phase whose opening grid barrier waits for one arrival too
+                                    // many, so that it ends in the barrier's own time-out (a host-set
+                                    // test of the fall-back path); ~0u: none
 };
 
 // Timeline marks of a phase (workgroup's thread 0): start (barrier departure or kernel start),
@@ -250,6 +253,12 @@ __host__ __device__ inline uint32_t step_wave_records(uint32_t units, uint32_t T
     const uint32_t fe = step_units(units, b, grid) * T * nst;
     return fe > w - 1 ? (fe - (w - 1) + kStepStreamWaves - 1) / kStepStreamWaves : 0u;
 }
+
+// Floats per attention chunk partial of the step kernel: GQ query heads of 256 unnormalised
+// outputs plus their softmax max and sum, padded to a multiple of 4 so that every chunk starts
+// on a 16-byte boundary and is stored and copied in whole 16-byte pieces (GQ * 258 alone is not a
+// multiple of 4 for odd GQ).
+__host__ __device__ constexpr uint32_t step_part_stride(uint32_t group) { return (group * (256u + 2u) + 3u) & ~3u; }
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group);
 uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim);

@@ -1,6 +1,7 @@
 // Host side of the C ABI (include/af.h): validation, weight repacking and
 // upload, standalone operators, and the generation session that captures the
-// whole decode step (48 layers + head + greedy) as one HIP graph.
+// whole decode step (the persistent launch of every layer, then the head with greedy
+// selection) as one HIP graph replayed per token.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -792,6 +793,7 @@ struct af_session {
     DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
     bool use_step = true;     // all layers of a step in one persistent launch
+    uint32_t fail_phase = ~0u;  // AF_STEP_FAIL_PHASE: a step-kernel barrier that times out (tests)
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
     size_t step_lds = 0;
     uint32_t max_kv_rows = 0;
@@ -990,6 +992,7 @@ struct af_session {
         a.xs_off = step_xs_offset(hidden, intermediate, max_q);
         a.advance = advance ? 1u : 0u;
         a.snap = snap;
+        a.fail_phase = fail_phase;
         return a;
     }
 
@@ -1037,8 +1040,11 @@ struct af_session {
         return AF_OK;
     }
 
+    // One decode (with_head) or prefill step: a replay of the graph captured at open, or direct
+    // launches (AF_DISABLE_GRAPHS).  Every argument of a step's launches is fixed for the session
+    // (the position, ids and stop state live in device memory), so one graph serves every token.
     hipError_t run_step(bool with_head) {
-        if (use_graphs && !use_step) return hipGraphLaunch(with_head ? decode_exec : prefill_exec, stream);
+        if (use_graphs) return hipGraphLaunch(with_head ? decode_exec : prefill_exec, stream);
         return enqueue_step(with_head);
     }
 
@@ -1050,6 +1056,42 @@ struct af_session {
         state_host[ST_STOP] = 0u;
         state_host[ST_NSTOP] = nstop;
         HIP_OK(hipMemcpyAsync(STATE.p, state_host, ST_HOST_WORDS * 4, hipMemcpyHostToDevice, stream), "state upload");
+        return AF_OK;
+    }
+
+    // After the stream has drained: true if a step-kernel launch timed out in a grid barrier or a
+    // tagged poll (state word ST_BAD = 2; the failed step's position is left in ST_POS).
+    int step_timed_out(bool& out, uint32_t* pos) {
+        out = false;
+        if (!use_step) return AF_OK;
+        uint32_t words[ST_WORDS] = {};
+        HIP_OK(hipMemcpy(words, STATE.p, sizeof(words), hipMemcpyDeviceToHost), "state download");
+        out = words[ST_BAD] == 2u;
+        if (pos) *pos = words[ST_POS];
+        return AF_OK;
+    }
+
+    // The persistent step kernel needs every workgroup of its grid resident at once; when they
+    // were not (its barrier or a tagged poll timed out), the session continues on the
+    // per-operation kernels, which make no such assumption.  The failed step is run again there by
+    // the caller: a step recomputes its activations from the embedding, and the K/V slots a failed
+    // step wrote are its own position's, which the rerun overwrites.  The attention merge tickets
+    // an interrupted merge left are cleared; the graphs are recaptured for the new path.
+    int fall_back() {
+        use_step = false;
+        HIP_OK(hipMemsetAsync(COUNTERS.p, 0, COUNTERS.bytes, stream), "attention counters clear");
+        HIP_OK(hipStreamSynchronize(stream), "fall-back");
+        if (use_graphs) {
+            if (decode_exec) (void)hipGraphExecDestroy(decode_exec);
+            if (prefill_exec) (void)hipGraphExecDestroy(prefill_exec);
+            if (decode_graph) (void)hipGraphDestroy(decode_graph);
+            if (prefill_graph) (void)hipGraphDestroy(prefill_graph);
+            decode_exec = prefill_exec = nullptr;
+            decode_graph = prefill_graph = nullptr;
+            int rc = capture(true, decode_graph, decode_exec);
+            if (rc) return rc;
+            if ((rc = capture(false, prefill_graph, prefill_exec))) return rc;
+        }
         return AF_OK;
     }
 };
@@ -1132,7 +1174,7 @@ int setup_step(af_session& s) {
     HIP_OK(hipMemset(s.ATT_IMG.p, 0, att_img), "digit image clear");
     HIP_OK(hipMemset(s.ACT_IMG.p, 0, act_img), "digit image clear");
     HIP_OK(hipMemset(s.BAR.p, 0, kStepBarBytes), "barrier clear");
-    const size_t part = (size_t)grid * group * (256 + 2) * 4;
+    const size_t part = (size_t)grid * step_part_stride(group) * 4;
     if (s.PART.bytes < part) {
         if ((rc = dev_alloc(s.PART, part, "attention partials"))) return rc;
     }
@@ -1158,11 +1200,8 @@ int setup_step(af_session& s) {
                                 s.STREAM_OFF.as<uint64_t>(), nullptr),
            "weight stream build");
     HIP_OK(hipDeviceSynchronize(), "weight stream build");
-    for (LayerDev& L : s.layers) {
-        L.qkv.codes.reset(), L.qkv.scales.reset(), L.o.codes.reset(), L.o.scales.reset();
-        L.gate.codes.reset(), L.gate.scales.reset(), L.up.codes.reset(), L.up.scales.reset();
-        L.down.codes.reset(), L.down.scales.reset();
-    }
+    // The tiled matrices stay resident: a step kernel that times out (its workgroups were not all
+    // resident at once) makes the session fall back to the per-operation kernels, which read them.
     return AF_OK;
 }
 
@@ -1199,6 +1238,9 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     s->use_graphs = !(env && *env && std::strcmp(env, "0") != 0);
     const char* step_env = std::getenv("AF_STEP_KERNEL");
     s->use_step = !(step_env && std::strcmp(step_env, "0") == 0);
+    // A test of the fall-back path: the step kernel's barrier opening this phase (5 l + 4 opens
+    // layer l's down projection) waits for one arrival more than the grid makes, and times out.
+    if (const char* fp = std::getenv("AF_STEP_FAIL_PHASE")) s->fail_phase = (uint32_t)std::strtoul(fp, nullptr, 10);
     HIP_OK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "session stream");
 
     uint32_t max_kv = 0, max_q = 0, max_group = 1;
@@ -1273,7 +1315,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         {&s->PROJT, (size_t)hidden * 8, true},
         {&s->DT, (size_t)hidden * 8, true},
         {&s->LOGITS, (size_t)hm.rows * 4, false},
-        {&s->PART, (size_t)max_kv * s->cmax * max_group * (256 + 2) * 4, false},
+        {&s->PART, (size_t)max_kv * s->cmax * std::max<uint32_t>(max_group * (256 + 2), step_part_stride(max_group)) * 4,
+         false},
         {&s->COUNTERS, (size_t)std::max<uint32_t>(max_kv, 64) * 4, true},
         {&s->HPART, (size_t)s->head_blocks * 16, false},
         {&s->HCOUNT, 256, true},
@@ -1296,7 +1339,10 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     HIP_OK(hipEventCreate(&s->ev_start), "event");
     if ((rc = setup_step(*s))) return rc;
     HIP_OK(hipDeviceSynchronize(), "session upload");
-    if (s->use_graphs && !s->use_step) {
+    if (s->use_graphs) {
+        // the step kernel and the head (decode), or the step kernel alone (prefill); on the
+        // per-operation path every layer's kernels.  No timeline memset is recorded: the timer
+        // that adds it is only set around direct launches (af_session_profile).
         if ((rc = s->capture(true, s->decode_graph, s->decode_exec))) return rc;
         if ((rc = s->capture(false, s->prefill_graph, s->prefill_exec))) return rc;
     }
@@ -1360,28 +1406,42 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
     if (rc) return rc;
     for (uint32_t i = 0; i + 1 < pend; ++i) HIP_OK(s->run_step(false), "prefill step");
     HIP_OK(hipStreamSynchronize(st), "prefill");
+    if (pend > 1) {  // a timed-out step kernel: rerun from its position on the per-operation kernels
+        bool timed_out = false;
+        uint32_t at = 0;
+        if ((rc = s->step_timed_out(timed_out, &at))) return rc;
+        if (timed_out) {
+            if ((rc = s->fall_back()) || (rc = s->set_state(at, (uint32_t)n_stop))) return rc;
+            for (uint32_t q = at; q + 1 < P; ++q) HIP_OK(s->run_step(false), "prefill step");
+            HIP_OK(hipStreamSynchronize(st), "prefill");
+        }
+    }
     const double prefill_ms = ms_since(started);
     const double start_offset = ms_since(started);
     HIP_OK(hipEventRecord(s->ev_start, st), "event");
-    // Enqueue all decode steps; each step's head writes its id and flags to mapped host
+    // Enqueue the decode steps from k0 on; each step's head writes its id and flags to mapped host
     // memory, and a stop id makes the remaining steps return at once.
-    s->timer = timer;
-    for (uint32_t k = 0; k < max_new; ++k) {
-        s->host_pos = P - 1 + k;
-        hipError_t e;
-        if (k == 0 && pend == 0)
-            e = s->timed(K_HEAD, (double)s->head.rows * (s->head.columns / 256) * 210.0 + 12.0 * s->hidden, [&] {
-                return launch_head(s->head_args(true, false), IN_RESID, s->head_blocks, st);
-            });
-        else
-            e = timer ? s->enqueue_step(true) : s->run_step(true);
-        if (e == hipSuccess) e = hipEventRecord(s->events[k], st);
-        if (e != hipSuccess) {
-            s->timer = nullptr;
-            return fail(AF_ERR_DEVICE, std::string("decode step: ") + hipGetErrorString(e));
+    auto enqueue_from = [&](uint32_t k0) -> int {
+        s->timer = timer;
+        for (uint32_t k = k0; k < max_new; ++k) {
+            s->host_pos = P - 1 + k;
+            hipError_t e;
+            if (k == 0 && pend == 0)
+                e = s->timed(K_HEAD, (double)s->head.rows * (s->head.columns / 256) * 210.0 + 12.0 * s->hidden, [&] {
+                    return launch_head(s->head_args(true, false), IN_RESID, s->head_blocks, st);
+                });
+            else
+                e = timer ? s->enqueue_step(true) : s->run_step(true);
+            if (e == hipSuccess) e = hipEventRecord(s->events[k], st);
+            if (e != hipSuccess) {
+                s->timer = nullptr;
+                return fail(AF_ERR_DEVICE, std::string("decode step: ") + hipGetErrorString(e));
+            }
         }
-    }
-    s->timer = nullptr;
+        s->timer = nullptr;
+        return AF_OK;
+    };
+    if ((rc = enqueue_from(0))) return rc;
     std::vector<uint32_t> ids;
     bool stopped = false, bad = false;
     double first_ms = 0, last_ms = 0;
@@ -1393,6 +1453,19 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
         r.bad = vr->bad;
         r.stop = vr->stop;
         r.done = vr->done;
+        if (!r.done && s->use_step) {
+            // step k's kernel may have timed out (its head then returned at once): rerun steps k..
+            // on the per-operation kernels from the step's position
+            HIP_OK(hipStreamSynchronize(st), "decode step");
+            bool timed_out = false;
+            if ((rc = s->step_timed_out(timed_out, nullptr))) return rc;
+            if (timed_out) {
+                if ((rc = s->fall_back()) || (rc = s->set_state(P - 1 + k, (uint32_t)n_stop)) || (rc = enqueue_from(k)))
+                    return rc;
+                --k;
+                continue;
+            }
+        }
         float t = 0;
         (void)hipEventElapsedTime(&t, s->ev_start, s->events[k]);
         if (!r.done || r.bad) {
@@ -1624,6 +1697,9 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     run.insert(run.end(), ids, ids + n);
     HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, run.data(), run.size() * 4, hipMemcpyHostToDevice, st),
            "ids upload");
+    // A step kernel that times out makes the session fall back to the per-operation kernels, and
+    // the whole trace runs again there (it rewrites the same K/V slots).
+    for (int attempt = 0; attempt < 2; ++attempt) {
     if ((rc = s->set_state(s->consumed, 0))) return rc;
     const bool step = s->use_step;
     for (size_t i = 0; i < pend; ++i) {
@@ -1685,6 +1761,11 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     if (logits) HIP_OK(hipMemcpyAsync(logits, s->LOGITS.p, (size_t)s->vocabulary * 4, hipMemcpyDeviceToHost, st), "logits");
     if (hidden) HIP_OK(hipMemcpyAsync(hidden, s->X.p, H * 4, hipMemcpyDeviceToHost, st), "hidden");
     HIP_OK(hipStreamSynchronize(st), "trace");
+    bool timed_out = false;
+    if ((rc = s->step_timed_out(timed_out, nullptr))) return rc;
+    if (!timed_out) break;
+    if ((rc = s->fall_back())) return rc;
+    }
     s->cached.insert(s->cached.end(), ids, ids + n);
     s->consumed = (uint32_t)s->cached.size();
     s->poisoned = false;

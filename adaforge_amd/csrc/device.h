@@ -1,6 +1,6 @@
 // Device helpers shared by the per-operation kernels and the persistent decode-step kernel
 // (gfx950): half conversions, wave/block reductions, the reference's fp64 rounding points,
-// Q6_K code unpacking, and the Q4_0 GEMV input prologue (exact int8 digit planes in LDS).
+// Q6_K code unpacking, and the Q4_0 GEMV input prologue (int8 digit planes in LDS).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -313,10 +313,11 @@ __device__ inline void input_stage(const InputStage& in, float* xs, uint32_t K, 
 
 // ---- Q4_0 GEMV on the int8 matrix cores ---------------------------------------------------------
 //
-// y = W x with W in Q4_0 and x fp32.  Each 32-element block b of x is written exactly as
-//   x_j = s_b (q0_j + q1_j 2^-7 + q2_j 2^-14 + q3_j 2^-21),  s_b = 2^(ilogb(max |x_b|) - 5),
-// with integer digits |q| <= 64 (every step is exact in fp32: scaling by a power of two,
-// rint, and subtracting an integer within 0.5).  Then for row r and block b
+// y = W x with W in Q4_0 and x fp32.  Each 32-element block b of x is written as
+//   x_j ~ s_b (q0_j + q1_j 2^-7 + q2_j 2^-14 + q3_j 2^-21),  s_b = 2^(e - 5),  e = ilogb(max |x_b|),
+// with integer digits |q| <= 64: elements with |x_j| >= 2^(e - 3) exactly, the others rounded to
+// the grid 2^(e - 26), an error of at most 2^(e - 27) <= 2^-27 max |x_b| (digit_words).  Then for
+// row r and block b
 //   sum_j (n_rj - 8) x_j = sum_t 2^-7t s_b sum_j n_rj q_tj  -  8 sum_j x_j,
 // and the integer sums over j come from v_mfma_i32_16x16x64_i8: A = the raw nibbles n of a
 // 16-row tile (lane (r, g) holds block g of row r: low nibbles feed one MFMA, high nibbles a

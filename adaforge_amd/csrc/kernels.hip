@@ -140,7 +140,8 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 // g read them, the others a zero block), B = the codes of (group g, row r) at lane 16 g + r, as
 // the lane's 16 unsigned 6-bit codes.  Lane 16 g + r then holds D[4 g + t][r] for t = 0..3, which
 // it folds with the group's plane scales and its sub-block scale, and with the row's d once per
-// record.  Input x_j = s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) per 16-element group, exactly.
+// record.  Input x_j ~ s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) per 16-element group (s = 2^(e - 5),
+// e = ilogb of the group's max |x|): exact for |x_j| >= 2^(e - 3), otherwise within 2^(e - 27).
 
 constexpr int kHeadRing = 6;  // records in flight per wave
 

@@ -14,7 +14,7 @@
 // next phase's early copies and the output stores, while waves 1-7 stream the weights, each
 // from its own contiguous run of weight records.  At a phase start all eight waves poll or copy
 // the phase's input into LDS (a streaming wave's weight loads still in flight were issued
-// before), and the input prologue (norms, exact int8 digit planes) runs on all 512 threads
+// before), and the input prologue (norms, int8 digit planes) runs on all 512 threads
 // from LDS.
 //
 // Coherence: the eight XCDs have private L2 caches.  Activations exchanged between workgroups
@@ -130,7 +130,9 @@ __device__ __forceinline__ void stamp(const Grid& g, uint32_t mark) {
 // the spin limit, which only a launch without co-resident workgroups could cause.  With `lead`
 // the workgroup first waits for all its waves (their stores are waited for before they arrive);
 // without it, wave 0 alone has published the phase's outputs and arrives for the workgroup.
-__device__ __forceinline__ bool grid_sync(Grid& g, bool lead) {
+// `extra` (0 or 1) raises the count waited for beyond what the grid can reach: the host's test of
+// the time-out (StepArgs::fail_phase).
+__device__ __forceinline__ bool grid_sync(Grid& g, bool lead, uint32_t extra) {
     if (lead) __syncthreads();
     if (threadIdx.x == 0) {
         stamp_at(g, g.p, M_ARRIVE);
@@ -140,7 +142,7 @@ __device__ __forceinline__ bool grid_sync(Grid& g, bool lead) {
         if (old + 1 == k * per) __hip_atomic_fetch_add(g.bar + kBarAll, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         uint32_t spins = 0;
         int ok = 1;
-        while (__hip_atomic_load(g.bar + kBarAll, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 8 * k) {
+        while (__hip_atomic_load(g.bar + kBarAll, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 8 * k + extra) {
             __builtin_amdgcn_s_sleep(1);
             if (++spins > kSpinLimit) {
                 ok = 0;
@@ -167,7 +169,10 @@ __device__ __forceinline__ void tagged_boundary(Grid& g) {
 }
 
 // Last workgroup out resets the barrier words for the next launch; with `advance` it also moves
-// the session position (a step without the head).
+// the session position (a step without the head), unless a workgroup failed: then the position
+// stays at the failed step, which the host runs again on the per-operation kernels.  A failing
+// workgroup's state stores are ordered before its exit arrival (release), and the last arrival
+// (acquire) reads them.
 __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance, bool failed) {
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -176,11 +181,13 @@ __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance
             __hip_atomic_store(state + ST_BAD, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(state + ST_STOP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        const uint32_t old = __hip_atomic_fetch_add(g.bar + kBarExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __hip_atomic_fetch_add(g.bar + kBarExit, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         if (old == gridDim.x - 1) {
             for (uint32_t i = 0; i < 10; ++i)
                 __hip_atomic_store(g.bar + 32 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (advance) state[ST_POS] += 1u;
+            const bool any_failed =
+                __hip_atomic_load(state + ST_BAD, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 2u;
+            if (advance && !any_failed) state[ST_POS] += 1u;
             state[ST_EPOCH] += 1u;  // read by the next launch, which the end of this one orders
         }
     }
@@ -999,8 +1006,10 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     else value_rows(std::false_type{});
     __syncthreads();
 
-    // chunk partial o[q][d] (unnormalised), m[q], l[q], staged in LDS and stored by wave 0
-    const uint32_t stride = GQ * (D + 2);
+    // chunk partial o[q][d] (unnormalised), m[q], l[q], staged in LDS and stored by wave 0; a chunk
+    // is `stride` floats, GQ (D + 2) rounded up to whole 16-byte pieces
+    constexpr uint32_t stride = step_part_stride(GQ);
+    static_assert(stride % 4 == 0 && stride >= GQ * (D + 2), "chunk partial stride");
     float* pst = scores;  // [GQ][D + 2]; the scores are no longer needed
     for (uint32_t i = tid; i < GQ * D; i += kThreads) {
         const uint32_t q = i / D, d = i % D;
@@ -1019,7 +1028,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
             *gp(reinterpret_cast<v2u*>(L.kcache + slot) + lane) = reinterpret_cast<const v2u*>(sh.knew)[lane];
             *gp(reinterpret_cast<v2u*>(L.vcache + slot) + lane) = reinterpret_cast<const v2u*>(sh.vnew)[lane];
         }
-        // stride * 4 bytes per chunk is a multiple of 16 (GQ * 1032)
+        // stride * 4 bytes per chunk: a multiple of 16, the padding included
         const v4u* ps = reinterpret_cast<const v4u*>(pst);
         for (uint32_t i = lane; i < stride / 4; i += 64) stc16(head_part, (c * stride + 4 * i) * 4, ps[i]);
         wait_vm();
@@ -1297,7 +1306,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         if (ph > 0) {
             if (tagged) {
                 tagged_boundary(g);
-            } else if (!grid_sync(g, (uint32_t)(ph - 1) % kPhases == P_ATTN)) {
+            } else if (!grid_sync(g, (uint32_t)(ph - 1) % kPhases == P_ATTN, (uint32_t)ph == a.fail_phase ? 1u : 0u)) {
                 failed = true;
                 break;
             }
@@ -1445,7 +1454,7 @@ hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint
 }
 
 uint32_t step_merge_chunks(uint32_t group, size_t lds) {
-    const size_t out = (size_t)group * 256 * 4, per = (size_t)group * 258 * 4;
+    const size_t out = (size_t)group * 256 * 4, per = (size_t)step_part_stride(group) * 4;
     return lds > out ? (uint32_t)((lds - out) / per) : 0u;
 }
 

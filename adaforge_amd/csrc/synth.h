@@ -114,6 +114,21 @@ static inline void synth_q4_block(uint64_t s, uint64_t b, double dlo, double dhi
     for (int j = 0; j < 8; ++j) out18[10 + j] = (uint8_t)(c >> (8 * j));
 }
 
+/* The same block with a random sign on d (bit 0 of the stream element that draws |d|, which
+ * the uniform draw does not use): GGUF's Q4_0 quantiser stores d = max / -8 for the block's
+ * largest-magnitude weight, so real scales take both signs, and with both signs the -0.5 d mean
+ * of a uniform nibble no longer gives every row of a matrix the same bias direction. */
+static inline void synth_q4_block_signed(uint64_t s, uint64_t b, double dlo, double dhi, uint8_t* out18) {
+    const uint64_t z = synth_at(s, 3 * b);
+    uint16_t d = synth_f32_to_f16((float)(dlo + (dhi - dlo) * synth_unit(z)));
+    if (z & 1u) d ^= 0x8000u;
+    out18[0] = (uint8_t)(d & 0xFF);
+    out18[1] = (uint8_t)(d >> 8);
+    uint64_t a = synth_at(s, 3 * b + 1), c = synth_at(s, 3 * b + 2);
+    for (int j = 0; j < 8; ++j) out18[2 + j] = (uint8_t)(a >> (8 * j));
+    for (int j = 0; j < 8; ++j) out18[10 + j] = (uint8_t)(c >> (8 * j));
+}
+
 /* Q6_K super-block b: 192 uniform random code bytes (so every 6-bit code is
  * uniform in 0..63), 16 int8 sub-scales uniform in [-32, 31], d ~ U[dlo, dhi]. */
 static inline void synth_q6_block(uint64_t s, uint64_t b, double dlo, double dhi, uint8_t* out210) {

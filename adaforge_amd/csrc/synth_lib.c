@@ -14,7 +14,7 @@
 uint64_t synth_tensor_seed(uint64_t base, const char* name) { return synth_seed(base, name); }
 
 typedef struct {
-    int kind; /* 0 q4, 1 q6, 2 normal */
+    int kind; /* 0 q4, 1 q6, 2 normal, 3 q4 with signed scales */
     uint64_t seed;
     double a, b;
     uint8_t* out;
@@ -26,6 +26,7 @@ static void* worker(void* p) {
     job* j = (job*)p;
     for (uint64_t i = j->begin; i < j->end; ++i) {
         if (j->kind == 0) synth_q4_block(j->seed, i, j->a, j->b, j->out + i * 18);
+        else if (j->kind == 3) synth_q4_block_signed(j->seed, i, j->a, j->b, j->out + i * 18);
         else if (j->kind == 1) synth_q6_block(j->seed, i, j->a, j->b, j->out + i * 210);
         else j->fout[i] = synth_normal(j->seed, i, j->a, j->b);
     }
@@ -56,6 +57,12 @@ static void run(int kind, uint64_t seed, double a, double b, uint8_t* out, float
 /* rows x columns Q4_0 matrix in GGUF row-major block order (18 B per 32 weights). */
 void synth_q4(uint64_t seed, uint32_t columns, uint32_t rows, double dlo, double dhi, uint8_t* out, int threads) {
     run(0, seed, dlo, dhi, out, NULL, (uint64_t)rows * (columns / 32), threads);
+}
+
+/* The same with |d| ~ U[dlo, dhi] and a random sign on d (synth_q4_block_signed). */
+void synth_q4_signed(uint64_t seed, uint32_t columns, uint32_t rows, double dlo, double dhi, uint8_t* out,
+                     int threads) {
+    run(3, seed, dlo, dhi, out, NULL, (uint64_t)rows * (columns / 32), threads);
 }
 
 /* rows x columns Q6_K matrix in GGUF row-major super-block order (210 B per 256 weights). */

@@ -31,6 +31,7 @@ def _synth():
         lib.synth_tensor_seed.restype = u64
         lib.synth_tensor_seed.argtypes = [u64, ctypes.c_char_p]
         lib.synth_q4.argtypes = [u64, u32, u32, f64, f64, P, i32]
+        lib.synth_q4_signed.argtypes = [u64, u32, u32, f64, f64, P, i32]
         lib.synth_q6.argtypes = [u64, u32, u32, f64, f64, P, i32]
         lib.synth_normal_vec.argtypes = [u64, u64, f64, f64, P, i32]
         lib.synth_half.restype = ctypes.c_uint16
@@ -43,10 +44,13 @@ def seed(name: str, base: int = BASE_SEED) -> int:
     return _synth().synth_tensor_seed(base, name.encode())
 
 
-def q4(name, columns, rows, dlo=1e-3, dhi=2e-2, base=BASE_SEED):
-    """rows x columns Q4_0 (GGUF bytes): d ~ U[dlo, dhi] as fp16, uniform nibbles."""
+def q4(name, columns, rows, dlo=1e-3, dhi=2e-2, base=BASE_SEED, signed=False):
+    """rows x columns Q4_0 (GGUF bytes): d ~ U[dlo, dhi] as fp16, uniform nibbles; with `signed`,
+    |d| ~ U[dlo, dhi] with a random sign (GGUF's quantiser stores d = max / -8, so real scales
+    take both signs)."""
     out = np.empty(rows * (columns // 32) * 18, dtype=np.uint8)
-    _synth().synth_q4(seed(name, base), columns, rows, dlo, dhi, out.ctypes.data, THREADS)
+    fn = _synth().synth_q4_signed if signed else _synth().synth_q4
+    fn(seed(name, base), columns, rows, dlo, dhi, out.ctypes.data, THREADS)
     return out
 
 
@@ -131,15 +135,23 @@ class SynthModel:
 
 def model(name="gemma3-12b", layers=48, hidden=3840, intermediate=15360, q_heads=16, kv_heads=8, head_width=256,
           vocabulary=262144, window=1024, local_theta=1e4, global_theta=1e6, global_every=6, scale=None,
-          table_d=(1e-5, 1e-4), v_norm=False, rope_context=131072, base=BASE_SEED):
+          table_d=(1e-6, 1e-5), v_norm=False, rope_context=131072, base=BASE_SEED, signed_q4=True):
     """Gemma-3-12B-shaped decode model with seeded random weights (BASELINE config 4 at the defaults).
 
     Layer i is global iff i % global_every == global_every - 1 (layers 5, 11, ..., 47); the others
     use a sliding window.  Norm weights are 1 + N(0, 0.1) (eps 1e-6), projections Q4_0 with
-    d ~ U[1e-3, 2e-2].  The tied Q6_K table uses d ~ U[table_d]: with config 2's [1e-4, 5e-3] the
-    sqrt(hidden)-scaled embedding is ~60x larger than every normalised residual branch, so the
-    model would only repeat its input token; the smaller range keeps the greedy path
-    context-dependent.  The attention scale defaults to 1/sqrt(head_width)."""
+    |d| ~ U[1e-3, 2e-2].  The attention scale defaults to 1/sqrt(head_width).
+
+    Two choices keep the greedy path of this random model varied and context-dependent:
+    * Q4_0 scales carry a random sign (`signed_q4`, as GGUF's quantiser's d = max / -8 does).  With
+      d > 0 every weight (n - 8) d of a uniform nibble n has mean -d / 2, so all rows of a matrix
+      share one positive bias direction and every token is driven to the same output (the greedy
+      run then repeats one id whatever the context).
+    * The tied Q6_K table uses d ~ U[table_d].  The sqrt(hidden)-scaled embedding of the input
+      token adds about 770 sigma_w / rms(h) times the typical winning logit to that token's own
+      logit (sigma_w: the table's weight scale, h: the final residual); at config 2's
+      [1e-4, 5e-3] the model only repeats its input, and even at [1e-5, 1e-4] a token, once
+      emitted, keeps winning.  At [1e-6, 1e-5] the bonus is about 0.15 of it."""
     if scale is None:
         scale = 1.0 / float(np.sqrt(head_width))
     p = f"{name}."
@@ -153,9 +165,9 @@ def model(name="gemma3-12b", layers=48, hidden=3840, intermediate=15360, q_heads
         L = f"blk.{i}."
         layer_list.append(SynthLayer(
             input_norm=nw(L + "attn_norm", hidden),
-            q=q4(p + L + "attn_q", hidden, q_heads * head_width, base=base),
-            k=q4(p + L + "attn_k", hidden, kv_heads * head_width, base=base),
-            v=q4(p + L + "attn_v", hidden, kv_heads * head_width, base=base),
+            q=q4(p + L + "attn_q", hidden, q_heads * head_width, base=base, signed=signed_q4),
+            k=q4(p + L + "attn_k", hidden, kv_heads * head_width, base=base, signed=signed_q4),
+            v=q4(p + L + "attn_v", hidden, kv_heads * head_width, base=base, signed=signed_q4),
             q_norm=nw(L + "attn_q_norm", head_width),
             k_norm=nw(L + "attn_k_norm", head_width),
             rope_base=global_theta if is_global else local_theta,
@@ -164,12 +176,12 @@ def model(name="gemma3-12b", layers=48, hidden=3840, intermediate=15360, q_heads
             q_heads=q_heads, kv_heads=kv_heads, head_width=head_width,
             window=None if is_global else window,
             scale=scale,
-            o=q4(p + L + "attn_output", q_heads * head_width, hidden, base=base),
+            o=q4(p + L + "attn_output", q_heads * head_width, hidden, base=base, signed=signed_q4),
             post_attn_norm=nw(L + "post_attention_norm", hidden),
             ffn_norm=nw(L + "ffn_norm", hidden),
-            gate=q4(p + L + "ffn_gate", hidden, intermediate, base=base),
-            up=q4(p + L + "ffn_up", hidden, intermediate, base=base),
-            down=q4(p + L + "ffn_down", intermediate, hidden, base=base),
+            gate=q4(p + L + "ffn_gate", hidden, intermediate, base=base, signed=signed_q4),
+            up=q4(p + L + "ffn_up", hidden, intermediate, base=base, signed=signed_q4),
+            down=q4(p + L + "ffn_down", intermediate, hidden, base=base, signed=signed_q4),
             post_ffn_norm=nw(L + "post_ffw_norm", hidden),
             v_norm=v_norm,
         ))

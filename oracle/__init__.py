@@ -350,7 +350,7 @@ class Model:
         return ids[:k].tolist(), bool(stopped.value), margins[:k + int(stopped.value)]
 
 
-def check_layer_stack(model, ids, outputs, kv, atol=1e-4, rtol=1e-4, kv_slack=1e-5, threads=None):
+def check_layer_stack(model, ids, outputs, kv, atol=1e-4, rtol=1e-4, kv_slack=1e-5, threads=None, positions=None):
     """Teacher-forced check of a GPU trace (crates/cuda-backend/src/stack.rs:707-817 contract).
 
     For each token t (positions 0..n-1 from an empty cache) and layer l the oracle runs layer l
@@ -364,22 +364,30 @@ def check_layer_stack(model, ids, outputs, kv, atol=1e-4, rtol=1e-4, kv_slack=1e
     1e-7 of the head's scale before rounding, which near zero spans several fp16 ulps).
 
     outputs: [n][layers][hidden]; kv: [n][layers][2][kv_rows] float32 (fp16 values).
+    positions: the token positions to check (default: all); the K/V history of every position
+    still comes from the GPU's trace.
     Returns (max layer tolerance ratio, max K/V ratio (<= 1 passes), number of K/V values whose
     fp16 rounding differs from the oracle's)."""
     H, V = model.hidden, model.vocabulary
     n = len(ids)
     table = layer_table(model)
-    emb = embedding(model.table, H, V, ids, scaled=True).reshape(n, H)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    # EmbeddingBatch takes at most 256 ids per call (crates/domain/src/embedding.rs)
+    emb = np.concatenate([embedding(model.table, H, V, ids[i:i + 256], scaled=True)
+                          for i in range(0, n, 256)]).reshape(n, H)
     hist = []
     for L in model.layers:
         kn = L.kv_heads * L.head_width
         hist.append((np.zeros(n * kn, np.float32), np.zeros(n * kn, np.float32), kn, L.head_width))
     worst, kv_worst, differ = 0.0, 0.0, 0
+    check = set(range(n)) if positions is None else set(int(p) for p in positions)
     for t in range(n):
         for l in range(len(model.layers)):
             keys, values, kn, hw = hist[l]
             keys[t * kn:(t + 1) * kn] = kv[t, l, 0, :kn]
             values[t * kn:(t + 1) * kn] = kv[t, l, 1, :kn]
+            if t not in check:
+                continue
             x = emb[t] if l == 0 else outputs[t, l - 1]
             y, k_own, v_own = layer_forward(model, table, l, x, keys, values, t, given_kv=True, threads=threads)
             try:

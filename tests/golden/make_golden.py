@@ -3,7 +3,7 @@ restatement of AdaForge's FP64 oracles).  Inputs come from the seeded generators
 adaforge_amd/synth.py, so any host regenerates identical inputs.
 
     python tests/golden/make_golden.py            # configs 0-3 (seconds)
-    python tests/golden/make_golden.py --config4  # + the 48-layer decode (~30 min on 8 cores)
+    python tests/golden/make_golden.py --config4  # + the 48-layer decode (~15 min on 8 cores)
 """
 import argparse
 import json
@@ -71,15 +71,31 @@ def config3():
     dump("config3_attention.json", out)
 
 
-def config4(threads):
+def config4(threads, top=8):
+    """The oracle's greedy run (or_model_generate's order: each step's logits, f32 greedy, then the
+    id is consumed) with each step's top `top` ids by f32 logit and their f64 logits."""
     model = synth.model()
     prompt = synth.prompt_ids(workloads.C4_PROMPT, model.vocabulary, name="config4.prompt")
     ref = oracle.Model(model, capacity=workloads.C4_PROMPT + workloads.C4_DECODE + 1, threads=threads)
     t = time.time()
-    ids, stopped, margins = ref.generate(prompt, [], workloads.C4_DECODE)
+    for tok in prompt:
+        ref.step(int(tok))
+    ids, margins, top_ids, top_logits = [], [], [], []
+    for _ in range(workloads.C4_DECODE):
+        logits = ref.logits()
+        l32 = logits.astype(np.float32)
+        tok = oracle.greedy(l32)
+        order = np.argsort(-l32, kind="stable")[:top]
+        second = np.max(np.delete(l32, tok))
+        ids.append(int(tok))
+        margins.append(float(l32[tok] - second))
+        top_ids.append([int(i) for i in order])
+        top_logits.append(f64list(logits[order]))
+        ref.step(tok)
     ref.close()
-    dump("config4_decode.json", {"prompt": [int(i) for i in prompt], "tokens": ids, "stopped": stopped,
-                                 "margins": [float(m) for m in margins], "oracle_seconds": time.time() - t,
+    dump("config4_decode.json", {"prompt": [int(i) for i in prompt], "tokens": ids, "stopped": False,
+                                 "margins": margins, "top_ids": top_ids, "top_logits": top_logits,
+                                 "distinct": len(set(ids)), "oracle_seconds": time.time() - t,
                                  "threads": threads})
 
 

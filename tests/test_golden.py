@@ -69,3 +69,11 @@ def test_config4_fixture_is_consistent():
     assert g["prompt"] == [int(i) for i in prompt]
     assert len(g["tokens"]) == W.C4_DECODE and len(g["margins"]) == W.C4_DECODE
     assert all(0 <= t < 262144 for t in g["tokens"]) and not g["stopped"]
+    # a varied greedy path (a model that repeats one id checks nothing about positions and caches)
+    assert len(set(g["tokens"])) >= 32 and g["distinct"] == len(set(g["tokens"]))
+    # per-step top-8: the chosen id first, f32 logits descending, margins from the same values
+    for k, (tok, ids, lg, m) in enumerate(zip(g["tokens"], g["top_ids"], g["top_logits"], g["margins"])):
+        l32 = np.asarray(lg, np.float64).astype(np.float32)
+        assert ids[0] == tok and len(set(ids)) == len(ids) == 8, k
+        assert np.all(np.diff(l32) <= 0), k
+        assert abs(float(l32[0] - l32[1]) - m) <= 1e-6 * max(1.0, abs(float(l32[0]))), k

@@ -1,7 +1,14 @@
 """BASELINE config 4 on the GPU: the 48-layer Gemma-3-12B-shaped decode loop (seeded weights,
 128-token prompt, 256 greedy tokens) against the oracle's golden run (tests/golden/
-config4_decode.json), teacher-forced per-layer parity on the first tokens, and a stop id in the
-middle of the sequence."""
+config4_decode.json: ids, per-step margins and top-8 logits), checked three ways:
+  * free-running: the session's own greedy ids equal the golden ids (README.md:379-401 token
+    identity), up to the first step whose golden top-2 margin is below MARGIN;
+  * teacher-forced: the golden ids fed one at a time; every step's GPU argmax equals the golden id
+    where its margin is at least MARGIN, and the GPU logits of the golden top-8 ids lie within
+    1e-4 + 1e-4 |ref| of the oracle's (crates/cuda-backend/src/logits.rs:70-201);
+  * per layer: every layer output at positions after the 128-token prefill, with the oracle run on
+    the GPU's own layer inputs and fp16 K/V history (stack.rs:707-817).
+and a stop id in the middle of the sequence."""
 import json
 import os
 
@@ -17,7 +24,8 @@ pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config4_decode.json")
 # Below this top-1/top-2 logit margin an fp32-vs-fp64 difference within the 1e-4 + 1e-4 |ref|
-# tolerance may legitimately change the greedy choice; ids are compared up to the first such step.
+# tolerance may legitimately change the greedy choice; the free-running ids are compared up to the
+# first such step, and teacher-forced steps with such a margin are not required to agree.
 MARGIN = 1e-3
 THREADS = max(1, min(16, os.cpu_count() or 1))
 
@@ -43,10 +51,10 @@ def session(model):
 
 
 def comparable(g):
-    """Number of leading golden ids whose choice is decided by more than MARGIN."""
+    """Number of leading golden ids whose choice is decided by at least MARGIN."""
     for i, m in enumerate(g["margins"]):
         if m < MARGIN:
-            return i + 1  # the id at i itself is still compared only if its margin is large
+            return i
     return len(g["tokens"])
 
 
@@ -63,21 +71,43 @@ def test_config4_greedy_ids_match_oracle_golden(golden, model, session):
     second = session.generate(prompt + first.ids, stop, 128)
     got = first.ids + second.ids
     n = comparable(golden)
-    if n < len(want):
-        n -= 1
+    print(f"config4: {len(set(want))} distinct golden ids; free-running ids compared over {n} steps", flush=True)
+    assert n >= 32
     assert got[:n] == want[:n], next(i for i in range(n) if got[i] != want[i])
 
 
-def test_config4_stop_ids(golden, model, session):
-    """A stop id ends the call before it: at the first id that is new in the golden run (none is
-    new after the first in this seeded model, whose greedy path settles on one id), or at once."""
+def test_config4_teacher_forced_argmax_and_top8_logits(golden, model, session):
+    """Each golden id fed in turn (af_session_trace): the logits after it are the next step's."""
     session.reset()
     prompt, want = golden["prompt"], golden["tokens"]
-    n = min(comparable(golden) - 1, 128)
-    k = next((i for i in range(1, n) if want[i] not in want[:i]), 0)
+    _, _, logits, _ = session.trace(prompt, layer_outputs=False, hidden=False)
+    worst, agreed, skipped = 0.0, 0, 0
+    for k in range(W.C4_DECODE):
+        ids = np.asarray(golden["top_ids"][k])
+        ref = np.asarray(golden["top_logits"][k], np.float64)
+        _, r = oracle.compare(ref, logits[ids])
+        worst = max(worst, r)
+        if golden["margins"][k] >= MARGIN:
+            assert int(np.argmax(logits)) == want[k] and oracle.greedy(logits) == want[k], k
+            agreed += 1
+        else:
+            skipped += 1
+        if k + 1 < W.C4_DECODE:
+            _, _, logits, _ = session.trace([want[k]], layer_outputs=False, hidden=False)
+    print(f"config4 teacher-forced: {agreed} steps agree, {skipped} near-ties skipped, "
+          f"top-8 logit ratio {worst:.3f}", flush=True)
+
+
+def test_config4_stop_ids(golden, model, session):
+    """A stop id ends the call before it: the first id in the golden run that differs from every
+    earlier one, past the first step."""
+    session.reset()
+    prompt, want = golden["prompt"], golden["tokens"]
+    n = min(comparable(golden), 128)
+    k = next(i for i in range(2, n) if want[i] not in want[:i])
     r = session.generate(prompt, [want[k]], 128)
     assert r.stopped and r.ids == want[:k]
-    assert r.stats.decode_tokens == max(k - 1, 0)
+    assert r.stats.decode_tokens == k - 1
 
 
 def test_config4_teacher_forced_layers_and_logits(model, session):
@@ -91,3 +121,17 @@ def test_config4_teacher_forced_layers_and_logits(model, session):
     n = oracle.rmsnorm(model.final_norm, model.final_eps, hidden).astype(np.float32)
     ref = oracle.q6_matvec(model.table, model.hidden, model.vocabulary, n, threads=THREADS)
     oracle.compare(ref, logits)
+
+
+def test_config4_layers_after_prefill_teacher_forced(golden, model, session):
+    """Every layer of the 48 at the last prompt position and the first decode positions (context
+    128..131: several attention chunks per KV head, merged across workgroups), with the oracle fed
+    the GPU's own layer inputs and the GPU's fp16 K/V history of all earlier positions."""
+    session.reset()
+    ids = golden["prompt"] + golden["tokens"][:3]
+    kv_rows = model.layers[0].kv_heads * model.layers[0].head_width
+    outputs, kv, _, _ = session.trace(ids, kv_rows=kv_rows, logits=False, hidden=False)
+    positions = [W.C4_PROMPT - 1, W.C4_PROMPT, W.C4_PROMPT + 2]
+    ratio, ulps, differ = oracle.check_layer_stack(model, ids, outputs, kv, threads=THREADS, positions=positions)
+    print(f"config4 after prefill: layer ratio {ratio:.3f}, K/V ratio {ulps:.3f}, {differ} fp16 values differ",
+          flush=True)

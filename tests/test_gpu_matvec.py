@@ -105,3 +105,18 @@ def test_device_pointer_entry_point_matches_host_level_run():
     finally:
         N.lib().af_q4_free(h)
     assert np.array_equal(y, gemv(w, cols, rows, [x])[0])
+
+
+def test_wide_dynamic_range_blocks_within_tolerance():
+    """Input blocks whose elements span 2^-40 .. 2^12 of one another: the digit image rounds the
+    elements far below their block's maximum (to 2^-27 of it, tests/test_digits.py), and the
+    outputs stay within 1e-4 + 1e-4 |ref| of the FP64 oracle on every row."""
+    cols, rows = 3840, 512
+    w = synth.q4("wide.W", cols, rows, signed=True)
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal(cols) * np.exp2(rng.integers(-40, 12, cols))).astype(np.float32)
+    x[::32] = np.float32(1000.0)                       # one large element per block
+    x[5::32] = np.float32(3.0e-9)
+    out = gemv(w, cols, rows, [x, -x, x * np.float32(2.0 ** -30)])
+    for xi, y in zip((x, -x, x * np.float32(2.0 ** -30)), out):
+        oracle.compare(oracle.q4_matvec(w, cols, rows, xi), y)

@@ -225,3 +225,30 @@ def test_attention_large_scores_and_value_norm():
     case = small_case(300, None, 4, 2, qscale=8.0, v_norm=True, tag="big")
     out, _, _ = attention_case(case)
     oracle.compare(small_reference(case), out)
+
+
+@pytest.mark.parametrize("width", [3840, 256, 100])
+def test_rmsnorm_check_port_eight_patterns_rms_norm_rs_22(width):
+    """GpuDiagnostics::check_rms_norm (crates/cuda-backend/src/rms_norm.rs:9-149): the reference's
+    eight input vectors (zeros, ones, 1e-8, alternating signs, ramp, xorshift, one spike,
+    +-8e9 steps) normalised on the GPU with weights 1 + N(0, 0.1) and eps 1e-6, every element
+    within 2e-5 + 2e-5 |ref| of the FP64 oracle (rms_norm.rs:131-149)."""
+    from adaforge_amd.backend import HipDiagnostics, RmsNorm
+    w = synth.normal(f"rmscheck.{width}", width, 1.0, 0.1)
+    report = HipDiagnostics(domain=oracle).check_rms_norm(RmsNorm(w, 1e-6))
+    assert (report.width, report.vectors) == (width, 8)
+    assert report.max_tolerance_ratio <= 1.0 and report.median_kernel_ms > 0.0
+    print(f"rmsnorm-check width {width}: max ratio {report.max_tolerance_ratio:.3g}, "
+          f"median {1000 * report.median_kernel_ms:.1f} us")
+
+
+def test_rmsnorm_device_entry_point_multiple_vectors():
+    """af_rmsnorm on device pointers: several contiguous vectors in one launch, each normalised
+    on its own (crates/domain/src/rms_norm.rs:24-41)."""
+    width, vectors = 3840, 5
+    w = synth.normal("rmsdev.w", width, 1.0, 0.1)
+    x = synth.normal("rmsdev.x", width * vectors, 0.0, 3.0)
+    xb, wb, yb = hip.Buffer.from_numpy(x), hip.Buffer.from_numpy(w), hip.Buffer(width * vectors)
+    N.check(L().af_rmsnorm(xb.ptr, wb.ptr, yb.ptr, width, vectors, ctypes.c_float(1e-6), None))
+    hip.synchronize()
+    oracle.compare(oracle.rmsnorm(w, 1e-6, x), yb.numpy(), 2e-5, 2e-5)

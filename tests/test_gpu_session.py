@@ -56,13 +56,30 @@ def fixture_model(table, rope_context, window):
                       layers=[layer(), layer()])
 
 
-def open_direct(model, capacity):
-    """A session whose steps run as direct launches instead of graph replays."""
-    os.environ["AF_DISABLE_GRAPHS"] = "1"
+def open_with_env(model, capacity, **env):
+    """A session opened with the given AF_* environment switches set (restored afterwards)."""
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
     try:
         return HipDiagnostics().open_session(model, capacity)
     finally:
-        del os.environ["AF_DISABLE_GRAPHS"]
+        for k, v in saved.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+def open_direct(model, capacity):
+    """A session whose steps run as direct launches instead of graph replays."""
+    return open_with_env(model, capacity, AF_DISABLE_GRAPHS=1)
+
+
+def ran_step_kernel(session, cached):
+    """True if the session's decode steps run on the persistent step kernel (it reports "layers"
+    launches; the per-operation kernels report their own kinds).  Consumes two more ids."""
+    _, t = session.profile(cached, 2)
+    return t["layers"][0] > 0
 
 
 def head_reference(model, hidden):
@@ -99,13 +116,15 @@ def test_session_prefix_reset_stop_and_budget_stack_rs_1887():
         assert again.stats.cached_tokens == 1 and again.stats.prompt_tokens == 1
 
 
-def test_graph_matches_direct_for_changing_tokens_positions_and_reset_stack_rs_1980():
+@pytest.mark.parametrize("step_kernel", ["1", "0"])
+def test_graph_matches_direct_for_changing_tokens_positions_and_reset_stack_rs_1980(step_kernel):
     """Graph replays and direct launches leave bit-identical caches: after generating from each
     sequence, a trace of one more token (which reads every cached K/V row of the sliding
-    window) returns identical layer outputs, appended K/V and logits on both sessions."""
+    window) returns identical layer outputs, appended K/V and logits on both sessions.  Both the
+    persistent step kernel (with the head, one graph per token) and the per-operation kernels."""
     model = fixture_model(packed_table(), 8, 2)
-    graph = HipDiagnostics().open_session(model, 8)
-    direct = open_direct(model, 8)
+    graph = open_with_env(model, 8, AF_STEP_KERNEL=step_kernel)
+    direct = open_with_env(model, 8, AF_STEP_KERNEL=step_kernel, AF_DISABLE_GRAPHS=1)
     try:
         for seq in ([0, 3, 1, 2], [4, 2, 0, 1]):
             a = graph.generate(seq[:3], [4], 2)
@@ -137,27 +156,75 @@ def test_fixture_model_tokens_and_logits_match_oracle():
     oracle.compare(head_reference(model, hidden), logits)
 
 
-@pytest.mark.parametrize("v_norm,layer_scale", [(False, 1.0), (True, 0.5)])
-def test_multi_layer_model_teacher_forced_and_greedy_ids(v_norm, layer_scale):
+@pytest.mark.parametrize("v_norm,layer_scale,q_heads,kv_heads,shared_v,step_kernel", [
+    (False, 1.0, 2, 1, False, "1"),
+    (True, 0.5, 2, 1, False, "1"),
+    (False, 1.0, 2, 2, False, "1"),   # one query head per KV head
+    (False, 1.0, 4, 1, False, "1"),   # four query heads per KV head
+    (True, 1.0, 2, 1, True, "1"),     # V shares K's weights (stack.rs:172), V-norm on
+    (False, 1.0, 4, 2, True, "0"),    # the per-operation kernels in their graph
+])
+def test_multi_layer_model_teacher_forced_and_greedy_ids(v_norm, layer_scale, q_heads, kv_heads, shared_v,
+                                                         step_kernel):
     """Four layers (local window 3, global every second layer) past the window's wrap; with a
-    layer scale the post-FFN norm and residual run outside the down projection."""
-    model = synth.tiny_model(layers=4, vocabulary=2048, window=3, name="session", v_norm=v_norm)
+    layer scale the post-FFN norm and residual run outside the down projection.  Greedy ids equal
+    the oracle's, and every layer of a trace is within tolerance teacher-forced."""
+    model = synth.tiny_model(layers=4, vocabulary=2048, window=3, name=f"session{q_heads}{kv_heads}", v_norm=v_norm,
+                             q_heads=q_heads, kv_heads=kv_heads)
     for L in model.layers:
         L.layer_scale = layer_scale
+        if shared_v:
+            L.v = None
     prompt = [int(i) for i in synth.prompt_ids(9, model.vocabulary, name="session.prompt")]
     stop = [model.vocabulary - 1]
-    ref = oracle.Model(model, capacity=32)
+    ref = oracle.Model(model, capacity=40)
     want, _, margins = ref.generate(prompt, stop, 8)
     ref.close()
     kv_rows = model.layers[0].kv_heads * model.layers[0].head_width
-    with HipDiagnostics().open_session(model, 32) as s:
+    with open_with_env(model, 40, AF_STEP_KERNEL=step_kernel) as s:
         got = s.generate(prompt, stop, 8)
         s.reset()
         ids = prompt + want[:4]
         outputs, kv, logits, hidden = s.trace(ids, kv_rows=kv_rows)
+        assert ran_step_kernel(s, ids) == (step_kernel == "1")
     assert got.ids == want, (got.ids, want, margins)
     oracle.check_layer_stack(model, ids, outputs, kv)
     oracle.compare(head_reference(model, hidden), logits)
+
+
+def test_step_kernel_time_out_falls_back_to_per_operation_kernels():
+    """A step-kernel launch whose grid barrier times out (forced from the host: the barrier opening
+    layer 1's down projection waits for one arrival more than the grid makes) does not poison the
+    session: the failed step and the rest of the generation run again on the per-operation
+    kernels, and ids, layer outputs and logits match the oracle.  Covers a failure during prefill
+    (the first launch is a prefill step) and the session's later calls."""
+    model = synth.tiny_model(layers=4, vocabulary=2048, window=3, name="fallback")
+    prompt = [int(i) for i in synth.prompt_ids(7, model.vocabulary, name="fallback.prompt")]
+    stop = [model.vocabulary - 1]
+    ref = oracle.Model(model, capacity=40)
+    want, _, margins = ref.generate(prompt, stop, 10)
+    ref.close()
+    kv_rows = model.layers[0].kv_heads * model.layers[0].head_width
+    with open_with_env(model, 40, AF_STEP_FAIL_PHASE=9) as s:
+        got = s.generate(prompt, stop, 10)
+        assert got.ids == want, (got.ids, want, margins)
+        s.reset()
+        outputs, kv, logits, hidden = s.trace(prompt, kv_rows=kv_rows)
+        assert not ran_step_kernel(s, prompt)
+    oracle.check_layer_stack(model, prompt, outputs, kv)
+    oracle.compare(head_reference(model, hidden), logits)
+    # the same failure met first by a trace, then by a decode step
+    with open_with_env(model, 40, AF_STEP_FAIL_PHASE=9) as s:
+        outputs2, kv2, _, _ = s.trace(prompt[:3], kv_rows=kv_rows)
+        oracle.check_layer_stack(model, prompt[:3], outputs2, kv2)
+        got = s.generate(prompt, stop, 10)
+        assert got.ids == want, (got.ids, want)
+    with open_with_env(model, 40, AF_STEP_FAIL_PHASE=9) as s:
+        got = s.generate(prompt[:1], stop, 10)  # no prefill step: the first decode step fails
+        ref = oracle.Model(model, capacity=40)
+        want1, _, _ = ref.generate(prompt[:1], stop, 10)
+        ref.close()
+        assert got.ids == want1, (got.ids, want1)
 
 
 def test_continuation_and_streaming_equal_one_generation():
