@@ -101,6 +101,7 @@ SIGNATURES = {
     "af_q6_upload": (i32, [u8p, sz, u32, u32, ctypes.POINTER(P)]),
     "af_q6_free": (None, [P]),
     "af_q6_gemv_argmax": (i32, [P, P, P, P, P]),
+    "af_q6_gemv_argmax_noalloc": (i32, [P, P, P, P, P]),
     "af_rmsnorm": (i32, [P, P, P, u32, u32, f32, P]),
     "af_ffn_create": (i32, [ctypes.POINTER(FfnDesc), ctypes.POINTER(P)]),
     "af_ffn_free": (None, [P]),

@@ -172,6 +172,7 @@ hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t wid
                           hipStream_t s);
 hipError_t launch_resid(const InputStage& in, uint32_t width, float* y, hipStream_t s);
 hipError_t launch_advance(uint32_t* state, hipStream_t s);
+hipError_t launch_zero_words(uint32_t* p, uint32_t n, hipStream_t s);
 uint32_t head_grid(uint32_t rows);
 
 constexpr uint32_t kAttnMinChunk = 32;

@@ -366,6 +366,31 @@ int grow(DevMem& m, size_t bytes, bool zero, const char* what) {
     return AF_OK;
 }
 
+// Scratch of the allocation-free head entry point (af_q6_gemv_argmax_noalloc): a fixed array in
+// the library's device memory, one copy per GPU, held until the process ends.  Bytes [0, 256) hold
+// the completion counter, then one 16-byte argmax partial per workgroup.  Its device address is
+// looked up once per device (with that device current) and kept: in host code `scratch` names a
+// host-side stand-in, never the device copy.
+constexpr size_t kNoAllocScratchBytes = AF_NOALLOC_SCRATCH_BYTES;
+constexpr size_t kNoAllocCounterBytes = 256;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+constexpr int kMaxDevices = 64;
+std::once_flag g_noalloc_once[kMaxDevices];
+void* g_noalloc_ptr[kMaxDevices];
+hipError_t g_noalloc_status[kMaxDevices];
+
+int noalloc_scratch(void** out) {
+    int dev = -1;
+    HIP_OK(hipGetDevice(&dev), "current device");
+    if (dev < 0 || dev >= kMaxDevices) return fail(AF_ERR_DEVICE, "device index outside the scratch table");
+    std::call_once(g_noalloc_once[dev], [dev] {
+        g_noalloc_status[dev] = hipGetSymbolAddress(&g_noalloc_ptr[dev], HIP_SYMBOL(scratch));
+    });
+    HIP_OK(g_noalloc_status[dev], "scratch array address");
+    *out = g_noalloc_ptr[dev];
+    return AF_OK;
+}
+
 }  // namespace
 
 // ================================================================================================
@@ -452,6 +477,30 @@ int af_q6_gemv_argmax(const af_q6* m, const float* x, float* logits, uint32_t* r
     a.partial = g_scratch.head_partial.as<uint4>();
     a.counter = g_scratch.head_counter.as<uint32_t>();
     a.result = result;
+    HIP_OK(launch_head(a, IN_PLAIN, grid, (hipStream_t)stream), "Q6_K head launch");
+    return AF_OK;
+}
+
+int af_q6_gemv_argmax_noalloc(const af_q6* m, const float* x, float* logits, uint32_t* result, void* stream) {
+    if (!m || !x || !result) return fail(AF_ERR_INVALID, "null argument");
+    const uint32_t grid = head_grid(m->m.rows);
+    const size_t need = kNoAllocCounterBytes + (size_t)grid * sizeof(uint4);
+    if (need > kNoAllocScratchBytes)
+        return fail(AF_ERR_INVALID, "Q6_K head needs " + std::to_string(need) + " bytes of scratch, above the " +
+                                        std::to_string(kNoAllocScratchBytes) + "-byte allocation-free array");
+    void* base = nullptr;
+    int rc = noalloc_scratch(&base);
+    if (rc) return rc;
+    uint8_t* p = static_cast<uint8_t*>(base);
+    HeadArgs a{};
+    a.w = m->m.view();
+    a.in.x = x;
+    a.logits = logits;
+    a.partial = reinterpret_cast<uint4*>(p + kNoAllocCounterBytes);
+    a.counter = reinterpret_cast<uint32_t*>(p);
+    a.result = result;
+    // the array keeps the last call's contents: the counter must start at zero
+    HIP_OK(launch_zero_words(a.counter, 1, (hipStream_t)stream), "scratch clear");
     HIP_OK(launch_head(a, IN_PLAIN, grid, (hipStream_t)stream), "Q6_K head launch");
     return AF_OK;
 }

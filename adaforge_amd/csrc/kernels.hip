@@ -700,6 +700,17 @@ hipError_t launch_resid(const InputStage& in, uint32_t width, float* y, hipStrea
 
 __global__ void advance_kernel(uint32_t* state) { state[ST_POS] += 1u; }
 
+// Clears n words with vector stores (a kernel rather than a memset, so that a caller may capture
+// it in a graph).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, uint32_t n) {
+    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+hipError_t launch_zero_words(uint32_t* p, uint32_t n, hipStream_t s) {
+    hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_advance(uint32_t* state, hipStream_t s) {
     hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(1), 0, s, state);
     return hipGetLastError();

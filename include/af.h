@@ -97,6 +97,19 @@ void af_q6_free(af_q6* m);
  * (device, rows floats) may be NULL. */
 int af_q6_gemv_argmax(const af_q6* m, const float* x, float* logits, uint32_t* result, void* stream);
 
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  The same computation
+ * and results as af_q6_gemv_argmax, but the kernel's scratch (a completion counter and one 16-byte
+ * argmax partial per workgroup) lives in a fixed array inside the library, AF_NOALLOC_SCRATCH_BYTES
+ * per GPU, held by each GPU the library runs on until the process ends, instead of memory the
+ * library allocates on its first call.  It allocates nothing: no hipMalloc, no hipFree.  Every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU (on different streams, or
+ * from different threads) race and must be serialised by the caller.  Matrices whose scratch would
+ * exceed the array are rejected with AF_ERR_INVALID (the head runs at most 256 workgroups, so every
+ * valid Q6_K matrix fits: 256 + 256 * 16 bytes). */
+#define AF_NOALLOC_SCRATCH_BYTES 8192u
+int af_q6_gemv_argmax_noalloc(const af_q6* m, const float* x, float* logits, uint32_t* result, void* stream);
+
 /* RMSNorm of `vectors` contiguous rows (kernels/ada/rms_norm.cu rms_norm, rms_norm.rs:72-108). */
 int af_rmsnorm(const float* x, const float* weights, float* y, uint32_t width, uint32_t vectors, float eps,
                void* stream);
