@@ -800,8 +800,11 @@ int validate_layer(const af_layer_weights& w, uint32_t hidden, uint32_t capacity
     return AF_OK;
 }
 
-enum KernelKind { K_QKV = 0, K_ATTN, K_OPROJ, K_GATEUP, K_DOWN, K_HEAD, K_LAYERS, K_BARRIER, K_KINDS };
-const char* const kKindNames[K_KINDS] = {"qkv", "attention", "o_proj", "gate_up", "down", "head", "layers", "barrier"};
+// K_LAYERS: plain launches of the step kernel; K_LAYERS_TL: launches that also write the in-kernel
+// timeline (slower by the timestamp stores).
+enum KernelKind { K_QKV = 0, K_ATTN, K_OPROJ, K_GATEUP, K_DOWN, K_HEAD, K_LAYERS, K_BARRIER, K_LAYERS_TL, K_KINDS };
+const char* const kKindNames[K_KINDS] = {"qkv", "attention", "o_proj", "gate_up", "down", "head", "layers", "barrier",
+                                         "layers_timeline"};
 
 // Event pairs around individual launches (direct-launch profiling only).
 struct KernelTimer {
@@ -841,6 +844,7 @@ struct af_session {
     // persistent step kernel: layer table, digit images, barrier words
     DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
+    uint32_t clock_skip = 0;                     // profiling: plain launches before the timelines
     bool use_step = true;     // all layers of a step in one persistent launch
     uint32_t fail_phase = ~0u;  // AF_STEP_FAIL_PHASE: a step-kernel barrier that times out (tests)
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
@@ -1058,12 +1062,16 @@ struct af_session {
     hipError_t enqueue_step(bool with_head) {
         if (use_step) {
             StepArgs a = step_args(!with_head, nullptr);
-            if (timer && clock_used < clock_steps) {
+            int kind = K_LAYERS;
+            if (timer && clock_skip) {
+                --clock_skip;
+            } else if (timer && clock_used < clock_steps) {
                 a.clock = CLOCK.as<uint64_t>() + (size_t)clock_used++ * clock_words();
                 hipError_t e = hipMemsetAsync(a.clock, 0, clock_words() * 8, stream);  // profiling only
                 if (e != hipSuccess) return e;
+                kind = K_LAYERS_TL;
             }
-            hipError_t e = timed(K_LAYERS, layer_bytes(), [&] { return launch_step(a, group, step_grid, step_lds, stream); });
+            hipError_t e = timed(kind, layer_bytes(), [&] { return launch_step(a, group, step_grid, step_lds, stream); });
             if (e != hipSuccess || !with_head) return e;
             return timed(K_HEAD, (double)head.rows * (head.columns / 256) * 210.0 + 4.0 * 3.0 * hidden,
                          [&] { return launch_head(head_args(true, false), IN_RESID, head_blocks, stream); });
@@ -1579,13 +1587,16 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
             int r = dev_alloc(s->CLOCK, bytes, "step timeline");
             if (r) return r;
         }
-        s->clock_steps = max_new;
+        // the first half of the steps run plain ("layers"), the rest write the timeline
+        // ("layers_timeline" and the phase entries)
+        s->clock_steps = max_new - max_new / 2;
+        s->clock_skip = max_new / 2;
         s->clock_used = 0;
     }
     int rc = generate_core(s, prompt, n_prompt, nullptr, 0, max_new, nullptr, nullptr, ids_out, n_out, nullptr,
                            nullptr, &timer);
     const uint32_t timed_steps = s ? s->clock_used : 0;
-    if (s) s->clock_steps = 0;
+    if (s) s->clock_steps = s->clock_skip = 0;
     if (rc) return rc;
     for (int k = 0; k < K_KINDS; ++k) {
         std::memset(&timings[k], 0, sizeof(timings[k]));

@@ -1,25 +1,40 @@
-"""Batch-1 greedy decode benchmark on one MI355X.
+"""Batch-1 greedy decode benchmark on one MI355X, with the standalone
+operators of configs 0-3 measured beside it.
 
-Workload: a 48-layer Gemma-3-12B-shaped model with seeded random weights (hidden 3840,
-FFN 15360, 16 q / 8 kv heads of width 256, 5:1 local(window 1024):global layers, Q4_0
+Workload (the `value`): a 48-layer Gemma-3-12B-shaped model with seeded random weights (hidden
+3840, FFN 15360, 16 q / 8 kv heads of width 256, 5:1 local(window 1024):global layers, Q4_0
 projections, tied Q6_K embedding/lm-head over 262144 ids); a 128-token random prompt is
 prefilled, then W warm-up and K timed greedy decode steps run through
-GenerationSession::generate (per token: one persistent launch for all 48 layers, one launch
-for the Q6_K head + greedy argmax; ids come back through mapped host memory).
-A "step" is one decoded token; `value` is tokens per second over the K timed steps.
+GenerationSession::generate (per token: one persistent launch for all 48 layers, one launch for
+the Q6_K head + greedy argmax, replayed as one hipGraph; ids come back through mapped host
+memory).  A "step" is one decoded token; `value` is tokens per second over the K timed steps.
 
-After the timed region, a few more decode steps run with a hipEvent pair around every launch
-(af_session_profile) to time the dominant kernel (the layers kernel) for the roofline object,
-with its per-phase timeline from in-kernel timestamps.  The CPU baseline is the C oracle (a
-port of the reference's FP64 CPU path) timed on a bounded sample on this host.
+After the timed region, PROFILE_STEPS more decode steps run with a hipEvent pair around every
+launch on the session stream (af_session_profile): the first half launch the step kernel plainly
+(the roofline's average launch), the second half with its in-kernel phase timeline.
 
-    python bench.py [--gpus 1] [--steps 240] [--warmup 16]
+Configs 0-3 (`configs` in the JSON line): each operator launched through the C ABI on its own
+stream with a hipEvent pair around every launch, cycling through copies of its weights (or KV
+cache) that together exceed 1 GiB, so the 256 MB Infinity Cache cannot serve them.  The event
+pair brackets the dispatch too, so a few-microsecond kernel reads slower here than in the
+rocprofv3 kernel trace (profiles/).
+
+CPU baseline: the C oracle (a port of the reference's FP64 CPU path), on this host: config 4 on
+all of the box's CPU share (16 threads at most) and on one core, configs 0-3 in both modes.
+
+    python bench.py [--gpus 1] [--steps 240] [--warmup 16] [--no-cpu] [--no-configs]
 """
 import argparse
+import ctypes
 import json
 import os
+import platform
+import statistics
+import subprocess
 import sys
 import time
+
+import numpy as np
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -27,18 +42,234 @@ sys.path.insert(0, ROOT)
 METRIC = "batch-1 decode tok/s @12B-shape Q4_0; Q4_0 GEMV HBM GB/s vs 8 TB/s peak"
 PEAK_GBS = 8000.0
 PROMPT = 128
-PROFILE_STEPS = 8
+PROFILE_STEPS = 16
+ROTATE_BYTES = 1 << 30   # weight / KV copies cycled per configuration
+CPU_SHARE = 16           # host threads a one-GPU box grants
+HIDDEN, INTER, VOCAB = 3840, 15360, 262144
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(model, prompt, tokens, threads):
-    """The oracle (C port of the reference's FP64 CPU chain) decoding `tokens` tokens after a
-    one-token prefill: each token is 48 layers + final norm + Q6_K head + greedy."""
-    import numpy as np
+def cpu_model():
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                return line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return platform.processor() or "unknown"
 
+
+def host_threads():
+    return max(1, min(CPU_SHARE, os.cpu_count() or 1))
+
+
+# ---- GPU legs of configs 0-3 ---------------------------------------------------------------------
+
+def timed_launches(launch, n_copies, passes, stream):
+    """Per-launch milliseconds (hipEvent pair around each launch on `stream`), after one warm pass."""
+    from adaforge_amd import hip
+    for i in range(n_copies):
+        launch(i)
+    stream.synchronize()
+    pairs = []
+    for _ in range(passes):
+        for i in range(n_copies):
+            a, b = hip.Event(), hip.Event()
+            a.record(stream)
+            launch(i)
+            b.record(stream)
+            pairs.append((a, b))
+    stream.synchronize()
+    return [a.elapsed_ms(b) for a, b in pairs]
+
+
+def summary(ms, nbytes, copies, extra=None):
+    mean, med = statistics.fmean(ms), statistics.median(ms)
+    d = {"launches": len(ms), "copies": copies, "mean_us": round(1000 * mean, 2), "median_us": round(1000 * med, 2),
+         "algorithmic_bytes": int(nbytes), "gbs": round(nbytes / (med * 1e6), 1),
+         "frac": round(nbytes / (med * 1e6) / PEAK_GBS, 4)}
+    if extra:
+        d.update(extra)
+    return d
+
+
+def gpu_config0():
+    """Q4_0 GEMV 4096x3840 (af_q4_gemv), algorithmic bytes W + x + y."""
+    from adaforge_amd import _native as N, hip, synth
+    rows, cols = 4096, 3840
+    w = synth.q4("config0.W", cols, rows)
+    nbytes = w.size + 4 * (cols + rows)
+    copies = -(-ROTATE_BYTES // w.size)
+    hs = []
+    for _ in range(copies):
+        h = N.P()
+        N.check(N.lib().af_q4_upload(w.ctypes.data_as(N.u8p), w.size, cols, rows, ctypes.byref(h)))
+        hs.append(h)
+    x, y, s = hip.Buffer.from_numpy(synth.normal("config0.x", cols)), hip.Buffer(rows), hip.Stream()
+    try:
+        ms = timed_launches(lambda i: N.check(N.lib().af_q4_gemv(hs[i], x.ptr, y.ptr, s.handle)), copies, 3, s)
+    finally:
+        for h in hs:
+            N.lib().af_q4_free(h)
+    return summary(ms, nbytes, copies, {"kernel": "q4_gemv_kernel", "shape": [rows, cols]})
+
+
+def gpu_config1():
+    """FFN block 3840 -> 15360 -> 3840 (af_ffn_run: RMSNorm + gate/up + GELU, down + residual)."""
+    from adaforge_amd import _native as N, hip, synth
+    H, I = HIDDEN, INTER
+    pre = synth.normal("config1.norm", H, 1.0, 0.1)
+    gate, up, down = synth.q4("config1.gate", H, I), synth.q4("config1.up", H, I), synth.q4("config1.down", I, H)
+    weights = gate.size + up.size + down.size
+    nbytes = weights + 4 * (3 * H + 2 * I)  # + x, norm weights, y, and the activation written and read
+    copies = -(-ROTATE_BYTES // weights)
+    mk = lambda a, c, r: N.MatrixDesc(a.ctypes.data_as(N.u8p), a.size, c, r)
+    desc = N.FfnDesc(N.RmsNormDesc(pre.ctypes.data_as(N.f32p), H, 1e-6), mk(gate, H, I), mk(up, H, I),
+                     mk(down, I, H), N.RmsNormDesc(None, 0, 0.0), 1.0)
+    hs = []
+    for _ in range(copies):
+        h = N.P()
+        N.check(N.lib().af_ffn_create(ctypes.byref(desc), ctypes.byref(h)))
+        hs.append(h)
+    x, y, s = hip.Buffer.from_numpy(synth.normal("config1.x", H)), hip.Buffer(H), hip.Stream()
+    try:
+        ms = timed_launches(lambda i: N.check(N.lib().af_ffn_run(hs[i], x.ptr, y.ptr, s.handle)), copies, 3, s)
+    finally:
+        for h in hs:
+            N.lib().af_ffn_free(h)
+    return summary(ms, nbytes, copies, {"kernel": "q4_gemv_kernel x2 (gate/up + GELU, down + residual)",
+                                        "weights_bytes": weights})
+
+
+def gpu_config2():
+    """Q6_K head 262144x3840 + greedy argmax (af_q6_gemv_argmax): weights + x + logits."""
+    from adaforge_amd import _native as N, hip, synth
+    w = synth.q6("config2.head", HIDDEN, VOCAB)
+    nbytes = w.size + 4 * (HIDDEN + VOCAB)
+    copies = max(2, -(-ROTATE_BYTES // w.size))
+    hs = []
+    for _ in range(copies):
+        h = N.P()
+        N.check(N.lib().af_q6_upload(w.ctypes.data_as(N.u8p), w.size, HIDDEN, VOCAB, ctypes.byref(h)))
+        hs.append(h)
+    x, lg, res, s = (hip.Buffer.from_numpy(synth.normal("config2.x", HIDDEN)), hip.Buffer(VOCAB),
+                     hip.Buffer(2, np.uint32), hip.Stream())
+    try:
+        ms = timed_launches(lambda i: N.check(N.lib().af_q6_gemv_argmax(hs[i], x.ptr, lg.ptr, res.ptr, s.handle)),
+                            copies, 10, s)
+    finally:
+        for h in hs:
+            N.lib().af_q6_free(h)
+    return summary(ms, nbytes, copies, {"kernel": "q6_head_kernel", "shape": [VOCAB, HIDDEN]})
+
+
+def gpu_config3(ctx, kind):
+    """GQA decode attention (af_attention_decode) at position ctx - 1 over an fp16 KV cache of N(0,1)
+    values; algorithmic bytes = the visible K and V rows read."""
+    from adaforge_amd import _native as N, hip, synth
+    QH, KVH, D = 16, 8, 256
+    window = 1024 if kind == "local" else 0
+    ring = ctx
+    visible = min(ctx, window) if window else ctx
+    nbytes = visible * KVH * D * 2 * 2
+    cache_bytes = KVH * ring * D * 2
+    copies = max(2, min(256, -(-ROTATE_BYTES // (2 * cache_bytes))))
+    tag = f"bench.config3.{kind}.{ctx}"
+    kv = synth.normal(tag + ".kv", KVH * ring * D).astype(np.float16)
+    first = hip.Buffer.from_numpy(kv.view(np.uint16))
+    caches = []
+    for _ in range(copies):
+        kb, vb = hip.Buffer(KVH * ring * D, np.uint16), hip.Buffer(KVH * ring * D, np.uint16)
+        hip.ok(hip.rt().hipMemcpy(kb.ptr, first.ptr, cache_bytes, hip.D2D))
+        hip.ok(hip.rt().hipMemcpy(vb.ptr, first.ptr, cache_bytes, hip.D2D))
+        caches.append((kb, vb))
+    q = hip.Buffer.from_numpy(synth.normal(tag + ".q", QH * D))
+    k = hip.Buffer.from_numpy(synth.normal(tag + ".k", KVH * D))
+    v = hip.Buffer.from_numpy(synth.normal(tag + ".v", KVH * D))
+    qn = hip.Buffer.from_numpy(synth.normal("config3.qnorm", D, 1.0, 0.1))
+    kn = hip.Buffer.from_numpy(synth.normal("config3.knorm", D, 1.0, 0.1))
+    out, s = hip.Buffer(QH * D), hip.Stream()
+    factors = np.ones(D // 2, np.float32)
+    base = 1e4 if kind == "local" else 1e6
+    args = []
+    for kb, vb in caches:
+        args.append(N.AttentionArgs(q.ptr, k.ptr, v.ptr, qn.ptr, kn.ptr, 1e-6, 1e-6, 1e-6, 0,
+                                    N.RopeDesc(D, base, factors.ctypes.data_as(N.f32p), 131072),
+                                    N.AttentionConfigDesc(QH, KVH, D, window, 1.0 / 16.0), kb.ptr, vb.ptr, ring,
+                                    ctx - 1, out.ptr))
+    ms = timed_launches(lambda i: N.check(N.lib().af_attention_decode(ctypes.byref(args[i]), s.handle)), copies,
+                        max(2, 512 // copies), s)
+    del caches
+    return summary(ms, nbytes, copies, {"kernel": "attention_kernel", "ctx": ctx, "window": window or None})
+
+
+def gpu_configs():
+    out = {}
+    for name, fn in (("config0_q4_gemv", gpu_config0), ("config1_ffn", gpu_config1), ("config2_q6_head", gpu_config2)):
+        t = time.perf_counter()
+        out[name] = fn()
+        log(f"  {name}: median {out[name]['median_us']} us -> {out[name]['gbs']} GB/s "
+            f"({100 * out[name]['frac']:.1f} % of 8 TB/s) over {out[name]['copies']} copies "
+            f"[{time.perf_counter() - t:.1f}s]")
+    for ctx in (512, 4096, 32768):
+        for kind in ("global", "local"):
+            name = f"config3_attention_{kind}_{ctx}"
+            out[name] = gpu_config3(ctx, kind)
+            log(f"  {name}: median {out[name]['median_us']} us -> {out[name]['gbs']} GB/s")
+    return out
+
+
+# ---- CPU legs (the oracle: test infrastructure, timed here as the reference CPU path) --------------
+
+def median_time(fn, runs):
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return statistics.median(ts)
+
+
+def cpu_configs(threads):
+    """Configs 0-3 on the oracle, one core and `threads` cores (median of 5 runs each)."""
+    import oracle
+    from adaforge_amd import synth
+    out = {}
+    w0, x0 = synth.q4("config0.W", 3840, 4096), synth.normal("config0.x", 3840)
+    pre = synth.normal("config1.norm", HIDDEN, 1.0, 0.1)
+    g, u, d = synth.q4("config1.gate", HIDDEN, INTER), synth.q4("config1.up", HIDDEN, INTER), synth.q4(
+        "config1.down", INTER, HIDDEN)
+    x1 = synth.normal("config1.x", HIDDEN)
+    w2, x2 = synth.q6("config2.head", HIDDEN, VOCAB), synth.normal("config2.x", HIDDEN)
+    jobs = {
+        "config0_q4_gemv": lambda t: oracle.q4_matvec(w0, 3840, 4096, x0, threads=t),
+        "config1_ffn": lambda t: oracle.ffn(pre, 1e-6, g, u, d, HIDDEN, INTER, None, 1e-6, 1.0, x1, threads=t),
+        "config2_q6_head": lambda t: oracle.greedy(oracle.q6_matvec(w2, HIDDEN, VOCAB, x2, threads=t).astype(np.float32)),
+    }
+    for ctx in (512, 4096, 32768):
+        for kind in ("global", "local"):
+            rng = np.random.default_rng(ctx)
+            q = rng.standard_normal(16 * 256).astype(np.float32)
+            kv = rng.standard_normal(ctx * 8 * 256).astype(np.float16).astype(np.float32)
+            window = 1024 if kind == "local" else None
+            jobs[f"config3_attention_{kind}_{ctx}"] = (
+                lambda t, q=q, kv=kv, window=window, ctx=ctx:
+                oracle.attention(16, 8, 256, window, 1.0 / 16.0, q, kv, kv, ctx, ctx - 1, threads=t))
+    for name, fn in jobs.items():
+        one = median_time(lambda: fn(1), 5)
+        many = median_time(lambda: fn(threads), 5)
+        out[name] = {"one_core_ms": round(1000 * one, 3), "all_core_ms": round(1000 * many, 3), "cores": threads}
+        log(f"  cpu {name}: 1 core {1000 * one:.2f} ms, {threads} cores {1000 * many:.2f} ms")
+    return out
+
+
+def cpu_decode(model, prompt, tokens, threads):
+    """The oracle decoding `tokens` greedy tokens (48 layers + final norm + Q6_K head + greedy each)
+    after a one-token prefill; returns tokens/s."""
     import oracle
     ref = oracle.Model(model, capacity=tokens + 2, threads=threads)
     ref.step(int(prompt[0]))
@@ -50,6 +281,8 @@ def cpu_baseline(model, prompt, tokens, threads):
     ref.close()
     return tokens / dt, dt
 
+
+# ---- the headline: config 4 -------------------------------------------------------------------------
 
 def measured_traffic(kernel="void af::decode_step_kernel<2>(af::StepArgs)"):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
@@ -78,10 +311,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=16)
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", action="store_true", help="skip the configs 0-3 operator legs")
+    ap.add_argument("--configs-only", action="store_true", help="only the configs 0-3 GPU legs (profiling)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
-              f"(--gpus {a.gpus} is not supported; see DESIGN.md for how the path would shard)", file=sys.stderr)
+              f"(--gpus {a.gpus} is not supported; DESIGN.md describes how the path would shard)", file=sys.stderr)
         sys.exit(2)
     if a.steps < 1 or a.warmup < 1:
         sys.exit("--steps and --warmup must be >= 1")
@@ -89,15 +324,19 @@ def main():
     from adaforge_amd import synth
     from adaforge_amd.backend import HipDiagnostics
 
+    diag = HipDiagnostics()
+    dev = diag.check()
+    log(f"device {dev.device_name} {dev.arch} CUs={dev.compute_units}")
+    if a.configs_only:
+        print(json.dumps(gpu_configs()), flush=True)
+        return
+
     t = time.perf_counter()
     model = synth.model()
     log(f"model generated in {time.perf_counter() - t:.1f}s")
     prompt = [int(i) for i in synth.prompt_ids(PROMPT, model.vocabulary, name="config4.prompt")]
     stop = [model.vocabulary - 1]
     capacity = PROMPT + a.warmup + a.steps + PROFILE_STEPS + 2
-    diag = HipDiagnostics()
-    dev = diag.check()
-    log(f"device {dev.device_name} {dev.arch} CUs={dev.compute_units}")
     t = time.perf_counter()
     session = diag.open_session(model, capacity)
     log(f"session open (weight upload) in {time.perf_counter() - t:.1f}s")
@@ -123,17 +362,19 @@ def main():
 
     _, timings = session.profile(cached, PROFILE_STEPS)
     session.close()
-    # dominant kernel: the persistent step kernel (all 48 layers of one token), timed with a
-    # hipEvent pair around every launch on the session stream
+    # dominant kernel: the persistent step kernel (all 48 layers of one token), plain launches timed
+    # with a hipEvent pair around each on the session stream
     n, ms, b = timings["layers"]
     avg_ms = ms / n
     kv_bytes = kv_read_bytes(model, len(cached))
     step_bytes = b + kv_bytes
     achieved = step_bytes / (avg_ms * 1e6)
+    tn, tms, _ = timings["layers_timeline"]
     hn, hms, hb = timings["head"]
     per_token_bytes = step_bytes + hb
-    log(f"  layers kernel: {n} launches, avg {1000 * avg_ms:.1f} us, {step_bytes / 1e9:.3f} GB "
-        f"(weights {b / 1e9:.3f} + KV {kv_bytes / 1e6:.1f} MB) -> {achieved:.0f} GB/s")
+    log(f"  layers kernel: {n} plain launches, avg {1000 * avg_ms:.1f} us, {step_bytes / 1e9:.3f} GB "
+        f"(weights {b / 1e9:.3f} + KV {kv_bytes / 1e6:.1f} MB) -> {achieved:.0f} GB/s; "
+        f"{tn} launches with the timeline avg {1000 * tms / max(tn, 1):.1f} us")
     log(f"  head kernel:   {hn} launches, avg {1000 * hms / hn:.1f} us, {hb / 1e6:.1f} MB -> "
         f"{hb / (hms / hn * 1e6):.0f} GB/s")
     for name in ("qkv", "attention", "o_proj", "gate_up", "down", "barrier"):
@@ -147,15 +388,28 @@ def main():
     log(f"algorithmic bytes per token {per_token_bytes / 1e9:.3f} GB -> roofline {PEAK_GBS * 1e9 / per_token_bytes:.0f} "
         f"tok/s at 8 TB/s; measured {tok_s:.1f} tok/s = {tok_s * per_token_bytes / (PEAK_GBS * 1e9):.3f} of it")
 
+    configs = None
+    if not a.no_configs:
+        configs = gpu_configs()
+
     cpu = None
     if not a.no_cpu:
-        threads = max(1, min(16, os.cpu_count() or 1))
-        cv, cdt = cpu_baseline(model, prompt, a.cpu_tokens, threads)
+        threads = host_threads()
+        model_name, nproc = cpu_model(), os.cpu_count()
+        cv, cdt = cpu_decode(model, prompt, a.cpu_tokens, threads)
+        log(f"cpu baseline: {cv:.3f} tok/s on {threads} threads ({cdt:.1f} s)")
+        c1, c1dt = cpu_decode(model, prompt, 1, 1)
+        log(f"cpu baseline, one core: {c1:.4f} tok/s ({c1dt:.1f} s)")
         cpu = {"value": round(cv, 4), "unit": "tok/s", "cores": threads, "kind": "port",
                "sample": f"C oracle (FP64-accumulation port of the reference CPU path), full 48-layer model: "
                          f"{a.cpu_tokens} greedy decode tokens (layers + Q6_K head + argmax) after a 1-token "
-                         f"prefill, {cdt:.1f} s on {threads} threads"}
-        log(f"cpu baseline: {cv:.3f} tok/s on {threads} threads ({cdt:.1f} s)")
+                         f"prefill, {cdt:.1f} s on {threads} threads (rows split across threads, per-row order "
+                         f"unchanged)",
+               "one_core": {"value": round(c1, 5), "unit": "tok/s", "cores": 1,
+                            "sample": f"1 greedy decode token after a 1-token prefill, {c1dt:.1f} s on one thread"},
+               "nproc": nproc, "cpu_model": model_name}
+        if configs is not None:
+            cpu["configs"] = cpu_configs(threads)
 
     line = {
         "metric": METRIC,
@@ -173,15 +427,17 @@ def main():
         "config": {
             "workload": "config4: 48-layer Gemma-3-12B-shaped decode loop, Q4_0 projections + tied Q6_K "
                         "embedding/lm-head (vocab 262144), 128-token prompt prefill then greedy decode steps "
-                        "(one persistent launch for the 48 layers + one head launch per token), fp16 KV cache",
+                        "(one persistent launch for the 48 layers + one head launch per token, replayed as a "
+                        "hipGraph), fp16 KV cache",
             "hidden": 3840, "intermediate": 15360, "layers": 48, "q_heads": 16, "kv_heads": 8, "head_width": 256,
             "prompt_tokens": PROMPT, "decode_tokens": a.warmup + produced, "batch": 1,
             "algorithmic_bytes_per_token": round(per_token_bytes),
+            "tok_s_roofline_frac": round(tok_s * per_token_bytes / (PEAK_GBS * 1e9), 4),
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "decode_step_kernel: all 48 layers of one token in one cooperative launch (Q4_0 "
-                      "GEMVs on int8 MFMA, fused norms, GQA attention over fp16 KV)",
+            "kernel": "decode_step_kernel: all 48 layers of one token in one persistent launch of one "
+                      "workgroup per CU (Q4_0 GEMVs on int8 MFMA, fused norms, GQA attention over fp16 KV)",
             "achieved": round(achieved, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
@@ -192,7 +448,9 @@ def main():
             "avg_us": round(1000.0 * avg_ms, 2),
             "bytes_per_launch": round(step_bytes),
             "launches": n,
+            "timeline_avg_us": round(1000.0 * tms / max(tn, 1), 2),
         },
+        "configs": configs,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -240,10 +240,12 @@ void af_session_close(af_session* s);
 /* Per-kernel decode timing, the event-based ADAFORGE_TIMING_DECODE diagnostic
  * (crates/cuda-backend/src/stack.rs:1245-1251, 1340-1372) at kernel granularity: behaves as
  * af_session_generate without stop ids, but launches every step's kernels directly with a
- * hipEvent pair around each launch on the session stream.  timings[] holds one entry per kind:
- * "layers" (the persistent step kernel) and "head" from the events; the step kernel's phases
- * "qkv", "attention", "o_proj", "gate_up", "down" and "barrier" from its in-kernel timeline
- * (one launch = one layer); then "<phase>.<mark>" entries splitting the slowest workgroup's
+ * hipEvent pair around each launch on the session stream.  The first max_new / 2 steps launch the
+ * persistent step kernel plainly, the others with its in-kernel timeline on.  timings[] holds one
+ * entry per kind: "layers" (plain launches of the step kernel), "layers_timeline" (the launches
+ * that write the timeline) and "head" from the events; the step kernel's phases "qkv",
+ * "attention", "o_proj", "gate_up", "down" and "barrier" from the timeline (one launch = one
+ * layer); then "<phase>.<mark>" entries splitting the slowest workgroup's
  * phase at its marks and "<phase>.mean" (mean workgroup time).  bytes_per_launch is the
  * algorithmic HBM traffic (weights read) averaged over launches; n_timings <= capacity. */
 typedef struct {

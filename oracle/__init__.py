@@ -41,6 +41,7 @@ def _load():
         "or_attention_validate": (i32, [u32, u32, u32, u32, f32]),
         "or_visible_range": (i32, [u32, u32, u32, P, P]),
         "or_attention": (i32, [u32, u32, u32, u32, f32, P, P, P, u32, u32, P]),
+        "or_attention_mt": (i32, [u32, u32, u32, u32, f32, P, P, P, u32, u32, P, i32]),
         "or_attention_output": (i32, [P, u32, u32, P, f32, P, P, P, i32]),
         "or_gelu_tanh": (f64, [f64]),
         "or_ffn": (i32, [P, f32, P, P, P, u32, u32, P, f32, f32, P, P, i32]),
@@ -162,14 +163,15 @@ def visible_range(window, tokens, position):
     return s.value, e.value
 
 
-def attention(q_heads, kv_heads, width, window, scale, q, keys, values, tokens, position):
-    """crates/domain/src/attention.rs:66-111 -> float64[q_heads*width]; window None/0 = global."""
+def attention(q_heads, kv_heads, width, window, scale, q, keys, values, tokens, position, threads=1):
+    """crates/domain/src/attention.rs:66-111 -> float64[q_heads*width]; window None/0 = global.
+    With threads > 1 the query heads run on separate threads (bit-identical output)."""
     q, k, v = _f32(q), _f32(keys), _f32(values)
     if q.size != q_heads * width or k.size != tokens * kv_heads * width or v.size != k.size:
         raise OracleError("attention layout")
     out = np.empty(q.size, dtype=np.float64)
-    _check(_lib.or_attention(q_heads, kv_heads, width, window or 0, float(scale), _p(q), _p(k), _p(v), tokens,
-                             position, _p(out)), "attention rejected")
+    _check(_lib.or_attention_mt(q_heads, kv_heads, width, window or 0, float(scale), _p(q), _p(k), _p(v), tokens,
+                                position, _p(out), int(threads)), "attention rejected")
     return out
 
 

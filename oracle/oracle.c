@@ -319,8 +319,64 @@ int or_visible_range(uint32_t window, uint32_t tokens, uint32_t position, uint32
 }
 
 /* crates/domain/src/attention.rs:66-111: FP64 scores * scale, max-subtracted exp, normalise, sum p*v. */
-int or_attention(uint32_t q_heads, uint32_t kv_heads, uint32_t width, uint32_t window, float scale, const float* q,
-                 const float* keys, const float* values, uint32_t tokens, uint32_t position, double* out) {
+/* One query head of or_attention (the loop body of attention.rs:66-111): scores in f64, the
+ * max-subtracted exponentials, then sum_t p_t / denominator * v_t, in token order. */
+typedef struct {
+    uint32_t group, width;
+    float scale;
+    const float *q, *keys, *values;
+    size_t start, n, stride;
+    double* out;
+} attn_job;
+
+static void attention_head(const attn_job* a, uint32_t head, double* scores) {
+    uint32_t kv = head / a->group;
+    const float* query = a->q + (size_t)head * a->width;
+    double max = -INFINITY;
+    for (size_t t = 0; t < a->n; ++t) {
+        const float* key = a->keys + (a->start + t) * a->stride + (size_t)kv * a->width;
+        double s = 0.0;
+        for (uint32_t c = 0; c < a->width; ++c) s += (double)query[c] * (double)key[c];
+        s *= (double)a->scale;
+        scores[t] = s;
+        max = fmax(max, s);
+    }
+    double denominator = 0.0;
+    for (size_t t = 0; t < a->n; ++t) {
+        scores[t] = exp(scores[t] - max);
+        denominator += scores[t];
+    }
+    double* o = a->out + (size_t)head * a->width;
+    for (size_t t = 0; t < a->n; ++t) {
+        const float* value = a->values + (a->start + t) * a->stride + (size_t)kv * a->width;
+        double p = scores[t];
+        for (uint32_t c = 0; c < a->width; ++c) o[c] += p / denominator * (double)value[c];
+    }
+}
+
+typedef struct {
+    const attn_job* a;
+    uint32_t begin, end;
+    int failed;
+} attn_part;
+
+static void* attention_worker(void* p) {
+    attn_part* w = (attn_part*)p;
+    double* scores = (double*)malloc((w->a->n ? w->a->n : 1) * sizeof(double));
+    if (!scores) {
+        w->failed = 1;
+        return NULL;
+    }
+    for (uint32_t h = w->begin; h < w->end; ++h) attention_head(w->a, h, scores);
+    free(scores);
+    return NULL;
+}
+
+/* crates/domain/src/attention.rs:66-111.  With threads > 1 the query heads are split across
+ * threads; each head runs the same loops, so the output is bit-identical to threads = 1. */
+int or_attention_mt(uint32_t q_heads, uint32_t kv_heads, uint32_t width, uint32_t window, float scale, const float* q,
+                    const float* keys, const float* values, uint32_t tokens, uint32_t position, double* out,
+                    int threads) {
     if (or_attention_validate(q_heads, kv_heads, width, window, scale) != OR_OK) return OR_ERR;
     uint32_t start, end;
     if (or_visible_range(window, tokens, position, &start, &end) != OR_OK) return OR_ERR;
@@ -329,37 +385,33 @@ int or_attention(uint32_t q_heads, uint32_t kv_heads, uint32_t width, uint32_t w
         if (!finite_f(q[i])) return OR_ERR;
     for (size_t i = 0; i < (size_t)tokens * stride; ++i)
         if (!finite_f(keys[i]) || !finite_f(values[i])) return OR_ERR;
-    size_t n = end - start;
-    double* scores = (double*)malloc(n * sizeof(double));
-    if (!scores) return OR_ERR;
     memset(out, 0, sizeof(double) * (size_t)q_heads * width);
-    uint32_t group = q_heads / kv_heads;
-    for (uint32_t head = 0; head < q_heads; ++head) {
-        uint32_t kv = head / group;
-        const float* query = q + (size_t)head * width;
-        double max = -INFINITY;
-        for (size_t t = 0; t < n; ++t) {
-            const float* key = keys + (start + t) * stride + (size_t)kv * width;
-            double s = 0.0;
-            for (uint32_t c = 0; c < width; ++c) s += (double)query[c] * (double)key[c];
-            s *= (double)scale;
-            scores[t] = s;
-            max = fmax(max, s);
+    attn_job a = {q_heads / kv_heads, width, scale, q, keys, values, start, end - start, stride, out};
+    if (threads < 1) threads = 1;
+    if ((uint32_t)threads > q_heads) threads = (int)q_heads;
+    if (threads > 64) threads = 64;
+    pthread_t tid[64];
+    attn_part parts[64];
+    uint32_t per = (q_heads + (uint32_t)threads - 1) / (uint32_t)threads;
+    int n = 0, failed = 0;
+    for (int t = 0; t < threads; ++t) {
+        uint32_t b = (uint32_t)t * per, e = b + per > q_heads ? q_heads : b + per;
+        if (b >= e) break;
+        parts[t] = (attn_part){&a, b, e, 0};
+        if (threads == 1 || pthread_create(&tid[n], NULL, attention_worker, &parts[t]) != 0) {
+            attention_worker(&parts[t]); /* this thread: same order, same bits */
+            continue;
         }
-        double denominator = 0.0;
-        for (size_t t = 0; t < n; ++t) {
-            scores[t] = exp(scores[t] - max);
-            denominator += scores[t];
-        }
-        double* o = out + (size_t)head * width;
-        for (size_t t = 0; t < n; ++t) {
-            const float* value = values + (start + t) * stride + (size_t)kv * width;
-            double p = scores[t];
-            for (uint32_t c = 0; c < width; ++c) o[c] += p / denominator * (double)value[c];
-        }
+        ++n;
     }
-    free(scores);
-    return OR_OK;
+    for (int t = 0; t < n; ++t) pthread_join(tid[t], NULL);
+    for (int t = 0; t < threads && (uint32_t)t * per < q_heads; ++t) failed |= parts[t].failed;
+    return failed ? OR_ERR : OR_OK;
+}
+
+int or_attention(uint32_t q_heads, uint32_t kv_heads, uint32_t width, uint32_t window, float scale, const float* q,
+                 const float* keys, const float* values, uint32_t tokens, uint32_t position, double* out) {
+    return or_attention_mt(q_heads, kv_heads, width, window, scale, q, keys, values, tokens, position, out, 1);
 }
 
 /* ---- output branch and FFN ----------------------------------------------------------- */

@@ -49,6 +49,10 @@ int or_attention_validate(uint32_t q_heads, uint32_t kv_heads, uint32_t width, u
 int or_visible_range(uint32_t window, uint32_t tokens, uint32_t position, uint32_t* start, uint32_t* end);
 int or_attention(uint32_t q_heads, uint32_t kv_heads, uint32_t width, uint32_t window, float scale, const float* q,
                  const float* keys, const float* values, uint32_t tokens, uint32_t position, double* out);
+/* or_attention with the query heads split over `threads` threads (bit-identical results). */
+int or_attention_mt(uint32_t q_heads, uint32_t kv_heads, uint32_t width, uint32_t window, float scale, const float* q,
+                    const float* keys, const float* values, uint32_t tokens, uint32_t position, double* out,
+                    int threads);
 
 int or_attention_output(const uint8_t* o_bytes, uint32_t o_cols, uint32_t o_rows, const float* norm_w, float norm_eps,
                         const float* attention, const float* residual, double* out, int threads);
