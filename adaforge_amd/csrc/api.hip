@@ -355,6 +355,8 @@ float median_of(std::vector<float> t) {
 struct Scratch {
     std::mutex mu;
     DevMem head_partial, head_counter, attn_part, attn_counters;
+    DevMem attn_freq;                   // the last RoPE inverse frequencies of af_attention_decode
+    std::vector<double> attn_freq_host; // their host copy (re-uploaded only when they change)
 };
 Scratch g_scratch;
 
@@ -714,10 +716,16 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     if ((rc = grow(g_scratch.attn_counters, (size_t)std::max<uint32_t>(64, p->config.kv_heads) * 4, true,
                    "attention counters")))
         return rc;
-    // inverse frequencies: uploaded per call (the standalone entry point is a diagnostic)
+    // inverse frequencies: kept on the device and re-uploaded only when the RoPE parameters change
+    // (after the device drains, so no launch still reads the old ones); repeated calls with the
+    // same parameters enqueue one kernel and nothing else
     std::vector<double> f = inverse_frequencies(p->rope);
-    DevMem freq;
-    if ((rc = dev_upload(freq, f.data(), f.size() * 8, "RoPE frequencies"))) return rc;
+    if (f != g_scratch.attn_freq_host) {
+        HIP_OK(hipDeviceSynchronize(), "attention frequencies");
+        if ((rc = grow(g_scratch.attn_freq, f.size() * 8, false, "RoPE frequencies"))) return rc;
+        HIP_OK(hipMemcpy(g_scratch.attn_freq.p, f.data(), f.size() * 8, hipMemcpyHostToDevice), "RoPE frequencies");
+        g_scratch.attn_freq_host = f;
+    }
     AttnArgs a{};
     a.q_raw = p->q;
     a.k_raw = p->k;
@@ -728,7 +736,7 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     a.k_eps = p->k_eps;
     a.v_eps = p->v_eps;
     a.v_norm = p->v_norm;
-    a.inv_freq = freq.as<double>();
+    a.inv_freq = g_scratch.attn_freq.as<double>();
     a.kcache = p->k_cache;
     a.vcache = p->v_cache;
     a.ring = p->ring;
@@ -742,7 +750,6 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     a.min_chunk = kAttnMinChunk;
     a.kv_heads = p->config.kv_heads;
     HIP_OK(launch_attention(a, group, D, (hipStream_t)stream), "attention launch");
-    HIP_OK(hipStreamSynchronize((hipStream_t)stream), "attention");  // freq is freed on return
     return AF_OK;
 }
 

@@ -36,6 +36,12 @@ def rt():
         h.hipGetErrorString.restype = ctypes.c_char_p
         h.hipGetErrorString.argtypes = [i32]
         h.hipGetDeviceCount.argtypes = [ctypes.POINTER(i32)]
+        h.hipStreamBeginCapture.argtypes = [P, i32]
+        h.hipStreamEndCapture.argtypes = [P, ctypes.POINTER(P)]
+        h.hipGraphInstantiate.argtypes = [ctypes.POINTER(P), P, P, P, sz]
+        h.hipGraphLaunch.argtypes = [P, P]
+        h.hipGraphExecDestroy.argtypes = [P]
+        h.hipGraphDestroy.argtypes = [P]
         _hip = h
     return _hip
 
@@ -136,5 +142,33 @@ class Event:
         try:
             if self.handle:
                 rt().hipEventDestroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """The launches `enqueue()` makes on `stream`, captured once (stream capture, thread-local mode)
+    and replayed with launch()."""
+
+    def __init__(self, stream, enqueue):
+        g, x = ctypes.c_void_p(), ctypes.c_void_p()
+        ok(rt().hipStreamBeginCapture(stream.handle, 1))
+        try:
+            enqueue()
+        finally:
+            ok(rt().hipStreamEndCapture(stream.handle, ctypes.byref(g)))
+        self.graph = g.value
+        ok(rt().hipGraphInstantiate(ctypes.byref(x), self.graph, None, None, 0))
+        self.exec = x.value
+
+    def launch(self, stream):
+        ok(rt().hipGraphLaunch(self.exec, stream.handle))
+
+    def __del__(self):
+        try:
+            if self.exec:
+                rt().hipGraphExecDestroy(self.exec)
+            if self.graph:
+                rt().hipGraphDestroy(self.graph)
         except Exception:
             pass

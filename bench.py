@@ -13,11 +13,11 @@ After the timed region, PROFILE_STEPS more decode steps run with a hipEvent pair
 launch on the session stream (af_session_profile): the first half launch the step kernel plainly
 (the roofline's average launch), the second half with its in-kernel phase timeline.
 
-Configs 0-3 (`configs` in the JSON line): each operator launched through the C ABI on its own
-stream with a hipEvent pair around every launch, cycling through copies of its weights (or KV
-cache) that together exceed 1 GiB, so the 256 MB Infinity Cache cannot serve them.  The event
-pair brackets the dispatch too, so a few-microsecond kernel reads slower here than in the
-rocprofv3 kernel trace (profiles/).
+Configs 0-3 (`configs` in the JSON line): each operator launched through the C ABI, cycling
+through copies of its weights (or KV cache) that together exceed 1 GiB, so the 256 MB Infinity
+Cache cannot serve them; one pass over the copies is captured as a hipGraph and replayed between
+a hipEvent pair, so the per-launch time includes the gaps between graph nodes (a few-microsecond
+kernel reads slower here than in the rocprofv3 kernel trace under profiles/).
 
 CPU baseline: the C oracle (a port of the reference's FP64 CPU path), on this host: config 4 on
 all of the box's CPU share (16 threads at most) and on one core, configs 0-3 in both modes.
@@ -70,26 +70,32 @@ def host_threads():
 # ---- GPU legs of configs 0-3 ---------------------------------------------------------------------
 
 def timed_launches(launch, n_copies, passes, stream):
-    """Per-launch milliseconds (hipEvent pair around each launch on `stream`), after one warm pass."""
+    """Per-launch milliseconds of `launch(i)` over the weight copies i < n_copies: the n_copies
+    launches are captured in one hipGraph, replayed `passes` times between a hipEvent pair on
+    `stream`, and the elapsed time is split evenly over the launches (so it includes the gaps
+    between graph nodes, not the host's dispatch).  One warm pass runs first (it also allocates
+    any scratch the entry points grow on first use, which a capture must not do)."""
     from adaforge_amd import hip
     for i in range(n_copies):
         launch(i)
     stream.synchronize()
-    pairs = []
-    for _ in range(passes):
-        for i in range(n_copies):
-            a, b = hip.Event(), hip.Event()
-            a.record(stream)
-            launch(i)
-            b.record(stream)
-            pairs.append((a, b))
+    g = hip.Graph(stream, lambda: [launch(i) for i in range(n_copies)])
+    g.launch(stream)
     stream.synchronize()
-    return [a.elapsed_ms(b) for a, b in pairs]
+    out = []
+    for _ in range(passes):
+        a, b = hip.Event(), hip.Event()
+        a.record(stream)
+        g.launch(stream)
+        b.record(stream)
+        stream.synchronize()
+        out.append(a.elapsed_ms(b) / n_copies)
+    return out
 
 
 def summary(ms, nbytes, copies, extra=None):
     mean, med = statistics.fmean(ms), statistics.median(ms)
-    d = {"launches": len(ms), "copies": copies, "mean_us": round(1000 * mean, 2), "median_us": round(1000 * med, 2),
+    d = {"passes": len(ms), "copies": copies, "mean_us": round(1000 * mean, 2), "median_us": round(1000 * med, 2),
          "algorithmic_bytes": int(nbytes), "gbs": round(nbytes / (med * 1e6), 1),
          "frac": round(nbytes / (med * 1e6) / PEAK_GBS, 4)}
     if extra:
@@ -111,7 +117,7 @@ def gpu_config0():
         hs.append(h)
     x, y, s = hip.Buffer.from_numpy(synth.normal("config0.x", cols)), hip.Buffer(rows), hip.Stream()
     try:
-        ms = timed_launches(lambda i: N.check(N.lib().af_q4_gemv(hs[i], x.ptr, y.ptr, s.handle)), copies, 3, s)
+        ms = timed_launches(lambda i: N.check(N.lib().af_q4_gemv(hs[i], x.ptr, y.ptr, s.handle)), copies, 5, s)
     finally:
         for h in hs:
             N.lib().af_q4_free(h)
@@ -137,7 +143,7 @@ def gpu_config1():
         hs.append(h)
     x, y, s = hip.Buffer.from_numpy(synth.normal("config1.x", H)), hip.Buffer(H), hip.Stream()
     try:
-        ms = timed_launches(lambda i: N.check(N.lib().af_ffn_run(hs[i], x.ptr, y.ptr, s.handle)), copies, 3, s)
+        ms = timed_launches(lambda i: N.check(N.lib().af_ffn_run(hs[i], x.ptr, y.ptr, s.handle)), copies, 10, s)
     finally:
         for h in hs:
             N.lib().af_ffn_free(h)
@@ -160,7 +166,7 @@ def gpu_config2():
                      hip.Buffer(2, np.uint32), hip.Stream())
     try:
         ms = timed_launches(lambda i: N.check(N.lib().af_q6_gemv_argmax(hs[i], x.ptr, lg.ptr, res.ptr, s.handle)),
-                            copies, 10, s)
+                            copies, 20, s)
     finally:
         for h in hs:
             N.lib().af_q6_free(h)
@@ -202,7 +208,7 @@ def gpu_config3(ctx, kind):
                                     N.AttentionConfigDesc(QH, KVH, D, window, 1.0 / 16.0), kb.ptr, vb.ptr, ring,
                                     ctx - 1, out.ptr))
     ms = timed_launches(lambda i: N.check(N.lib().af_attention_decode(ctypes.byref(args[i]), s.handle)), copies,
-                        max(2, 512 // copies), s)
+                        max(3, 512 // copies), s)
     del caches
     return summary(ms, nbytes, copies, {"kernel": "attention_kernel", "ctx": ctx, "window": window or None})
 

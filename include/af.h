@@ -163,7 +163,9 @@ int af_ffn_run(af_ffn* f, const float* x, float* y, void* stream);
  * crates/cuda-backend/src/attention.rs:107-170, stack.rs:332-497): per-head RMSNorm and
  * NeoX RoPE of q and k at `position`, optional unit-weight RMSNorm of v, K/V rounded to
  * fp16 and appended at slot position % ring of the caches ([kv_heads][ring][width] fp16,
- * device), then softmax(scale q.k) v over [max(0, position + 1 - window), position]. */
+ * device), then softmax(scale q.k) v over [max(0, position + 1 - window), position].  Calls share
+ * the library's split-K scratch: calls on different streams must not overlap.  A call whose RoPE
+ * parameters differ from the previous call's waits for the device before it uploads them. */
 typedef struct {
     const float* q;      /* device [q_heads][width], raw projection outputs */
     const float* k;      /* device [kv_heads][width] */
