@@ -235,6 +235,7 @@ __device__ __forceinline__ BlockTab block_tab(float m, float sum) {
 // in flight while this one finishes and during the boundary and prologue in between.  Slot
 // `slot` holds the next record to consume.
 static_assert(kRing * kStepRecord <= kStepStreamPad, "stream padding below the ring's over-read");
+
 struct Ring {
     v4u code[kRing];
     uint32_t scale[kRing];
@@ -253,6 +254,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ring_rsrc(const Ring& r) {
                        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane(r.base_lo);
     return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(p), 0, (int)__builtin_amdgcn_readfirstlane(r.len),
                                              0x00020000);
+}
+
+// Records a streaming wave of a workgroup without an attention item pulls through the caches during
+// the attention phase: those after its ring, i.e. the rest of o-proj and most of gate/up.  The
+// copies land in a 1 KB LDS slot that nothing reads (a DMA needs an LDS destination and no
+// registers); what matters is that the bytes then sit in L2 and the Infinity Cache, so the wave's
+// own ring loads of them later return at cache latency while HBM would otherwise idle.
+constexpr uint32_t kPrefetchRecords = 32;
+static_assert((kRing + kPrefetchRecords) * kStepRecord <= kStepStreamPad, "stream padding below the prefetch");
+
+__device__ __forceinline__ void prefetch_records(const Ring& r, uint8_t* sink, uint32_t lane) {
+    const uint64_t base = ((uint64_t)r.base_hi << 32) | r.base_lo;
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(base) + r.soff;
+    for (uint32_t i = 0; i < kPrefetchRecords * kStepRecord; i += 1024)
+        __builtin_amdgcn_global_load_lds(src + i + lane * 16, (lds_ptr)sink, 16, 0, 0);
 }
 
 __device__ __forceinline__ void ring_fill(Ring& r, const __amdgpu_buffer_rsrc_t& rs, int u, uint32_t lane) {
@@ -1263,6 +1279,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     __shared__ int ok_flag, att_flag, poll_bad;
     __shared__ uint32_t done_cnt;  // streaming waves done with a GEMV phase, 64 per wave
     __shared__ float act_l[kMaxUnits][32];
+    __shared__ __align__(16) uint8_t pf_sink[1024];  // prefetch_records' destination, never read
 
     if (a.state[ST_STOP]) return;  // uniform: written only before the launch
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -1318,6 +1335,8 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             if (item < ag.items)
                 attention_item<GQ>(L, a, pos, item / ag.chunks, item % ag.chunks, ag.chunks, ag.cmax, ag.clen, ag.start,
                                    tag0 + l, lds, &att_flag, &poll_bad, g);
+            else if (wave != 0)
+                prefetch_records(r, pf_sink, lane);  // waited for in the o-proj stage (poll_image)
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(poll_bad)) {
                 failed = true;
