@@ -217,7 +217,28 @@ struct StepArgs {
     uint32_t fail_phase;            // a phase whose opening grid barrier waits for one arrival too
                                     // many, so that it ends in the barrier's own time-out (a host-set
                                     // test of the fall-back path); ~0u: none
+    uint32_t xcd_local;             // 1: head group h's qkv rows, attention items and chunk partials all
+                                    // live on XCD h (workgroups b with b % 8 == h) and are exchanged
+                                    // through that XCD's L2 (step_qkv_tile, step_attn_chunk)
 };
+
+// XCD-local layout (StepArgs::xcd_local): eight KV heads of two query heads each, a 256-workgroup
+// grid whose workgroup b runs on XCD b % 8 (verified at session open by step_xcd_map).  Head group
+// h = b % 8 owns 64 qkv tiles (its two query heads' 32, its K head's 16, its V head's 16), two per
+// workgroup of rank r = b / 8; its attention chunk c runs on workgroup 8 (31 - c) + h.
+constexpr uint32_t kXcds = 8;
+
+// Row tile of qkv unit k (0 or 1) of workgroup b: b + k grid, or in the XCD-local layout the head
+// group's tile 2 r + k (qn_tiles = query rows / 16, kn_tiles = key rows / 16).
+__host__ __device__ inline uint32_t step_qkv_tile(uint32_t b, uint32_t k, uint32_t grid, uint32_t xl, uint32_t qn_tiles,
+                                                  uint32_t kn_tiles) {
+    if (!xl) return b + k * grid;
+    const uint32_t h = b % kXcds, j = 2 * (b / kXcds) + k;
+    const uint32_t gq = qn_tiles / kXcds, gk = kn_tiles / kXcds;  // tiles per head group
+    if (j < gq) return h * gq + j;
+    if (j < gq + gk) return qn_tiles + h * gk + (j - gq);
+    return qn_tiles + kn_tiles + h * gk + (j - gq - gk);
+}
 
 // Timeline marks of a phase (workgroup's thread 0): start (barrier departure or kernel start),
 // inputs staged, digit image built, weights streamed, outputs stored, arrival at the closing
@@ -267,7 +288,10 @@ uint32_t step_merge_chunks(uint32_t group, size_t lds);  // chunk partials one m
 hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid);
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s);
 // Fills the weight stream (StepArgs::stream at stream_off) from the layers' tiled Q4View matrices.
-hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint32_t grid, uint8_t* stream,
-                                const uint64_t* stream_off, hipStream_t s);
+hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint32_t grid, uint32_t xcd_local,
+                                uint8_t* stream, const uint64_t* stream_off, hipStream_t s);
+// The XCD each workgroup of a `grid`-workgroup launch runs on (hardware register XCC_ID), one word
+// per workgroup into xcc (device memory).
+hipError_t step_xcd_map(uint32_t grid, uint32_t* xcc, hipStream_t s);
 
 }  // namespace af

@@ -854,6 +854,7 @@ struct af_session {
     uint32_t clock_skip = 0;                     // profiling: plain launches before the timelines
     bool use_step = true;     // all layers of a step in one persistent launch
     uint32_t fail_phase = ~0u;  // AF_STEP_FAIL_PHASE: a step-kernel barrier that times out (tests)
+    bool xcd_local = false;     // the step kernel's XCD-local layout (setup_step)
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
     size_t step_lds = 0;
     uint32_t max_kv_rows = 0;
@@ -1053,6 +1054,7 @@ struct af_session {
         a.advance = advance ? 1u : 0u;
         a.snap = snap;
         a.fail_phase = fail_phase;
+        a.xcd_local = xcd_local ? 1u : 0u;
         return a;
     }
 
@@ -1191,6 +1193,24 @@ int setup_step(af_session& s) {
     s.step_cmax = cm;
     s.group = group;
     s.step_lds = lds;
+    int rc;
+    // XCD-local layout (StepArgs::xcd_local): BASELINE's attention geometry (8 KV heads of two query
+    // heads, width 256, separate V) on a 256-workgroup grid whose workgroup b runs on XCD b % 8,
+    // which a probe launch checks on this device; AF_STEP_XCD_LOCAL=0 turns it off.
+    bool xl = grid == 256 && group == 2 && !(std::getenv("AF_STEP_XCD_LOCAL") &&
+                                              std::strcmp(std::getenv("AF_STEP_XCD_LOCAL"), "0") == 0);
+    for (const LayerDev& L : s.layers)
+        xl = xl && L.kv_heads == kXcds && L.q_heads == 2 * kXcds && L.width == 256 && !L.shared_v &&
+             L.qkv.rows == (L.q_heads + 2 * L.kv_heads) * 256u;
+    if (xl) {
+        DevMem map;
+        if ((rc = dev_alloc(map, (size_t)grid * 4, "XCD map"))) return rc;
+        HIP_OK(step_xcd_map(grid, map.as<uint32_t>(), nullptr), "XCD map");
+        std::vector<uint32_t> xcc(grid);
+        HIP_OK(hipMemcpy(xcc.data(), map.p, (size_t)grid * 4, hipMemcpyDeviceToHost), "XCD map");
+        for (uint32_t b = 0; b < grid; ++b) xl = xl && xcc[b] == b % kXcds;
+    }
+    s.xcd_local = xl;
     std::vector<StepLayer> table(s.layers.size());
     for (size_t i = 0; i < s.layers.size(); ++i) {
         const LayerDev& L = s.layers[i];
@@ -1227,7 +1247,6 @@ int setup_step(af_session& s) {
         t.window = L.window;
         t.v_norm = L.v_norm ? 1u : 0u;
     }
-    int rc;
     if ((rc = dev_upload(s.STEP_LAYERS, table.data(), table.size() * sizeof(StepLayer), "layer table"))) return rc;
     // the o-proj input image is handed over as tagged pieces: 16 bytes per 8-byte image word
     const size_t att_img = (size_t)((s.max_q / 32 + 3) / 4) * kStepImg * 2,
@@ -1260,8 +1279,8 @@ int setup_step(af_session& s) {
     if ((rc = dev_upload(s.STREAM_OFF, off.data(), off.size() * 8, "weight stream offsets"))) return rc;
     if ((rc = dev_alloc(s.STREAM, off.back() + kStepStreamPad, "weight stream"))) return rc;
     HIP_OK(hipMemset(s.STREAM.as<uint8_t>() + off.back(), 0, kStepStreamPad), "weight stream padding");
-    HIP_OK(launch_stream_repack(s.STEP_LAYERS.as<StepLayer>(), (uint32_t)s.layers.size(), grid, s.STREAM.as<uint8_t>(),
-                                s.STREAM_OFF.as<uint64_t>(), nullptr),
+    HIP_OK(launch_stream_repack(s.STEP_LAYERS.as<StepLayer>(), (uint32_t)s.layers.size(), grid, s.xcd_local ? 1u : 0u,
+                                s.STREAM.as<uint8_t>(), s.STREAM_OFF.as<uint64_t>(), nullptr),
            "weight stream build");
     HIP_OK(hipDeviceSynchronize(), "weight stream build");
     // The tiled matrices stay resident: a step kernel that times out (its workgroups were not all

@@ -31,8 +31,15 @@ namespace {
 constexpr uint32_t kThreads = 512;
 constexpr uint32_t kStreamWaves = kStepStreamWaves;  // waves 1..7 stream weights
 constexpr int kRing = 8;              // weight records in flight per streaming wave
-constexpr int kSC1 = 16;              // cache policy: agent-scope coherent access
-constexpr int kNT = 2;                // cache policy: non-temporal (weights are read once per step)
+constexpr int kSC1 = 16;              // cache policy: agent-scope coherent access (through to the
+                                      // memory side, where every XCD's accesses meet)
+constexpr int kSC0 = 1;               // cache policy (stores): workgroup scope, into the XCD's L2;
+                                      // other workgroups of the XCD read it with kNT loads, which
+                                      // miss their CU's L1 and hit that L2 (measured round trip
+                                      // between two workgroups of one XCD: 0.42 us, against 1.04 us
+                                      // through the memory side with kSC1)
+constexpr int kNT = 2;                // cache policy: non-temporal (weights are read once per step; a
+                                      // non-temporal load also misses the CU's L1)
 constexpr int kVmWait = 0x0F70;       // s_waitcnt vmcnt(0) with expcnt / lgkmcnt unconstrained
 constexpr uint32_t kSpinLimit = 1u << 21;
 constexpr uint32_t kMaxUnits = kStepMaxUnits;
@@ -65,6 +72,14 @@ __device__ __forceinline__ void stc8(void* base, uint32_t off, v2u v) {
 __device__ __forceinline__ void stc16(void* base, uint32_t off, v4u v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), off, 0, kSC1);
 }
+template <int Pol>
+__device__ __forceinline__ void st8p(void* base, uint32_t off, v2u v) {
+    __builtin_amdgcn_raw_buffer_store_b64(v, rsrc(base), off, 0, Pol);
+}
+template <int Pol>
+__device__ __forceinline__ void st16p(void* base, uint32_t off, v4u v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc(base), off, 0, Pol);
+}
 __device__ __forceinline__ void wait_vm() { __builtin_amdgcn_s_waitcnt(kVmWait); }
 
 // threadIdx.x through an empty asm, read once per phase: the per-lane values derived from it are
@@ -87,12 +102,14 @@ __device__ __forceinline__ void dma(const void* src, uint32_t bytes, uint8_t* ld
 }
 
 // The same copy split over the workgroup's 8 waves (wave w takes every 8th KB), so that one
-// wave's issue rate does not bound it; each wave waits for its own part.
+// wave's issue rate does not bound it; each wave waits for its own part.  Pol: the loads' cache
+// policy (kSC1, or kSC0 for data another workgroup of this XCD wrote).
+template <int Pol = kSC1>
 __device__ __forceinline__ void dma_all(const void* src, uint32_t bytes, uint8_t* lds, uint32_t wave, uint32_t lane) {
     for (uint32_t off = wave * 1024; off < bytes; off += 8 * 1024) {
         if (off + lane * 16 < bytes)
             __builtin_amdgcn_global_load_lds(static_cast<const uint8_t*>(src) + off + lane * 16,
-                                             (lds_ptr)(lds + off), 16, 0, kSC1);
+                                             (lds_ptr)(lds + off), 16, 0, Pol);
     }
 }
 
@@ -777,11 +794,17 @@ __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t 
 // stay in flight), except for chunks too long to stage, whose K/V rows every wave reads directly,
 // and the merge's copy of the chunk partials.  Barriers: staged; norms summed; q/k rotated;
 // scores; softmax; values; partial; published (and, merging: partials copied; outputs merged).
-template <int GQ>
+template <int GQ, bool XL>
 __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uint32_t pos, uint32_t h, uint32_t c,
                                                uint32_t chunks, uint32_t cmax, uint32_t clen, uint32_t start,
                                                uint32_t tag, uint8_t* lds, int* flag, int* bad, const Grid& g) {
     constexpr int D = 256, NH = GQ + 2;
+    // XCD-local layout: this head group's q/k/v and chunk partials were written by workgroups of
+    // this XCD, so they are read from its L2 (non-temporal loads: they miss the CU's L1, where a
+    // poll would otherwise keep hitting a stale line) and the merge ticket is an L2 atomic
+    constexpr int kPol = XL ? kNT : kSC1;
+    constexpr int kSt = XL ? kSC0 : kSC1;  // stores: into the XCD's L2, or through to the memory side
+    constexpr int kScope = XL ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
     AttnLds<GQ> sh(lds);
     float* nrm = sh.nrm;
     float* qs = sh.qs;
@@ -819,7 +842,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
 #pragma unroll
             for (int j = 0; j < J; ++j)
                 if (need >> j & 1)
-                    __builtin_amdgcn_global_load_lds(src(j), (lds_ptr)(stg + j * 1024), 16, 0, kSC1);
+                    __builtin_amdgcn_global_load_lds(src(j), (lds_ptr)(stg + j * 1024), 16, 0, kPol);
             if (spins == 0) {
                 // the RoPE angles of this position, while the first copies are in flight
 #pragma unroll
@@ -1046,11 +1069,11 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
         }
         // stride * 4 bytes per chunk: a multiple of 16, the padding included
         const v4u* ps = reinterpret_cast<const v4u*>(pst);
-        for (uint32_t i = lane; i < stride / 4; i += 64) stc16(head_part, (c * stride + 4 * i) * 4, ps[i]);
+        for (uint32_t i = lane; i < stride / 4; i += 64) st16p<kSt>(head_part, (c * stride + 4 * i) * 4, ps[i]);
         wait_vm();
         if (lane == 0) {
             const uint32_t ticket =
-                __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_fetch_add(a.counters + h, 1u, __ATOMIC_RELAXED, kScope);
             *flag = ticket == chunks - 1;
         }
         wait_vm();
@@ -1063,7 +1086,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     // sum_c w_c o_c / sum_c w_c l_c, in chunk order
     float* mrg = reinterpret_cast<float*>(lds);  // [chunks][stride]
     float* outv = mrg + chunks * stride;        // [GQ][D]
-    dma_all(head_part, chunks * stride * 4, lds, wave, lane);
+    dma_all<kPol>(head_part, chunks * stride * 4, lds, wave, lane);
     wait_vm();
     __syncthreads();
     for (uint32_t i = tid; i < GQ * D; i += kThreads) {
@@ -1093,7 +1116,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
                 quad_digits_store_tagged(v, reinterpret_cast<uint32_t*>(a.att_img), nst_att, h * GQ * 8 + blk, p, tag);
             }
         }
-        if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_store(a.counters + h, 0u, __ATOMIC_RELAXED, kScope);
         wait_vm();
     }
 }
@@ -1212,12 +1235,30 @@ __device__ __forceinline__ AttnGeo attn_geo(CLayer& L, uint32_t pos, uint32_t cm
     return g;
 }
 
+// The attention item (KV head h, chunk c) of this workgroup, if it has one: item i = h chunks + c
+// runs on workgroup grid - 1 - i, or in the XCD-local layout chunk c of head h on workgroup
+// 8 (grid / 8 - 1 - c) + h (every chunk of a head on XCD h).
+template <bool XL>
+__device__ __forceinline__ bool attn_item(const AttnGeo& ag, uint32_t& h, uint32_t& c) {
+    if constexpr (XL) {
+        const uint32_t b = blockIdx.x;
+        h = b % kXcds;
+        c = gridDim.x / kXcds - 1 - b / kXcds;
+        return c < ag.chunks && h * ag.chunks < ag.items;
+    } else {
+        const uint32_t item = gridDim.x - 1 - blockIdx.x;
+        h = item / max(ag.chunks, 1u);
+        c = item % max(ag.chunks, 1u);
+        return item < ag.items;
+    }
+}
+
 }  // namespace
 
 // Wave 0: copies for phase ph that do not depend on the phase before it (norm weights of a
 // residual prologue, or the attention item's RoPE frequencies, norm weights and cached K/V
 // rows).  Issued only: the caller waits (wave 0 waits for everything at the end of its epilogue).
-template <int GQ>
+template <int GQ, bool XL>
 __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t pos, uint8_t* lds,
                                           uint32_t lane) {
     if (ph >= n_phases) return;
@@ -1225,8 +1266,8 @@ __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t
     if (kind == P_ATTN) {
         CLayer& L = layer_at(a, l);
         const AttnGeo ag = attn_geo(L, pos, a.cmax);
-        const uint32_t item = gridDim.x - 1 - blockIdx.x;
-        if (item < ag.items) attention_pre<GQ>(L, pos, item / ag.chunks, item % ag.chunks, ag.clen, ag.start, lds, lane);
+        uint32_t h, c;
+        if (attn_item<XL>(ag, h, c)) attention_pre<GQ>(L, pos, h, c, ag.clen, ag.start, lds, lane);
     } else if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
         preload_norms(d.in_kind, d.in, d.K, a.xs_off, lds, lane);
@@ -1271,7 +1312,7 @@ __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, i
 // consume their weight stream (refilling the ring with the next phase's records) while wave 0
 // stores the residual and prepares the next phase when its LDS is free; wave 0 stores the
 // outputs.  Every phase's code appears once in the loop over (layer, phase).
-template <int GQ>
+template <int GQ, bool XL>
 __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ float part[kPart];
@@ -1307,7 +1348,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
 #pragma unroll
         for (int u = 0; u < kRing; ++u) ring_fill(r, rs, u, lane);
     } else {
-        phase_pre<GQ>(a, 0, n_phases, pos, lds, lane);
+        phase_pre<GQ, XL>(a, 0, n_phases, pos, lds, lane);
         wait_vm();
     }
 
@@ -1331,10 +1372,10 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
         if (kind == P_ATTN) {
             CLayer& L = layer_at(a, l);
             const AttnGeo ag = attn_geo(L, pos, a.cmax);
-            const uint32_t item = gridDim.x - 1 - blockIdx.x;
-            if (item < ag.items)
-                attention_item<GQ>(L, a, pos, item / ag.chunks, item % ag.chunks, ag.chunks, ag.cmax, ag.clen, ag.start,
-                                   tag0 + l, lds, &att_flag, &poll_bad, g);
+            uint32_t h, c;
+            if (attn_item<XL>(ag, h, c))
+                attention_item<GQ, XL>(L, a, pos, h, c, ag.chunks, ag.cmax, ag.clen, ag.start, tag0 + l, lds, &att_flag,
+                                       &poll_bad, g);
             else if (wave != 0)
                 prefetch_records(r, pf_sink, lane);  // waited for in the o-proj stage (poll_image)
             __syncthreads();
@@ -1379,7 +1420,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                     wait_vm();
                 }
                 if (pre_now && (ph + 1 >= n_phases || (uint32_t)(ph + 1) % kPhases == P_ATTN))
-                    phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
+                    phase_pre<GQ, XL>(a, ph + 1, n_phases, pos, lds, lane);
                 stamp(g, M_PRE);
                 // the streaming waves with records (wave - 1 < fe) have left their partials in part
                 const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
@@ -1391,14 +1432,22 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                     __builtin_amdgcn_s_sleep(1);
                 done_cnt = 0;  // next incremented after the next phase's stage barrier
                 stamp(g, M_STREAMED);
-                if (!pre_now) phase_pre<GQ>(a, ph + 1, n_phases, pos, lds, lane);
+                if (!pre_now) phase_pre<GQ, XL>(a, ph + 1, n_phases, pos, lds, lane);
                 const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
                 if (d.y || d.yt) {
                     if (tid < 16 * mu) {
-                        const uint32_t k = tid >> 4, rr = tid & 15, row = (blockIdx.x + k * gridDim.x) * 16 + rr;
+                        const uint32_t k = tid >> 4, rr = tid & 15;
+                        uint32_t tile = blockIdx.x + k * gridDim.x;
+                        if (XL && kind == P_QKV) {
+                            CLayer& L = layer_at(a, l);
+                            tile = step_qkv_tile(blockIdx.x, k, gridDim.x, 1u, L.qn / 16, L.kn / 16);
+                        }
+                        const uint32_t row = tile * 16 + rr;
                         const float y = (float)(rn * (double)part_sum(part, k, 0, rr));
                         if (row < d.rows) {
-                            if (d.yt)
+                            if (XL && kind == P_QKV)  // read by this XCD's attention items, from its L2
+                                st8p<kSC0>(d.yt, row * 8, v2u{__float_as_uint(y), d.ytag});
+                            else if (d.yt)
                                 stc8(d.yt, row * 8, v2u{__float_as_uint(y), d.ytag});
                             else
                                 stc(d.y, row * 4, __float_as_uint(y));
@@ -1432,7 +1481,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
 // that wave's records, every GEMV phase of every layer in consume order, from the layers' tiled
 // matrices into its run (a unit past the last row tile reads as zero weights).
 __global__ __launch_bounds__(256) void stream_repack_kernel(const StepLayer* layers, uint32_t n_layers, uint32_t grid,
-                                                            uint8_t* stream, const uint64_t* off) {
+                                                            uint32_t xl, uint8_t* stream, const uint64_t* off) {
     const uint32_t b = blockIdx.x / kStreamWaves, w = blockIdx.x % kStreamWaves + 1;
     uint4* dst = reinterpret_cast<uint4*>(stream + off[blockIdx.x]);
     constexpr uint32_t kChunks = kStepRecord / 16;  // 64 code chunks, then 8 scale chunks
@@ -1451,7 +1500,8 @@ __global__ __launch_bounds__(256) void stream_repack_kernel(const StepLayer* lay
                     const uint32_t f = w - 1 + kStreamWaves * j, seg = f / nst, st = f % nst, ts = seg % T, k = seg / T;
                     const uint32_t u = b + k * grid;
                     const Q4View& m = pair && ts >= 2 ? L.up : m0;
-                    const uint32_t tile = pair ? 2 * u + (ts & 1) : u;
+                    const uint32_t tile = pair ? 2 * u + (ts & 1)
+                                               : kind == 0 ? step_qkv_tile(b, k, grid, xl, L.qn / 16, L.kn / 16) : u;
                     const size_t src = (size_t)tile * nst + st;
                     uint4 v = make_uint4(0u, 0u, 0u, 0u);
                     if (tile < tiles)
@@ -1465,10 +1515,20 @@ __global__ __launch_bounds__(256) void stream_repack_kernel(const StepLayer* lay
     }
 }
 
-hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint32_t grid, uint8_t* stream,
-                                const uint64_t* stream_off, hipStream_t s) {
-    hipLaunchKernelGGL(stream_repack_kernel, dim3(grid * kStreamWaves), dim3(256), 0, s, layers, n_layers, grid, stream,
-                       stream_off);
+hipError_t launch_stream_repack(const StepLayer* layers, uint32_t n_layers, uint32_t grid, uint32_t xcd_local,
+                                uint8_t* stream, const uint64_t* stream_off, hipStream_t s) {
+    hipLaunchKernelGGL(stream_repack_kernel, dim3(grid * kStreamWaves), dim3(256), 0, s, layers, n_layers, grid,
+                       xcd_local, stream, stream_off);
+    return hipGetLastError();
+}
+
+// Thread 0 of workgroup b stores the XCD it runs on (the XCC_ID hardware register, bits [3:0]).
+__global__ __launch_bounds__(64) void xcd_map_kernel(uint32_t* xcc) {
+    if (threadIdx.x == 0) xcc[blockIdx.x] = __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 0xFu;
+}
+
+hipError_t step_xcd_map(uint32_t grid, uint32_t* xcc, hipStream_t s) {
+    hipLaunchKernelGGL(xcd_map_kernel, dim3(grid), dim3(64), 0, s, xcc);
     return hipGetLastError();
 }
 
@@ -1496,10 +1556,14 @@ size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t 
 // would end in the barriers' spin limit, reported as a failed step, not in a hang.  The
 // cooperative launch API gives the same residency and costs about 12 us more per launch.
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s) {
+    if (a.xcd_local && group != 2) return hipErrorInvalidValue;
     switch (group) {
-        case 1: hipLaunchKernelGGL(decode_step_kernel<1>, dim3(grid), dim3(kThreads), lds, s, a); break;
-        case 2: hipLaunchKernelGGL(decode_step_kernel<2>, dim3(grid), dim3(kThreads), lds, s, a); break;
-        case 4: hipLaunchKernelGGL(decode_step_kernel<4>, dim3(grid), dim3(kThreads), lds, s, a); break;
+        case 1: hipLaunchKernelGGL((decode_step_kernel<1, false>), dim3(grid), dim3(kThreads), lds, s, a); break;
+        case 2:
+            if (a.xcd_local) hipLaunchKernelGGL((decode_step_kernel<2, true>), dim3(grid), dim3(kThreads), lds, s, a);
+            else hipLaunchKernelGGL((decode_step_kernel<2, false>), dim3(grid), dim3(kThreads), lds, s, a);
+            break;
+        case 4: hipLaunchKernelGGL((decode_step_kernel<4, false>), dim3(grid), dim3(kThreads), lds, s, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -1509,8 +1573,9 @@ hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid) {
     int dev = 0, cus = 0, per = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    const void* k = group == 1 ? (const void*)decode_step_kernel<1>
-                               : group == 2 ? (const void*)decode_step_kernel<2> : (const void*)decode_step_kernel<4>;
+    const void* k = group == 1   ? (const void*)decode_step_kernel<1, false>
+                    : group == 2 ? (const void*)decode_step_kernel<2, false>
+                                 : (const void*)decode_step_kernel<4, false>;
     if (e == hipSuccess) e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, kThreads, lds);
     if (e != hipSuccess) return e;
     *grid = per >= 1 ? (uint32_t)(cus / 8 * 8) : 0u;
