@@ -103,6 +103,7 @@ SIGNATURES = {
     "af_q6_gemv_argmax": (i32, [P, P, P, P, P]),
     "af_q6_gemv_argmax_noalloc": (i32, [P, P, P, P, P]),
     "af_rmsnorm": (i32, [P, P, P, u32, u32, f32, P]),
+    "af_softcap": (i32, [P, P, sz, f32, P]),
     "af_ffn_create": (i32, [ctypes.POINTER(FfnDesc), ctypes.POINTER(P)]),
     "af_ffn_free": (None, [P]),
     "af_ffn_run": (i32, [P, P, P, P]),

@@ -298,6 +298,17 @@ class HipDiagnostics:
         return GenerationTokens(out[:n.value].tolist(), bool(stopped.value), _stats(st))
 
 
+def softcap(logits, cap):
+    """Final logit softcapping on the GPU (af_softcap; crates/domain/src/q6.rs:66-71): the capped
+    logits of the reference's logits report (crates/cuda-backend/src/logits.rs:70-201)."""
+    from . import hip
+    x = np.ascontiguousarray(logits, dtype=np.float32)
+    xb, yb = hip.Buffer.from_numpy(x), hip.Buffer(x.shape, np.float32)
+    check(N.lib().af_softcap(xb.ptr, yb.ptr, x.size, float(cap), None))
+    hip.synchronize()
+    return yb.numpy()
+
+
 def rmsnorm_patterns(width):
     """The eight vectors of crates/cuda-backend/src/rms_norm.rs:22-52 (xorshift32 from 0x4090)."""
     out = np.empty((8, width), np.float32)

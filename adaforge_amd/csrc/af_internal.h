@@ -156,22 +156,25 @@ struct AttnArgs {
     const uint32_t* state;   // non-null: position = state[ST_POS]
     uint32_t position;
     float* out;              // [q_heads][head_width]
-    float* part;             // [kv_heads][cmax][group][head_width + 2]
-    uint32_t* counters;      // [kv_heads]
+    float* part;             // [kv_heads * group / G][cmax][G][head_width + 2] (G: attention_block_heads)
+    uint32_t* counters;      // [kv_heads * group / G]
     int8_t* dig_out;         // digit image of `out` for the output projection (may be null)
     uint32_t cmax;
     uint32_t min_chunk;
     uint32_t kv_heads;
+    uint32_t group;          // query heads per KV head
 };
 
 // ---- launchers (kernels.hip) -----------------------------------------------------------------
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s);
+uint32_t attention_block_heads(uint32_t group, uint32_t head_width);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t width, uint32_t vectors, float eps,
                           hipStream_t s);
 hipError_t launch_resid(const InputStage& in, uint32_t width, float* y, hipStream_t s);
 hipError_t launch_advance(uint32_t* state, hipStream_t s);
+hipError_t launch_softcap(const float* x, float* y, size_t n, float cap, hipStream_t s);
 hipError_t launch_zero_words(uint32_t* p, uint32_t n, hipStream_t s);
 uint32_t head_grid(uint32_t rows);
 

@@ -193,8 +193,11 @@ int check_supported_q4(uint32_t columns, const char* what) {
 }
 int check_supported_attention(const af_attention_config& c) {
     const uint32_t g = c.q_heads / c.kv_heads;
-    if (c.width != 256) return fail(AF_ERR_INVALID, "attention head width must be 256");
-    if (g != 1 && g != 2 && g != 4) return fail(AF_ERR_INVALID, "query heads per KV head must be 1, 2 or 4");
+    if (c.width != 256 && c.width != 512) return fail(AF_ERR_INVALID, "attention head width must be 256 or 512");
+    if (c.width == 256 && g != 1 && g != 2 && g != 4)
+        return fail(AF_ERR_INVALID, "query heads per KV head must be 1, 2 or 4 at width 256");
+    if (c.width == 512 && g != 1 && g != 2 && g != 4 && g != 8 && g != 16)
+        return fail(AF_ERR_INVALID, "query heads per KV head must be 1, 2, 4, 8 or 16 at width 512");
     return AF_OK;
 }
 
@@ -515,6 +518,13 @@ int af_rmsnorm(const float* x, const float* weights, float* y, uint32_t width, u
     return AF_OK;
 }
 
+int af_softcap(const float* x, float* y, size_t n, float cap, void* stream) {
+    if (!x || !y || n == 0) return fail(AF_ERR_INVALID, "invalid softcap arguments");
+    if (!std::isfinite(cap) || cap <= 0.0f) return fail(AF_ERR_INVALID, "Softcapping invalide");  // q6.rs:67-69
+    HIP_OK(launch_softcap(x, y, n, cap, (hipStream_t)stream), "softcap launch");
+    return AF_OK;
+}
+
 int af_matvec_run(const uint8_t* q4, size_t len, uint32_t columns, uint32_t rows, const float* inputs,
                   uint32_t n_inputs, uint32_t timed_repetitions, float* outputs, float* median_ms) {
     int rc = check_q4(q4, len, columns, rows, "Q4_0 matrix");
@@ -713,7 +723,7 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     std::lock_guard<std::mutex> lock(g_scratch.mu);
     if ((rc = grow(g_scratch.attn_part, (size_t)p->config.kv_heads * cmax * group * (D + 2) * 4, false, "attention scratch")))
         return rc;
-    if ((rc = grow(g_scratch.attn_counters, (size_t)std::max<uint32_t>(64, p->config.kv_heads) * 4, true,
+    if ((rc = grow(g_scratch.attn_counters, (size_t)std::max<uint32_t>(64, p->config.q_heads) * 4, true,
                    "attention counters")))
         return rc;
     // inverse frequencies: kept on the device and re-uploaded only when the RoPE parameters change
@@ -749,6 +759,7 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     a.cmax = cmax;
     a.min_chunk = kAttnMinChunk;
     a.kv_heads = p->config.kv_heads;
+    a.group = group;
     HIP_OK(launch_attention(a, group, D, (hipStream_t)stream), "attention launch");
     return AF_OK;
 }
@@ -958,6 +969,7 @@ struct af_session {
         aa.cmax = cmax;
         aa.min_chunk = kAttnMinChunk;
         aa.kv_heads = L.kv_heads;
+        aa.group = L.q_heads / L.kv_heads;
         const double nvis = L.window ? std::min<double>(host_pos + 1, L.window) : host_pos + 1.0;
         const double attn_bytes = nvis * 2.0 * L.kn * 2.0 + 4.0 * (2.0 * L.qn + 2.0 * L.kn) + 4.0 * L.kn;
         if ((e = timed(K_ATTN, attn_bytes, [&] { return launch_attention(aa, L.q_heads / L.kv_heads, L.width, stream); })) !=
@@ -1326,7 +1338,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     if (const char* fp = std::getenv("AF_STEP_FAIL_PHASE")) s->fail_phase = (uint32_t)std::strtoul(fp, nullptr, 10);
     HIP_OK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "session stream");
 
-    uint32_t max_kv = 0, max_q = 0, max_group = 1;
+    uint32_t max_kv = 0, max_q = 0, max_group = 1, max_qh_part = 0, max_qh = 0;
     s->layers.resize(n_layers);
     for (uint32_t i = 0; i < n_layers; ++i) {
         const af_layer_weights& w = layers[i];
@@ -1373,6 +1385,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         max_kv = std::max(max_kv, L.kv_heads);
         max_q = std::max(max_q, L.qn);
         max_group = std::max(max_group, L.q_heads / L.kv_heads);
+        max_qh_part = std::max(max_qh_part, L.q_heads * (L.width + 2));  // attention_kernel's partials per chunk
+        max_qh = std::max(max_qh, L.q_heads);
         s->max_qkv = std::max(s->max_qkv, L.qkv.rows);
         s->max_kv_rows = std::max(s->max_kv_rows, L.kn);
     }
@@ -1398,9 +1412,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         {&s->PROJT, (size_t)hidden * 8, true},
         {&s->DT, (size_t)hidden * 8, true},
         {&s->LOGITS, (size_t)hm.rows * 4, false},
-        {&s->PART, (size_t)max_kv * s->cmax * std::max<uint32_t>(max_group * (256 + 2), step_part_stride(max_group)) * 4,
-         false},
-        {&s->COUNTERS, (size_t)std::max<uint32_t>(max_kv, 64) * 4, true},
+        {&s->PART, (size_t)s->cmax * std::max<uint32_t>(max_qh_part, max_kv * step_part_stride(max_group)) * 4, false},
+        {&s->COUNTERS, (size_t)std::max<uint32_t>(max_qh, 64) * 4, true},
         {&s->HPART, (size_t)s->head_blocks * 16, false},
         {&s->HCOUNT, 256, true},
         {&s->STATE, ST_WORDS * 4, true},

@@ -410,17 +410,20 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
 // token), chunk softmax, and p-weighted values; chunk partials (acc, max, sum)
 // are merged by the last block of the KV head.
 
-template <int D, int GQ>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
-    static_assert(D == 256, "one thread per channel");
-    constexpr int NH = GQ + 2;  // query heads, then the new key and value
+template <int D, int G>
+__global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
+    static_assert(D == 256 || D == 512, "one thread per channel");
+    constexpr int NH = G + 2;     // this block's query heads, then the new key and value
+    constexpr int W = D / 64;     // waves
+    constexpr int LK = D / 16;    // lanes per token in the score loop (16 channels each)
+    constexpr int TG = D / LK;    // token groups in the score loop (16)
     __shared__ float nrm[NH][D];
-    __shared__ float qs[GQ][D];
-    __shared__ float scores[GQ][kAttnMaxChunkLen];
-    __shared__ float vred[8][GQ][D];
-    __shared__ double dred[4][NH];
+    __shared__ float qs[G][D];
+    __shared__ float scores[G][kAttnMaxChunkLen];
+    __shared__ float vred[8][G][D];
+    __shared__ double dred[W][NH];
     __shared__ float fred[8];
-    __shared__ float cw[GQ][kAttnMaxChunks];
+    __shared__ float cw[G][kAttnMaxChunks];
     __shared__ bool last;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -431,20 +434,24 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     uint32_t chunks = min(a.cmax, (nvis + a.min_chunk - 1) / a.min_chunk);
     const uint32_t clen = (nvis + chunks - 1) / chunks;
     chunks = (nvis + clen - 1) / clen;
-    const uint32_t c = blockIdx.x, kvh = blockIdx.y;
+    // block (c, kvh * qgroups + qg): chunk c of query heads kvh * group + qg * G + [0, G)
+    const uint32_t qgroups = a.group / G;
+    const uint32_t c = blockIdx.x, kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
+    const uint32_t qh0 = kvh * a.group + qg * G;
     if (c >= chunks) return;
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
     const uint32_t n = t1 - t0;
     const uint32_t ring = a.ring;
-    const bool append = t1 == pos + 1;  // this chunk holds the new token: append its K and V
-    const int nh = append ? NH : GQ;
+    const bool has_new = t1 == pos + 1;      // this chunk holds the new token (its K and V computed here)
+    const bool append = has_new && qg == 0;  // and this block stores them in the cache
+    const int nh = has_new ? NH : G;
 
     // ---- prologue: RMSNorm of the query heads (and new K, V) with one block reduction, then RoPE
     float raw[NH];
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) raw[h] = a.q_raw[(size_t)(kvh * GQ + h) * D + tid];
-    raw[GQ] = append ? a.k_raw[(size_t)kvh * D + tid] : 0.0f;
-    raw[GQ + 1] = append ? a.v_raw[(size_t)kvh * D + tid] : 0.0f;
+    for (int h = 0; h < G; ++h) raw[h] = a.q_raw[(size_t)(qh0 + h) * D + tid];
+    raw[G] = has_new ? a.k_raw[(size_t)kvh * D + tid] : 0.0f;
+    raw[G + 1] = has_new ? a.v_raw[(size_t)kvh * D + tid] : 0.0f;
     double sn = 0.0, cs = 1.0;
     if (tid < D / 2) sincos((double)pos * a.inv_freq[tid], &sn, &cs);
 #pragma unroll
@@ -456,52 +463,66 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         if (h >= nh) break;
-        const double ss = (dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h]);
-        if (h < GQ) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.q_eps), a.q_norm[tid]);
-        else if (h == GQ) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.k_eps), a.k_norm[tid]);
+        double ss = 0.0;  // waves summed pairwise in index order
+        if constexpr (W == 4) {
+            ss = (dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h]);
+        } else {
+            ss = ((dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h])) +
+                 ((dred[4][h] + dred[5][h]) + (dred[6][h] + dred[7][h]));
+        }
+        if (h < G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.q_eps), a.q_norm[tid]);
+        else if (h == G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.k_eps), a.k_norm[tid]);
         else nrm[h][tid] = a.v_norm ? (float)__dmul_rn((double)raw[h], inv_rms(ss, D, a.v_eps)) : raw[h];
     }
     __syncthreads();
+    // the new token's K (rotated) and V, fp16, for this block's reads: in the cache when this block
+    // appends them, otherwise in LDS (another block of the KV head appends the same values)
+    __shared__ uint16_t knew[D], vnew[D];
     if (tid < D / 2) {
 #pragma unroll
-        for (int h = 0; h < GQ + 1; ++h) {
-            if (h == GQ && !append) break;
+        for (int h = 0; h < G + 1; ++h) {
+            if (h == G && !has_new) break;
             const double x = (double)nrm[h][tid], y = (double)nrm[h][tid + D / 2];
             const float r0 = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
             const float r1 = (float)__dadd_rn(__dmul_rn(x, sn), __dmul_rn(y, cs));
-            if (h < GQ) {
+            if (h < G) {
                 qs[h][tid] = r0;
                 qs[h][tid + D / 2] = r1;
             } else {
-                const size_t slot = ((size_t)kvh * ring + pos % ring) * D;
-                a.kcache[slot + tid] = f2h(r0);
-                a.kcache[slot + tid + D / 2] = f2h(r1);
+                knew[tid] = f2h(r0);
+                knew[tid + D / 2] = f2h(r1);
             }
         }
     }
-    if (append) a.vcache[((size_t)kvh * ring + pos % ring) * D + tid] = f2h(nrm[GQ + 1][tid]);
+    if (has_new) vnew[tid] = f2h(nrm[G + 1][tid]);
     __syncthreads();
+    if (append) {
+        const size_t slot = ((size_t)kvh * ring + pos % ring) * D;
+        a.kcache[slot + tid] = knew[tid];
+        a.vcache[slot + tid] = vnew[tid];
+    }
 
-    // ---- scores: 16 lanes per token, 16 channels per lane, two tokens in flight per group
+    // ---- scores: LK lanes per token (16 channels each), TG token groups, two tokens in flight
     {
-        const uint32_t grp = tid >> 4, j = tid & 15;
-        float qr[GQ][16];
+        const uint32_t grp = tid / LK, j = tid % LK;
+        float qr[G][16];
 #pragma unroll
-        for (int gi = 0; gi < GQ; ++gi)
+        for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 16; ++e) qr[gi][e] = qs[gi][16 * j + e];
-        for (uint32_t tb = t0 + grp; tb < t1; tb += 32) {
+        for (uint32_t tb = t0 + grp; tb < t1; tb += 2 * TG) {
             uint4 k[2][2];
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const uint32_t t = tb + 16 * u;
-                const uint16_t* kp = a.kcache + ((size_t)kvh * ring + (t < t1 ? t : tb) % ring) * D + 16 * j;
+                const uint32_t t = tb + TG * u;
+                const uint32_t tt = t < t1 ? t : tb;
+                const uint16_t* kp = (tt == pos ? knew : a.kcache + ((size_t)kvh * ring + tt % ring) * D) + 16 * j;
                 k[u][0] = *reinterpret_cast<const uint4*>(kp);
                 k[u][1] = *reinterpret_cast<const uint4*>(kp + 8);
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const uint32_t t = tb + 16 * u;
+                const uint32_t t = tb + TG * u;
                 const uint32_t kw[8] = {k[u][0].x, k[u][0].y, k[u][0].z, k[u][0].w,
                                         k[u][1].x, k[u][1].y, k[u][1].z, k[u][1].w};
                 float kf[16];
@@ -511,11 +532,12 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
                     kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
                 }
 #pragma unroll
-                for (int gi = 0; gi < GQ; ++gi) {
+                for (int gi = 0; gi < G; ++gi) {
                     float d = 0.0f;
 #pragma unroll
                     for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
                     d = row_sum(d);
+                    if constexpr (LK == 32) d += __shfl_xor(d, 16);  // the token's second row of 16 lanes
                     if (j == 0 && t < t1) scores[gi][t - t0] = d * a.scale;
                 }
             }
@@ -523,9 +545,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    float m[GQ], l[GQ];
+    float m[G], l[G];
 #pragma unroll
-    for (int gi = 0; gi < GQ; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
         float mx = -INFINITY;
         for (uint32_t i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, scores[gi][i]);
         m[gi] = block_max_f(mx, fred);
@@ -539,12 +561,13 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
     __syncthreads();
 
-    // ---- values: 32 lanes per token row, 8 channels per lane, 8 token groups, 2 rows in flight
+    // ---- values: D / 8 lanes per token row (8 channels each), 8 token groups, 2 rows in flight
     {
-        const uint32_t tg = tid >> 5, dl = tid & 31;
-        float acc[GQ][8];
+        constexpr uint32_t LV = D / 8;
+        const uint32_t tg = tid / LV, dl = tid % LV;
+        float acc[G][8];
 #pragma unroll
-        for (int gi = 0; gi < GQ; ++gi)
+        for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[gi][e] = 0.0f;
         for (uint32_t tb = t0 + tg; tb < t1; tb += 16) {
@@ -552,8 +575,9 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const uint32_t t = tb + 8 * u;
-                vv[u] = *reinterpret_cast<const uint4*>(a.vcache + ((size_t)kvh * ring + (t < t1 ? t : tb) % ring) * D +
-                                                        8 * dl);
+                const uint32_t tt = t < t1 ? t : tb;
+                const uint16_t* vp = tt == pos ? vnew : a.vcache + ((size_t)kvh * ring + tt % ring) * D;
+                vv[u] = *reinterpret_cast<const uint4*>(vp + 8 * dl);
             }
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
@@ -567,7 +591,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
                     vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
                 }
 #pragma unroll
-                for (int gi = 0; gi < GQ; ++gi) {
+                for (int gi = 0; gi < G; ++gi) {
                     const float p = scores[gi][t - t0];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[gi][e] = fmaf(p, vf[e], acc[gi][e]);
@@ -575,14 +599,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
             }
         }
 #pragma unroll
-        for (int gi = 0; gi < GQ; ++gi)
+        for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 8; ++e) vred[tg][gi][8 * dl + e] = acc[gi][e];
     }
     __syncthreads();
-    float o[GQ];
+    float o[G];
 #pragma unroll
-    for (int gi = 0; gi < GQ; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
         float t = 0.0f;
 #pragma unroll
         for (int g = 0; g < 8; ++g) t += vred[g][gi][tid];
@@ -590,15 +614,16 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     }
     if (chunks == 1) {
 #pragma unroll
-        for (int gi = 0; gi < GQ; ++gi) a.out[(size_t)(kvh * GQ + gi) * D + tid] = o[gi] / l[gi];
+        for (int gi = 0; gi < G; ++gi) a.out[(size_t)(qh0 + gi) * D + tid] = o[gi] / l[gi];
         return;
     }
 
-    // ---- split-K merge: the last block of this KV head combines the chunk partials
-    const size_t stride = (size_t)GQ * (D + 2);
-    float* mine = a.part + ((size_t)kvh * a.cmax + c) * stride;
+    // ---- split-K merge: the last block of this (KV head, query group) combines the chunk partials
+    const size_t stride = (size_t)G * (D + 2);
+    const uint32_t slot = blockIdx.y;  // (KV head, query group)
+    float* mine = a.part + ((size_t)slot * a.cmax + c) * stride;
 #pragma unroll
-    for (int gi = 0; gi < GQ; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
         mine[gi * (D + 2) + tid] = o[gi];
         if (tid == 0) {
             mine[gi * (D + 2) + D] = m[gi];
@@ -608,52 +633,69 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     __syncthreads();
     if (tid == 0) {
         __threadfence();
-        const uint32_t ticket = atomicAdd(a.counters + kvh, 1u);
+        const uint32_t ticket = atomicAdd(a.counters + slot, 1u);
         last = ticket == chunks - 1;
     }
     __syncthreads();
     if (!last) return;
     __threadfence();
-    const float* all = a.part + (size_t)kvh * a.cmax * stride;
+    const float* all = a.part + (size_t)slot * a.cmax * stride;
     // chunk maxima and sums into LDS (one load per thread), then the weights exp(m_c - M)
-    for (uint32_t i = tid; i < chunks * GQ; i += blockDim.x) {
-        const uint32_t k = i / GQ, gi = i % GQ;
+    for (uint32_t i = tid; i < chunks * G; i += blockDim.x) {
+        const uint32_t k = i / G, gi = i % G;
         cw[gi][k] = all[k * stride + gi * (D + 2) + D];
         vred[0][gi][k] = all[k * stride + gi * (D + 2) + D + 1];
     }
     __syncthreads();
-    float M[GQ], L[GQ];
+    float M[G], L[G];
 #pragma unroll
-    for (int gi = 0; gi < GQ; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
         M[gi] = -INFINITY;
         for (uint32_t k = 0; k < chunks; ++k) M[gi] = fmaxf(M[gi], cw[gi][k]);
     }
     __syncthreads();
-    for (uint32_t i = tid; i < chunks * GQ; i += blockDim.x) {
-        const uint32_t k = i / GQ, gi = i % GQ;
+    for (uint32_t i = tid; i < chunks * G; i += blockDim.x) {
+        const uint32_t k = i / G, gi = i % G;
         cw[gi][k] = expf(cw[gi][k] - M[gi]);
     }
     __syncthreads();
 #pragma unroll
-    for (int gi = 0; gi < GQ; ++gi) {
+    for (int gi = 0; gi < G; ++gi) {
         L[gi] = 0.0f;
         for (uint32_t k = 0; k < chunks; ++k) L[gi] = fmaf(cw[gi][k], vred[0][gi][k], L[gi]);
         float acc = 0.0f;
 #pragma unroll 8
         for (uint32_t k = 0; k < chunks; ++k) acc = fmaf(cw[gi][k], all[k * stride + gi * (D + 2) + tid], acc);
-        a.out[(size_t)(kvh * GQ + gi) * D + tid] = acc / L[gi];
+        a.out[(size_t)(qh0 + gi) * D + tid] = acc / L[gi];
     }
-    if (tid == 0) a.counters[kvh] = 0u;
+    if (tid == 0) a.counters[slot] = 0u;
+}
+
+// Query heads per attention block: all of a KV head's at width 256 (1, 2 or 4), two at width 512
+// (one for a single query head per KV head), so the block's LDS stays within bounds.
+uint32_t attention_block_heads(uint32_t group, uint32_t head_width) {
+    return head_width == 256 ? group : std::min<uint32_t>(group, 2u);
 }
 
 hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s) {
-    if (head_width != 256) return hipErrorInvalidValue;
-    const dim3 grid(a.cmax, a.kv_heads);
-    switch (group) {
-        case 1: hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((attention_kernel<256, 2>), grid, dim3(256), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((attention_kernel<256, 4>), grid, dim3(256), 0, s, a); break;
-        default: return hipErrorInvalidValue;
+    const uint32_t G = attention_block_heads(group, head_width);
+    if (a.group != group || group % G) return hipErrorInvalidValue;
+    const dim3 grid(a.cmax, a.kv_heads * (group / G));
+    if (head_width == 256) {
+        switch (G) {
+            case 1: hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a); break;
+            case 2: hipLaunchKernelGGL((attention_kernel<256, 2>), grid, dim3(256), 0, s, a); break;
+            case 4: hipLaunchKernelGGL((attention_kernel<256, 4>), grid, dim3(256), 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else if (head_width == 512) {
+        switch (G) {
+            case 1: hipLaunchKernelGGL((attention_kernel<512, 1>), grid, dim3(512), 0, s, a); break;
+            case 2: hipLaunchKernelGGL((attention_kernel<512, 2>), grid, dim3(512), 0, s, a); break;
+            default: return hipErrorInvalidValue;
+        }
+    } else {
+        return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
@@ -708,6 +750,19 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, uint32_t n
 
 hipError_t launch_zero_words(uint32_t* p, uint32_t n, hipStream_t s) {
     hipLaunchKernelGGL(zero_words_kernel, dim3(1), dim3(256), 0, s, p, n);
+    return hipGetLastError();
+}
+
+// Final logit softcapping, crates/domain/src/q6.rs:66-71: y = tanh(x / cap) * cap, the quotient and
+// product in f32 as the reference computes them and tanh in double rounded to f32.
+__global__ __launch_bounds__(256) void softcap_kernel(const float* x, float* y, size_t n, float cap) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        y[i] = __fmul_rn((float)tanh((double)__fdiv_rn(x[i], cap)), cap);
+}
+
+hipError_t launch_softcap(const float* x, float* y, size_t n, float cap, hipStream_t s) {
+    const size_t blocks = std::min<size_t>((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(softcap_kernel, dim3((uint32_t)blocks), dim3(256), 0, s, x, y, n, cap);
     return hipGetLastError();
 }
 

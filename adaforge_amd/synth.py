@@ -135,7 +135,7 @@ class SynthModel:
 
 def model(name="gemma3-12b", layers=48, hidden=3840, intermediate=15360, q_heads=16, kv_heads=8, head_width=256,
           vocabulary=262144, window=1024, local_theta=1e4, global_theta=1e6, global_every=6, scale=None,
-          table_d=(1e-6, 1e-5), v_norm=False, rope_context=131072, base=BASE_SEED, signed_q4=True):
+          table_d=(1e-7, 1e-6), v_norm=False, rope_context=131072, base=BASE_SEED, signed_q4=True, final_scale=100.0):
     """Gemma-3-12B-shaped decode model with seeded random weights (BASELINE config 4 at the defaults).
 
     Layer i is global iff i % global_every == global_every - 1 (layers 5, 11, ..., 47); the others
@@ -149,9 +149,14 @@ def model(name="gemma3-12b", layers=48, hidden=3840, intermediate=15360, q_heads
       run then repeats one id whatever the context).
     * The tied Q6_K table uses d ~ U[table_d].  The sqrt(hidden)-scaled embedding of the input
       token adds about 770 sigma_w / rms(h) times the typical winning logit to that token's own
-      logit (sigma_w: the table's weight scale, h: the final residual); at config 2's
-      [1e-4, 5e-3] the model only repeats its input, and even at [1e-5, 1e-4] a token, once
-      emitted, keeps winning.  At [1e-6, 1e-5] the bonus is about 0.15 of it."""
+      logit (sigma_w: the table's weight scale, h: the final residual), while the top two of
+      262144 logits lie a few per cent apart: at config 2's [1e-4, 5e-3] the model only repeats
+      its input, at [1e-6, 1e-5] (a bonus of about 0.15) an emitted token still tends to repeat
+      (21 distinct ids in 256 greedy steps), and at the default [1e-7, 1e-6] (about 0.015) the
+      run has 47 distinct ids.
+    * The final norm weights are final_scale (1 + N(0, 0.1)).  The logits scale with them and the
+      residual stream does not, so the default 100 lifts every top-2 logit margin of the 256-step
+      run above 2.5e-3, well clear of the GPU-vs-oracle tolerance."""
     if scale is None:
         scale = 1.0 / float(np.sqrt(head_width))
     p = f"{name}."
@@ -187,7 +192,66 @@ def model(name="gemma3-12b", layers=48, hidden=3840, intermediate=15360, q_heads
         ))
     return SynthModel(hidden=hidden, intermediate=intermediate, vocabulary=vocabulary,
                       table=q6(p + "token_embd", hidden, vocabulary, table_d[0], table_d[1], base=base),
-                      final_norm=nw("output_norm", hidden), final_eps=1e-6, layers=layer_list)
+                      final_norm=(nw("output_norm", hidden) * np.float32(final_scale)).astype(np.float32), final_eps=1e-6,
+                      layers=layer_list)
+
+
+def gemma4_rope_factors(width, rotating=64):
+    """Gemma 4's proportional RoPE on its global layers (README.md:150, rope_freqs.weight): the first
+    `rotating` pairs turn with factor 1, the other width / 2 - rotating pairs carry a factor of 1e30,
+    which all but stops their rotation."""
+    f = np.full(width // 2, 1e30, dtype=np.float32)
+    f[:rotating] = 1.0
+    return f
+
+
+def gemma4_model(name="gemma4", layers=6, hidden=1024, intermediate=2048, local_q=(4, 2, 256), global_q=(4, 1, 512),
+                 vocabulary=2048, window=16, global_every=6, table_d=(1e-7, 1e-6), final_scale=100.0,
+                 base=BASE_SEED):
+    """A Gemma-4-shaped model (the reference's own model family, README.md:135-150,
+    crates/application/src/stack.rs:26-107): local layers of local_q = (query heads, KV heads,
+    width) with a sliding window and RoPE base 1e4; every `global_every`-th layer global, with
+    global_q's geometry (one KV head of width 512 at full size), V computed with K's weights (no V
+    tensor), RoPE base 1e6 with gemma4_rope_factors; attention scale 1.0 and unit-weight V RMSNorm
+    on every layer; final logit softcap 30.  The full-size model is gemma4_model(layers=48,
+    hidden=3840, intermediate=15360, local_q=(16, 8, 256), global_q=(16, 1, 512), vocabulary=262144,
+    window=1024)."""
+    p = f"{name}."
+
+    def nw(tag, n):
+        return normal(p + tag, n, 1.0, 0.1, base)
+
+    out = []
+    for i in range(layers):
+        is_global = (i % global_every) == global_every - 1
+        qh, kvh, hw = global_q if is_global else local_q
+        L = f"blk.{i}."
+        out.append(SynthLayer(
+            input_norm=nw(L + "attn_norm", hidden),
+            q=q4(p + L + "attn_q", hidden, qh * hw, base=base, signed=True),
+            k=q4(p + L + "attn_k", hidden, kvh * hw, base=base, signed=True),
+            v=None if is_global else q4(p + L + "attn_v", hidden, kvh * hw, base=base, signed=True),
+            q_norm=nw(L + "attn_q_norm", hw),
+            k_norm=nw(L + "attn_k_norm", hw),
+            rope_base=1e6 if is_global else 1e4,
+            rope_factors=gemma4_rope_factors(hw) if is_global else np.ones(hw // 2, dtype=np.float32),
+            rope_context=131072,
+            q_heads=qh, kv_heads=kvh, head_width=hw,
+            window=None if is_global else window,
+            scale=1.0,
+            o=q4(p + L + "attn_output", qh * hw, hidden, base=base, signed=True),
+            post_attn_norm=nw(L + "post_attention_norm", hidden),
+            ffn_norm=nw(L + "ffn_norm", hidden),
+            gate=q4(p + L + "ffn_gate", hidden, intermediate, base=base, signed=True),
+            up=q4(p + L + "ffn_up", hidden, intermediate, base=base, signed=True),
+            down=q4(p + L + "ffn_down", intermediate, hidden, base=base, signed=True),
+            post_ffn_norm=nw(L + "post_ffw_norm", hidden),
+            v_norm=True,
+        ))
+    return SynthModel(hidden=hidden, intermediate=intermediate, vocabulary=vocabulary,
+                      table=q6(p + "token_embd", hidden, vocabulary, table_d[0], table_d[1], base=base),
+                      final_norm=(nw("output_norm", hidden) * np.float32(final_scale)).astype(np.float32), final_eps=1e-6,
+                      layers=out, cap=30.0)
 
 
 def tiny_model(layers=3, hidden=512, intermediate=1024, q_heads=2, kv_heads=1, head_width=256, vocabulary=1024,

@@ -114,6 +114,11 @@ int af_q6_gemv_argmax_noalloc(const af_q6* m, const float* x, float* logits, uin
 int af_rmsnorm(const float* x, const float* weights, float* y, uint32_t width, uint32_t vectors, float eps,
                void* stream);
 
+/* Final logit softcapping y = tanh(x / cap) * cap over n device floats (crates/domain/src/q6.rs:66-71;
+ * the GPU half of the capped logits ResidentHead / logits::check report, crates/cuda-backend/src/
+ * logits.rs:70-201).  Greedy selection uses the raw logits (logits.rs:267-276). */
+int af_softcap(const float* x, float* y, size_t n, float cap, void* stream);
+
 /* Host-side weight descriptors, mirroring the domain types the ports borrow
  * (crates/application/src/lib.rs:919-927, 1049-1053). */
 typedef struct {
