@@ -87,6 +87,23 @@ class KernelTiming(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char * 32), ("launches", u64), ("total_ms", f64), ("bytes_per_launch", f64)]
 
 
+class GgufFile(ctypes.Structure):
+    _fields_ = [("version", u32), ("tensors", u64), ("metadata", u64), ("data_offset", u64), ("file_bytes", u64)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("type", u32), ("n_dims", u32), ("dims", u64 * 4), ("offset", u64), ("bytes", u64)]
+
+
+class GgufValue(ctypes.Structure):
+    _fields_ = [("kind", i32), ("u", u64), ("i", ctypes.c_int64), ("f", f64), ("text", ctypes.c_void_p),
+                ("length", u64), ("element_type", u32)]
+
+
+AF_GGUF_WHOLE = 0xFFFFFFFFFFFFFFFF
+GGUF_UNSIGNED, GGUF_SIGNED, GGUF_FLOAT, GGUF_BOOL, GGUF_TEXT, GGUF_ARRAY, GGUF_ARRAY_SUMMARY = range(7)
+GGUF_F32, GGUF_F16, GGUF_Q4_0, GGUF_Q8_0, GGUF_Q6_K, GGUF_BF16 = 0, 1, 2, 8, 14, 30
+
 TOKEN_FN = ctypes.CFUNCTYPE(None, P, u32)
 
 # name -> (restype, argtypes): every function include/af.h declares.
@@ -118,6 +135,15 @@ SIGNATURES = {
     "af_session_trace": (i32, [P, u32p, sz, f32p, u16p, f32p, f32p]),
     "af_session_profile": (i32, [P, u32p, sz, u32, u32p, ctypes.POINTER(sz), ctypes.POINTER(KernelTiming), sz,
                                  ctypes.POINTER(sz)]),
+    "af_gguf_open": (i32, [ctypes.c_char_p, ctypes.POINTER(P)]),
+    "af_gguf_close": (None, [P]),
+    "af_gguf_info": (i32, [P, ctypes.POINTER(GgufFile)]),
+    "af_gguf_tensor_at": (i32, [P, u64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(GgufTensor)]),
+    "af_gguf_tensor": (i32, [P, ctypes.c_char_p, ctypes.POINTER(GgufTensor)]),
+    "af_gguf_read": (i32, [P, ctypes.c_char_p, u64, P, u64]),
+    "af_gguf_meta_at": (i32, [P, u64, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(GgufValue)]),
+    "af_gguf_meta": (i32, [P, ctypes.c_char_p, u64, ctypes.POINTER(GgufValue)]),
+    "af_gguf_session_open": (i32, [P, u32, ctypes.POINTER(P)]),
 }
 
 _lib = None

@@ -165,6 +165,10 @@ struct AttnArgs {
     uint32_t group;          // query heads per KV head
 };
 
+// The C ABI's thread-local error message (af_last_error), set by every entry point that fails;
+// returns code.
+int set_error(int code, std::string msg);
+
 // ---- launchers (kernels.hip) -----------------------------------------------------------------
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s);

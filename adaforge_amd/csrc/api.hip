@@ -29,6 +29,12 @@ int fail(int code, std::string msg) {
     return code;
 }
 
+}  // namespace
+
+int af::set_error(int code, std::string msg) { return fail(code, std::move(msg)); }
+
+namespace {
+
 #define HIP_OK(expr, what)                                                                   \
     do {                                                                                     \
         hipError_t e_ = (expr);                                                              \

@@ -282,6 +282,72 @@ int af_generate(const af_layer_weights* layers, uint32_t n_layers, const af_outp
 int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_outputs, uint16_t* kv_appended,
                      float* logits, float* hidden);
 
+/* ---- GGUF model files: GgufInspector (crates/model-formats/src/gguf.rs:10-540) and the Gemma 4
+ *      layer assembly of crates/application/src/stack.rs:26-107 -------------------------------------- */
+/* Tensor types (GGUF type ids; crates/domain/src/lib.rs:12-20 block layouts). */
+#define AF_GGUF_F32 0u
+#define AF_GGUF_F16 1u
+#define AF_GGUF_Q4_0 2u
+#define AF_GGUF_Q8_0 8u
+#define AF_GGUF_Q6_K 14u
+#define AF_GGUF_BF16 30u
+/* Metadata value kinds (MetadataValue, crates/application/src/lib.rs): arrays of at most 4096
+ * elements are kept (AF_GGUF_ARRAY), larger ones are summarised (AF_GGUF_ARRAY_SUMMARY). */
+#define AF_GGUF_UNSIGNED 0
+#define AF_GGUF_SIGNED 1
+#define AF_GGUF_FLOAT 2
+#define AF_GGUF_BOOL 3
+#define AF_GGUF_TEXT 4
+#define AF_GGUF_ARRAY 5
+#define AF_GGUF_ARRAY_SUMMARY 6
+#define AF_GGUF_WHOLE UINT64_MAX /* af_gguf_meta: the value itself rather than one array element */
+typedef struct af_gguf af_gguf;  /* an indexed GGUF file, memory-mapped read-only */
+typedef struct {
+    uint32_t version;
+    uint64_t tensors, metadata, data_offset, file_bytes;
+} af_gguf_file;                   /* ModelInfo's header fields */
+typedef struct {
+    uint32_t type;                /* AF_GGUF_* tensor type */
+    uint32_t n_dims;
+    uint64_t dims[4];             /* contiguous dimension first (columns, rows) */
+    uint64_t offset;              /* absolute file offset */
+    uint64_t bytes;
+} af_gguf_tensor_info;            /* TensorInfo (crates/domain/src/lib.rs) */
+typedef struct {
+    int32_t kind;                 /* AF_GGUF_UNSIGNED ... AF_GGUF_ARRAY_SUMMARY */
+    uint64_t u;                   /* UNSIGNED; BOOL as 0 / 1 */
+    int64_t i;                    /* SIGNED */
+    double f;                     /* FLOAT */
+    const char* text;             /* TEXT (owned by the af_gguf; not NUL-terminated when it holds NULs) */
+    uint64_t length;              /* TEXT bytes, or ARRAY / ARRAY_SUMMARY elements */
+    uint32_t element_type;        /* ARRAY / ARRAY_SUMMARY: GGUF type id of the elements */
+} af_gguf_value;
+/* GgufInspector::inspect (gguf.rs:419-540): reads and validates the header of a little-endian GGUF
+ * v3 file (signature, version, at most 100000 tensors and keys, unique keys and tensor names,
+ * general.alignment a power of two up to 1 MiB, known tensor types with whole blocks per row,
+ * aligned offsets, every tensor inside the file, no overlaps, a 256 MiB header budget). */
+int af_gguf_open(const char* path, af_gguf** out);
+void af_gguf_close(af_gguf* g);
+int af_gguf_info(const af_gguf* g, af_gguf_file* out);
+/* Tensor `index` (file order) or tensor `name`. */
+int af_gguf_tensor_at(const af_gguf* g, uint64_t index, const char** name, af_gguf_tensor_info* out);
+int af_gguf_tensor(const af_gguf* g, const char* name, af_gguf_tensor_info* out);
+/* len bytes of tensor `name` from byte `offset` (read_q4_matrix / read_q6_matrix / read_f32_vector /
+ * read_rms_norm / read_embeddings take their bytes this way, gguf.rs:44-391). */
+int af_gguf_read(const af_gguf* g, const char* name, uint64_t offset, void* dst, uint64_t len);
+/* Metadata entry `index` (key order) or `key`; for a kept array, `element` selects one element
+ * (AF_GGUF_WHOLE: the array itself). */
+int af_gguf_meta_at(const af_gguf* g, uint64_t index, const char** key, af_gguf_value* out);
+int af_gguf_meta(const af_gguf* g, const char* key, uint64_t element, af_gguf_value* out);
+/* The generation session of a Gemma 4 file (load_generation + GpuDiagnostics::open_session,
+ * crates/application/src/stack.rs:318-357, lib.rs:29-36): every block assembled as stack.rs:26-107
+ * (V from K's weights when attn_v is absent, local layers' sliding window and RoPE base
+ * freq_base_swa with unit factors, global layers' freq_base and rope_freqs factors, attention scale
+ * 1.0, unit-weight V RMSNorm, optional layer_output_scale, the file's RMSNorm epsilon), the tied
+ * Q6_K token_embd table as embedding and lm-head, final_logit_softcapping as the head's cap.  The
+ * session owns device copies; the af_gguf may be closed afterwards. */
+int af_gguf_session_open(const af_gguf* g, uint32_t capacity, af_session** out);
+
 #ifdef __cplusplus
 }
 #endif
