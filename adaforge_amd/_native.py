@@ -115,6 +115,7 @@ SIGNATURES = {
     "af_q4_upload": (i32, [u8p, sz, u32, u32, ctypes.POINTER(P)]),
     "af_q4_free": (None, [P]),
     "af_q4_gemv": (i32, [P, P, P, P]),
+    "af_q4_gemm": (i32, [P, P, u32, P, P]),
     "af_q6_upload": (i32, [u8p, sz, u32, u32, ctypes.POINTER(P)]),
     "af_q6_free": (None, [P]),
     "af_q6_gemv_argmax": (i32, [P, P, P, P, P]),

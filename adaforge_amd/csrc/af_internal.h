@@ -169,6 +169,55 @@ struct AttnArgs {
 // returns code.
 int set_error(int code, std::string msg);
 
+// ---- batched prefill (batch.hip) ---------------------------------------------------------------
+//
+// Digit image of T vectors of nb blocks: planes img[((b T + t) 4 + i) 32 + j] (digit i of element
+// j of block b of vector t), then BlockTab tabs[b T + t] at img + nb T 128.
+constexpr uint32_t kBatchMax = 32;  // tokens per batch (crates/cuda-backend/src/batch.rs MAX_BATCH)
+
+struct BlockTab {
+    float s14;    // s_b 2^-14: scale of 2^14 D0 + 2^7 D1 + D2
+    float s21;    // s_b 2^-21: scale of D3
+    float nbias;  // -8 sum_j x_j
+    float pad;
+};
+
+enum BatchInputKind : int { BI_PLAIN = 0, BI_RESID = 1, BI_EMBED = 2 };
+
+struct BatchIn {
+    int mode;               // BatchInputKind
+    uint32_t T, K, nb;      // vectors, elements, image blocks (>= K / 32, the GEMM's nst * 4)
+    size_t stride;          // floats between the vectors of x, res and x_out
+    const float* x;
+    const float* res;
+    const float* w_a;
+    float eps_a;
+    float scale;
+    const float* w_n;       // null: no RMSNorm of the input
+    float eps_n;
+    float* x_out;
+    float* snap;            // optional copy of x_out (layer outputs for tracing)
+    size_t snap_stride;
+    Q6View table;
+    const uint32_t* ids;
+    uint32_t pos0;          // BI_EMBED: vector t is row ids[pos0 + t]
+    float emb_scale;
+    int8_t* img;
+};
+
+struct BatchGemm {
+    Q4View w, w2;           // w2: the up matrix of a gate/up pair
+    const int8_t* img;      // digit image of T vectors of w.nst * 4 blocks
+    uint32_t T, rows;       // rows of y written (the pair's output width for gate/up)
+    float* y;               // y[t * y_stride + r]
+    size_t y_stride;
+    const float* add;       // optional residual added to y (same layout)
+};
+
+size_t batch_image_bytes(uint32_t nst, uint32_t tokens);
+hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s);
+hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s);
+
 // ---- launchers (kernels.hip) -----------------------------------------------------------------
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s);

@@ -364,6 +364,7 @@ float median_of(std::vector<float> t) {
 struct Scratch {
     std::mutex mu;
     DevMem head_partial, head_counter, attn_part, attn_counters;
+    DevMem batch_image;                 // digit image of af_q4_gemm's inputs
     DevMem attn_freq;                   // the last RoPE inverse frequencies of af_attention_decode
     std::vector<double> attn_freq_host; // their host copy (re-uploaded only when they change)
 };
@@ -456,6 +457,36 @@ int af_q4_gemv(const af_q4* m, const float* x, float* y, void* stream) {
     a.in.x = x;
     a.y = y;
     HIP_OK(launch_q4_gemv(a, IN_PLAIN, OUT_PLAIN, m->m.rows, (hipStream_t)stream), "Q4_0 GEMV launch");
+    return AF_OK;
+}
+
+int af_q4_gemm(const af_q4* m, const float* x, uint32_t tokens, float* y, void* stream) {
+    if (!m || !x || !y) return fail(AF_ERR_INVALID, "null argument");
+    if (tokens == 0 || tokens > kBatchMax)
+        return fail(AF_ERR_INVALID, "batched GEMV takes 1 to " + std::to_string(kBatchMax) + " vectors");
+    const Q4View w = m->m.view();
+    std::lock_guard<std::mutex> lock(g_scratch.mu);
+    int rc;
+    if ((rc = grow(g_scratch.batch_image, batch_image_bytes(w.nst, kBatchMax), false, "batch digit image")))
+        return rc;
+    const hipStream_t s = (hipStream_t)stream;
+    BatchIn in{};
+    in.mode = BI_PLAIN;
+    in.T = tokens;
+    in.K = w.blocks * 32;
+    in.nb = w.nst * 4;
+    in.stride = in.K;
+    in.x = x;
+    in.img = g_scratch.batch_image.as<int8_t>();
+    HIP_OK(launch_batch_digits(in, s), "batched GEMV input digits");
+    BatchGemm g{};
+    g.w = w;
+    g.img = in.img;
+    g.T = tokens;
+    g.rows = w.rows;
+    g.y = y;
+    g.y_stride = w.rows;
+    HIP_OK(launch_batch_gemm(g, false, s), "batched GEMV launch");
     return AF_OK;
 }
 

@@ -185,9 +185,10 @@ __device__ __forceinline__ uint32_t q6_codes(uint32_t a, uint32_t b, uint32_t h,
 
 // Embedding row (Q6_K, repacked) times emb_scale into xs; one thread per unit dword (16
 // elements), threads first, first + step, ... of the caller's range.
-__device__ inline void embed_row(const InputStage& in, float* xs, uint32_t first, uint32_t step) {
-    const Q6View& t = in.table;
-    const uint32_t row = min(gp(in.ids)[gp(in.state)[ST_POS]], t.rows - 1);  // ids are validated; never read past the table
+// Table row `row`, dequantised and times emb_scale, into xs (elements first, first + step, ...).
+__device__ inline void embed_row_at(const Q6View& t, uint32_t row, float emb_scale, float* xs, uint32_t first,
+                                    uint32_t step) {
+    row = min(row, t.rows - 1);  // ids are validated; never read past the table
     const uint32_t units = t.units, sblocks = units / 4;
     const auto* A = gp(reinterpret_cast<const uint32_t*>(t.a + (size_t)row * units * 16));
     const auto* B = gp(reinterpret_cast<const uint32_t*>(t.b + (size_t)row * units * 16));
@@ -206,10 +207,15 @@ __device__ inline void embed_row(const InputStage& in, float* xs, uint32_t first
             for (int n = 0; n < 4; ++n) {
                 const int code = (int)((c >> (8 * n)) & 0xFF) - 32;
                 const uint32_t e = sb * 256 + g * 128 + q * 32 + hh * 16 + 4 * k + n;
-                xs[e] = __fmul_rn(__fmul_rn(ds, (float)code), in.emb_scale);
+                xs[e] = __fmul_rn(__fmul_rn(ds, (float)code), emb_scale);
             }
         }
     }
+}
+
+// The row of the token at the session position (ids[state[ST_POS]]).
+__device__ inline void embed_row(const InputStage& in, float* xs, uint32_t first, uint32_t step) {
+    embed_row_at(in.table, gp(in.ids)[gp(in.state)[ST_POS]], in.emb_scale, xs, first, step);
 }
 
 // Loads N float4 per thread from p at float4 indices base + j * blockDim + thread (zero past n4).

@@ -87,6 +87,11 @@ int af_q4_upload(const uint8_t* q4, size_t len, uint32_t columns, uint32_t rows,
 void af_q4_free(af_q4* m);
 /* y[rows] = W x[columns] (kernels/ada/q4_matvec.cu q4_matvec, launched by matvec.rs:72-101). */
 int af_q4_gemv(const af_q4* m, const float* x, float* y, void* stream);
+/* y[t][rows] = W x[t][columns] for t < tokens, 1 <= tokens <= 32, with W read once for all
+ * vectors (crates/cuda-backend/src/batch.rs:113-148 BatchKernels::matvec, MAX_BATCH = 32 at
+ * batch.rs:10; kernels/ada/q4_batch.cu).  The vectors' digit image lives in library scratch shared by
+ * all calls: calls that overlap on different streams race. */
+int af_q4_gemm(const af_q4* m, const float* x, uint32_t tokens, float* y, void* stream);
 
 /* Q6Matrix upload (crates/domain/src/q6.rs:8-20; crates/cuda-backend/src/logits.rs:292-316). */
 int af_q6_upload(const uint8_t* q6, size_t len, uint32_t columns, uint32_t rows, af_q6** out);
