@@ -156,13 +156,22 @@ struct AttnArgs {
     const uint32_t* state;   // non-null: position = state[ST_POS]
     uint32_t position;
     float* out;              // [q_heads][head_width]
-    float* part;             // [kv_heads * group / G][cmax][G][head_width + 2] (G: attention_block_heads)
-    uint32_t* counters;      // [kv_heads * group / G]
+    float* part;             // [tokens][kv_heads * group / G][cmax][G][head_width + 2] (G: attention_block_heads)
+    uint32_t* counters;      // [tokens][kv_heads * group / G], zero between launches
     int8_t* dig_out;         // digit image of `out` for the output projection (may be null)
     uint32_t cmax;
     uint32_t min_chunk;
     uint32_t kv_heads;
     uint32_t group;          // query heads per KV head
+    int mode;                // AttnMode
+    size_t in_stride;        // batch: floats between the tokens' q / k / v rows
+    size_t out_stride;       // batch: floats between the tokens' outputs
+};
+
+enum AttnMode : int {
+    ATT_DECODE = 0,  // append the new K/V, attend
+    ATT_APPEND = 1,  // append only
+    ATT_ATTEND = 2,  // attend, every position's K/V already appended
 };
 
 // The C ABI's thread-local error message (af_last_error), set by every entry point that fails;
@@ -171,22 +180,18 @@ int set_error(int code, std::string msg);
 
 // ---- batched prefill (batch.hip) ---------------------------------------------------------------
 //
-// Digit image of T vectors of nb blocks: planes img[((b T + t) 4 + i) 32 + j] (digit i of element
-// j of block b of vector t), then BlockTab tabs[b T + t] at img + nb T 128.
+// Digit image of T vectors of nb 32-element blocks for the batched GEMV, with the tokens padded to
+// Tp = 16 ceil(T / 16) (padding tokens all zero): block b of vector t in the digit form of the decode
+// GEMV, s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21), s = 2^(ilogb(max |x_b|) - 5):
+//   planes img[((b 4 + i) Tp + t) 32 + j]   digit i of element j
+//   tabs   float2 at img + nb 4 Tp 32, [b Tp + t] = {s 2^-14, -8 sum_j x_j}
 constexpr uint32_t kBatchMax = 32;  // tokens per batch (crates/cuda-backend/src/batch.rs MAX_BATCH)
-
-struct BlockTab {
-    float s14;    // s_b 2^-14: scale of 2^14 D0 + 2^7 D1 + D2
-    float s21;    // s_b 2^-21: scale of D3
-    float nbias;  // -8 sum_j x_j
-    float pad;
-};
 
 enum BatchInputKind : int { BI_PLAIN = 0, BI_RESID = 1, BI_EMBED = 2 };
 
 struct BatchIn {
     int mode;               // BatchInputKind
-    uint32_t T, K, nb;      // vectors, elements, image blocks (>= K / 32, the GEMM's nst * 4)
+    uint32_t T, K;          // vectors, elements (a multiple of 32)
     size_t stride;          // floats between the vectors of x, res and x_out
     const float* x;
     const float* res;
@@ -207,21 +212,24 @@ struct BatchIn {
 
 struct BatchGemm {
     Q4View w, w2;           // w2: the up matrix of a gate/up pair
-    const int8_t* img;      // digit image of T vectors of w.nst * 4 blocks
-    uint32_t T, rows;       // rows of y written (the pair's output width for gate/up)
-    float* y;               // y[t * y_stride + r]
+    const int8_t* img;      // digit image of T vectors of w.blocks blocks
+    uint32_t T;
+    float* y;               // y[t * y_stride + r], r < w.rows (gate/up: f32(gelu(gate)) * up)
     size_t y_stride;
     const float* add;       // optional residual added to y (same layout)
+    float* part;            // split-K partials (batch_gemm_part_bytes)
 };
 
-size_t batch_image_bytes(uint32_t nst, uint32_t tokens);
+size_t batch_image_bytes(uint32_t blocks, uint32_t tokens);
+size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair);
 hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s);
 hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s);
 
 // ---- launchers (kernels.hip) -----------------------------------------------------------------
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s);
-hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s);
+hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s,
+                            uint32_t tokens = 1);
 uint32_t attention_block_heads(uint32_t group, uint32_t head_width);
 hipError_t launch_rmsnorm(const float* x, const float* w, float* y, uint32_t width, uint32_t vectors, float eps,
                           hipStream_t s);

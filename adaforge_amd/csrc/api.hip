@@ -364,7 +364,7 @@ float median_of(std::vector<float> t) {
 struct Scratch {
     std::mutex mu;
     DevMem head_partial, head_counter, attn_part, attn_counters;
-    DevMem batch_image;                 // digit image of af_q4_gemm's inputs
+    DevMem batch_image, batch_part;     // digit image and split-K partials of af_q4_gemm
     DevMem attn_freq;                   // the last RoPE inverse frequencies of af_attention_decode
     std::vector<double> attn_freq_host; // their host copy (re-uploaded only when they change)
 };
@@ -467,14 +467,16 @@ int af_q4_gemm(const af_q4* m, const float* x, uint32_t tokens, float* y, void* 
     const Q4View w = m->m.view();
     std::lock_guard<std::mutex> lock(g_scratch.mu);
     int rc;
-    if ((rc = grow(g_scratch.batch_image, batch_image_bytes(w.nst, kBatchMax), false, "batch digit image")))
+    if ((rc = grow(g_scratch.batch_image, batch_image_bytes(w.blocks, kBatchMax), false, "batch digit image")))
+        return rc;
+    if ((rc = grow(g_scratch.batch_part, batch_gemm_part_bytes(w.rows, w.blocks, kBatchMax, false) + 4, false,
+                   "batch partials")))
         return rc;
     const hipStream_t s = (hipStream_t)stream;
     BatchIn in{};
     in.mode = BI_PLAIN;
     in.T = tokens;
     in.K = w.blocks * 32;
-    in.nb = w.nst * 4;
     in.stride = in.K;
     in.x = x;
     in.img = g_scratch.batch_image.as<int8_t>();
@@ -483,9 +485,9 @@ int af_q4_gemm(const af_q4* m, const float* x, uint32_t tokens, float* y, void* 
     g.w = w;
     g.img = in.img;
     g.T = tokens;
-    g.rows = w.rows;
     g.y = y;
     g.y_stride = w.rows;
+    g.part = g_scratch.batch_part.as<float>();
     HIP_OK(launch_batch_gemm(g, false, s), "batched GEMV launch");
     return AF_OK;
 }
@@ -919,6 +921,13 @@ struct af_session {
     bool poisoned = false;
     bool use_graphs = true;
     KernelTimer* timer = nullptr;  // set during af_session_profile
+    // Batched prefill (batch.hip): prompt positions run through the layers up to kBatchMax at a time,
+    // every weight read once per batch.  prefill_batch: positions per batch for generation
+    // (AF_PREFILL_BATCH, default kBatchMax; 0 or 1 prefills one position per step-kernel launch);
+    // trace_batch: the same for af_session_trace (AF_TRACE_BATCH, default 0: the step kernel).
+    uint32_t prefill_batch = kBatchMax, trace_batch = 0;
+    uint32_t max_qh = 0, max_qh_part = 0;
+    DevMem XB, HB, QKVB, ATTB, PROJB, ACTB, DB, BIMG, BGEMM, BPART, BCOUNT;
 
     // Launches f(); when profiling, brackets it with an event pair tagged with its kind and bytes.
     template <typename F>
@@ -1209,6 +1218,169 @@ struct af_session {
         }
         return AF_OK;
     }
+
+    // Attention chunks of a batch: the tokens already spread the grid, so each (token, KV head)
+    // splits its visible range only past kBatchMinChunk positions, into at most kBatchCmax chunks
+    // (kBatchCmax * kAttnMaxChunkLen covers AF_MAX_CONTEXT).
+    static constexpr uint32_t kBatchCmax = 16, kBatchMinChunk = 256;
+
+    int ensure_batch() {
+        if (XB.p) return AF_OK;
+        uint32_t blocks = std::max({hidden, max_q, intermediate}) / 32;
+        size_t part = 4;
+        for (const LayerDev& L : layers) {
+            part = std::max({part, batch_gemm_part_bytes(L.qkv.rows, hidden / 32, kBatchMax, false),
+                             batch_gemm_part_bytes(L.o.rows, L.qn / 32, kBatchMax, false),
+                             batch_gemm_part_bytes(L.gate.rows, hidden / 32, kBatchMax, true),
+                             batch_gemm_part_bytes(L.down.rows, intermediate / 32, kBatchMax, false)});
+        }
+        const size_t T = kBatchMax;
+        struct {
+            DevMem* m;
+            size_t bytes;
+        } bufs[] = {
+            {&XB, T * hidden * 4},        {&HB, T * hidden * 4},  {&QKVB, T * max_qkv * 4},
+            {&ATTB, T * max_q * 4},       {&PROJB, T * hidden * 4}, {&ACTB, T * intermediate * 4},
+            {&DB, T * hidden * 4},        {&BIMG, batch_image_bytes(blocks, kBatchMax)}, {&BGEMM, part},
+            {&BPART, T * kBatchCmax * max_qh_part * 4}, {&BCOUNT, T * std::max<uint32_t>(max_qh, 64) * 4},
+        };
+        for (auto& b : bufs) {
+            int rc = dev_alloc(*b.m, b.bytes, "batch buffer");
+            if (rc) return rc;
+        }
+        HIP_OK(hipMemsetAsync(BCOUNT.p, 0, BCOUNT.bytes, stream), "batch counters clear");
+        return AF_OK;
+    }
+
+    // Digit image of T vectors for the GEMV of matrix m (see BatchIn).
+    BatchIn batch_in(int mode, uint32_t T, uint32_t K, const float* x, size_t stride) {
+        BatchIn in{};
+        in.mode = mode;
+        in.T = T;
+        in.K = K;
+        in.stride = stride;
+        in.x = x;
+        in.scale = 1.0f;
+        in.img = BIMG.as<int8_t>();
+        return in;
+    }
+
+    hipError_t batch_gemm(const Q4Dev& m, const Q4Dev* m2, uint32_t T, float* y, size_t y_stride) {
+        BatchGemm g{};
+        g.w = m.view();
+        if (m2) g.w2 = m2->view();
+        g.img = BIMG.as<int8_t>();
+        g.T = T;
+        g.y = y;
+        g.y_stride = y_stride;
+        g.part = BGEMM.as<float>();
+        return launch_batch_gemm(g, m2 != nullptr, stream);
+    }
+
+    // Runs positions p0 .. p0 + T - 1 (ids in IDS) through every layer, appending their K/V; leaves
+    // the last layer's down output in DB and FFN residual in HB.  snap: layer outputs [T][layers][hidden]
+    // (null: none).  The decoder layer as the step kernel computes it (crates/cuda-backend/src/stack.rs
+    // 502-700, run_batch), with the GEMVs over the batch.
+    hipError_t enqueue_batch(uint32_t p0, uint32_t T, float* snap) {
+        const size_t H = hidden, nl = layers.size();
+        hipError_t e;
+        for (uint32_t l = 0; l < nl; ++l) {
+            LayerDev& L = layers[l];
+            BatchIn in = batch_in(l == 0 ? BI_EMBED : BI_RESID, T, hidden, l ? DB.as<float>() : nullptr, H);
+            in.w_n = L.input_norm.as<float>();
+            in.eps_n = L.input_eps;
+            in.x_out = XB.as<float>();
+            if (l == 0) {
+                in.table = head.view();
+                in.ids = IDS.as<uint32_t>();
+                in.pos0 = p0;
+                in.emb_scale = emb_scale;
+            } else {
+                const LayerDev& P = layers[l - 1];
+                in.res = HB.as<float>();
+                in.w_a = P.post_ffn.as<float>();
+                in.eps_a = P.post_ffn_eps;
+                in.scale = P.layer_scale;
+                if (snap) {
+                    in.snap = snap + (l - 1) * H;
+                    in.snap_stride = nl * H;
+                }
+            }
+            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = batch_gemm(L.qkv, nullptr, T, QKVB.as<float>(), L.qkv.rows)) != hipSuccess) return e;
+
+            AttnArgs aa{};
+            const float* qkv = QKVB.as<float>();
+            aa.q_raw = qkv;
+            aa.k_raw = qkv + L.qn;
+            aa.v_raw = L.shared_v ? qkv + L.qn : qkv + L.qn + L.kn;
+            aa.in_stride = L.qkv.rows;
+            aa.q_norm = L.q_norm.as<float>();
+            aa.k_norm = L.k_norm.as<float>();
+            aa.q_eps = L.q_eps;
+            aa.k_eps = L.k_eps;
+            aa.v_eps = L.input_eps;
+            aa.v_norm = L.v_norm;
+            aa.inv_freq = L.inv_freq.as<double>();
+            aa.kcache = L.kcache.as<uint16_t>();
+            aa.vcache = L.vcache.as<uint16_t>();
+            aa.ring = L.ring;
+            aa.window = L.window;
+            aa.scale = L.scale;
+            aa.position = p0;
+            aa.out = ATTB.as<float>();
+            aa.out_stride = L.qn;
+            aa.part = BPART.as<float>();
+            aa.counters = BCOUNT.as<uint32_t>();
+            aa.cmax = kBatchCmax;
+            aa.min_chunk = kBatchMinChunk;
+            aa.kv_heads = L.kv_heads;
+            aa.group = L.q_heads / L.kv_heads;
+            aa.mode = ATT_APPEND;
+            if ((e = launch_attention(aa, aa.group, L.width, stream, T)) != hipSuccess) return e;
+            aa.mode = ATT_ATTEND;
+            if ((e = launch_attention(aa, aa.group, L.width, stream, T)) != hipSuccess) return e;
+
+            in = batch_in(BI_PLAIN, T, L.qn, ATTB.as<float>(), L.qn);
+            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = batch_gemm(L.o, nullptr, T, PROJB.as<float>(), H)) != hipSuccess) return e;
+
+            in = batch_in(BI_RESID, T, hidden, PROJB.as<float>(), H);
+            in.res = XB.as<float>();
+            in.w_a = L.post_attn.as<float>();
+            in.eps_a = L.post_attn_eps;
+            in.w_n = L.ffn_norm.as<float>();
+            in.eps_n = L.ffn_eps;
+            in.x_out = HB.as<float>();
+            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = batch_gemm(L.gate, &L.up, T, ACTB.as<float>(), intermediate)) != hipSuccess) return e;
+
+            in = batch_in(BI_PLAIN, T, intermediate, ACTB.as<float>(), intermediate);
+            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = batch_gemm(L.down, nullptr, T, DB.as<float>(), H)) != hipSuccess) return e;
+        }
+        if (!snap) return hipSuccess;
+        // the last layer's output (its image is not used)
+        const LayerDev& P = layers.back();
+        BatchIn in = batch_in(BI_RESID, T, hidden, DB.as<float>(), H);
+        in.res = HB.as<float>();
+        in.w_a = P.post_ffn.as<float>();
+        in.eps_a = P.post_ffn_eps;
+        in.scale = P.layer_scale;
+        in.x_out = XB.as<float>();
+        in.snap = snap + (nl - 1) * H;
+        in.snap_stride = nl * H;
+        return launch_batch_digits(in, stream);
+    }
+
+    // Positions [from, to) through the batched layers (K/V appended), in batches of `batch`.
+    hipError_t prefill_batched(uint32_t from, uint32_t to, uint32_t batch) {
+        for (uint32_t p = from; p < to; p += batch) {
+            hipError_t e = enqueue_batch(p, std::min(batch, to - p), nullptr);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
 };
 
 namespace {
@@ -1373,6 +1545,10 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     // A test of the fall-back path: the step kernel's barrier opening this phase (5 l + 4 opens
     // layer l's down projection) waits for one arrival more than the grid makes, and times out.
     if (const char* fp = std::getenv("AF_STEP_FAIL_PHASE")) s->fail_phase = (uint32_t)std::strtoul(fp, nullptr, 10);
+    if (const char* pb = std::getenv("AF_PREFILL_BATCH"))
+        s->prefill_batch = std::min<uint32_t>((uint32_t)std::strtoul(pb, nullptr, 10), kBatchMax);
+    if (const char* tb = std::getenv("AF_TRACE_BATCH"))
+        s->trace_batch = std::min<uint32_t>((uint32_t)std::strtoul(tb, nullptr, 10), kBatchMax);
     HIP_OK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "session stream");
 
     uint32_t max_kv = 0, max_q = 0, max_group = 1, max_qh_part = 0, max_qh = 0;
@@ -1411,9 +1587,10 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         if ((rc = dev_upload(L.post_ffn, w.ffn.post.weights, (size_t)hidden * 4, "norm upload"))) return rc;
         std::vector<double> f = inverse_frequencies(w.rope);
         if ((rc = dev_upload(L.inv_freq, f.data(), f.size() * 8, "RoPE upload"))) return rc;
-        // Sliding-window layers keep a ring of `window` slots: a decode step never
-        // writes past the token it consumes, so no visible slot is overwritten.
-        L.ring = L.window ? std::min(L.window, capacity) : capacity;
+        // Sliding-window layers keep a ring of window + kBatchMax slots (crates/cuda-backend/src/
+        // stack.rs:94-102): a batch appends up to kBatchMax positions before any of them attends,
+        // and the first still sees its window - 1 predecessors.
+        L.ring = L.window ? std::min(L.window + kBatchMax, capacity) : capacity;
         const size_t kv = (size_t)L.kv_heads * L.ring * L.width * 2;
         if ((rc = dev_alloc(L.kcache, kv, "K cache"))) return rc;
         if ((rc = dev_alloc(L.vcache, kv, "V cache"))) return rc;
@@ -1428,6 +1605,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         s->max_kv_rows = std::max(s->max_kv_rows, L.kn);
     }
     s->max_q = max_q;
+    s->max_qh = max_qh;
+    s->max_qh_part = max_qh_part;
     if ((rc = upload_q6(s->head, hm.bytes, hm.columns, hm.rows))) return rc;
     if ((rc = dev_upload(s->final_norm, head->norm.weights, (size_t)hidden * 4, "final norm"))) return rc;
 
@@ -1535,11 +1714,19 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
            "prompt upload");
     if (n_stop) HIP_OK(hipMemcpyAsync(s->STOPS.p, stop, n_stop * 4, hipMemcpyHostToDevice, st), "stop ids upload");
     std::memset(s->records + P, 0, (size_t)(s->capacity + 2 - P) * sizeof(StepRecord));
-    int rc = s->set_state(pend == 0 ? s->consumed - 1 : s->consumed, (uint32_t)n_stop);
+    // Positions consumed .. P - 2 fill the KV caches: in batches through the batched layers, or one
+    // step-kernel launch (graph replay) each; the decode steps then start at position P - 1.
+    const bool batched = s->prefill_batch > 1 && pend > 1 && !timer;
+    int rc = s->set_state(batched ? P - 1 : pend == 0 ? s->consumed - 1 : s->consumed, (uint32_t)n_stop);
     if (rc) return rc;
-    for (uint32_t i = 0; i + 1 < pend; ++i) HIP_OK(s->run_step(false), "prefill step");
+    if (batched) {
+        if ((rc = s->ensure_batch())) return rc;
+        HIP_OK(s->prefill_batched(s->consumed, P - 1, s->prefill_batch), "batched prefill");
+    } else {
+        for (uint32_t i = 0; i + 1 < pend; ++i) HIP_OK(s->run_step(false), "prefill step");
+    }
     HIP_OK(hipStreamSynchronize(st), "prefill");
-    if (pend > 1) {  // a timed-out step kernel: rerun from its position on the per-operation kernels
+    if (pend > 1 && !batched) {  // a timed-out step kernel: rerun from its position on the per-operation kernels
         bool timed_out = false;
         uint32_t at = 0;
         if ((rc = s->step_timed_out(timed_out, &at))) return rc;
@@ -1833,6 +2020,48 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     run.insert(run.end(), ids, ids + n);
     HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + s->consumed, run.data(), run.size() * 4, hipMemcpyHostToDevice, st),
            "ids upload");
+    if (s->trace_batch > 1) {
+        // every position through the batched layers: layer outputs and appended K/V per batch
+        if ((rc = s->ensure_batch())) return rc;
+        if (layer_outputs && (rc = grow(s->SNAP, (size_t)kBatchMax * nl * H * 4, false, "trace buffer"))) return rc;
+        const uint32_t B = s->trace_batch, first = s->consumed + (uint32_t)pend;
+        HIP_OK(s->prefill_batched(s->consumed, first, B), "trace batch");
+        uint32_t T = 0;
+        for (size_t p = 0; p < n; p += T) {
+            T = (uint32_t)std::min<size_t>(B, n - p);
+            HIP_OK(s->enqueue_batch(first + (uint32_t)p, T, layer_outputs ? s->SNAP.as<float>() : nullptr),
+                   "trace batch");
+            if (layer_outputs)
+                HIP_OK(hipMemcpyAsync(layer_outputs + p * nl * H, s->SNAP.p, (size_t)T * nl * H * 4,
+                                      hipMemcpyDeviceToHost, st),
+                       "trace download");
+            for (uint32_t t = 0; kv_appended && t < T; ++t) {
+                for (uint32_t l = 0; l < nl; ++l) {
+                    const LayerDev& L = s->layers[l];
+                    const size_t slot = (first + p + t) % L.ring, row = (size_t)L.width * 2;
+                    uint8_t* dst = s->KVSNAP.as<uint8_t>() + (size_t)l * 2 * kvr * 2;
+                    HIP_OK(hipMemcpy2DAsync(dst, row, L.kcache.as<uint8_t>() + slot * row, (size_t)L.ring * row, row,
+                                            L.kv_heads, hipMemcpyDeviceToDevice, st),
+                           "trace K/V copy");
+                    HIP_OK(hipMemcpy2DAsync(dst + kvr * 2, row, L.vcache.as<uint8_t>() + slot * row,
+                                            (size_t)L.ring * row, row, L.kv_heads, hipMemcpyDeviceToDevice, st),
+                           "trace K/V copy");
+                }
+                HIP_OK(hipMemcpyAsync(kv_appended + (p + t) * nl * 2 * kvr, s->KVSNAP.p, kv_bytes,
+                                      hipMemcpyDeviceToHost, st),
+                       "trace download");
+            }
+        }
+        // head on the last position's final hidden state (raw logits)
+        HeadArgs h = s->head_args(false, true);
+        h.in.x = s->DB.as<float>() + (size_t)(T - 1) * H;
+        h.in.res = s->HB.as<float>() + (size_t)(T - 1) * H;
+        HIP_OK(launch_head(h, IN_RESID, s->head_blocks, st), "trace head");
+        if (logits)
+            HIP_OK(hipMemcpyAsync(logits, s->LOGITS.p, (size_t)s->vocabulary * 4, hipMemcpyDeviceToHost, st), "logits");
+        if (hidden) HIP_OK(hipMemcpyAsync(hidden, s->X.p, H * 4, hipMemcpyDeviceToHost, st), "hidden");
+        HIP_OK(hipStreamSynchronize(st), "trace");
+    } else
     // A step kernel that times out makes the session fall back to the per-operation kernels, and
     // the whole trace runs again there (it rewrites the same K/V slots).
     for (int attempt = 0; attempt < 2; ++attempt) {

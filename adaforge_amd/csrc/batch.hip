@@ -1,66 +1,95 @@
 // Batched prefill kernels for gfx950: up to kBatchMax prompt tokens through a layer with every
 // weight read once for the whole batch (crates/cuda-backend/src/batch.rs, kernels/ada/q4_batch.cu
-// in the reference, which runs the same per-token arithmetic as its single-token kernels; here the
-// batch runs its own arithmetic, within the reference's tolerance of the FP64 oracle).
+// in the reference).  A layer's batch is a chain of launches: the digit image of every token's GEMV
+// input (batch_digits_kernel, with the residual and RMSNorm prologues), the Q4_0 GEMM over all tokens
+// (batch_gemm_kernel, then batch_reduce_kernel when the GEMM splits K across workgroups), and the
+// attention of all tokens (attention_kernel with one grid z-slice per token, after a pass that
+// appends every token's K and V).
 //
-// A layer's batch is a chain of launches: the digit image of every token's GEMV input
-// (batch_digits_kernel, with the residual and RMSNorm prologues), the Q4_0 GEMM over all tokens
-// (batch_gemm_kernel), the attention of all tokens (attention_kernel with one grid z-slice per
-// token, after a pass that appends every token's K and V), and so on per phase.
-//
-// The GEMM runs on the int8 matrix cores as the decode step does, with the batch in the MFMA's
-// M dimension: v_mfma_i32_16x16x32_i8 with A = the digit planes of four tokens (row m = 4 t + i:
-// digit i of token t) over one 32-weight block (k), B = the block's 32 nibble codes of 16 weight
-// rows.  Each lane then holds the four digit sums of one (token, row) pair of that block, which it
-// folds with the block's input scales and weight scale.  One block per MFMA, so nothing in an MFMA
-// is zero padding.
+// Each token's input is written in the decode step's digit form (digit_words): block b is
+// s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) with s = 2^(ilogb(max |x_b|) - 5), int8 digits, error at most
+// 2^-27 max |x_b|.  The GEMM runs on the int8 matrix cores with the tokens in the MFMA's M
+// dimension: v_mfma_i32_16x16x32_i8 with A = one digit plane of 16 tokens over one 32-weight block
+// (k) and B = the block's raw nibble codes n of 16 weight rows, so D_i[t][r] = sum_j n_rj q_ij(t).
+// Per (token, row, block), I = 2^14 D0 + 2^7 D1 + D2 is exact in int32 and
+//   sum_j (n_rj - 8) x_j = s 2^-14 I + s 2^-21 D3 - 8 sum_j x_j,
+// which each lane folds into its fp32 partial with the block's weight scale d_r.
 #include "device.h"
 
 namespace af {
 
 namespace {
 
-constexpr uint32_t kThreads = 512;
+constexpr uint32_t kGemmThreads = 256;  // four waves splitting the blocks of the workgroup's K range
+constexpr uint32_t kGemmTargetGrid = 512;
 
-// Table entry of a block with max |x| m and element sum `sum`.
-__device__ __forceinline__ BlockTab block_tab_of(float m, float sum) {
+// Table entry of a block with max |x| m and element sum `sum` (digit_words' scale s = 2^(ilogb(m) - 5)):
+// {s 2^-14, -8 sum}.
+__device__ __forceinline__ float2 block_tab(float m, float sum) {
     const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
-    return BlockTab{ldexpf(s, -14), ldexpf(s, -21), -8.0f * sum, 0.0f};
+    return make_float2(ldexpf(s, -14), -8.0f * sum);
+}
+
+uint32_t padded_tokens(uint32_t T) { return (T + 15) / 16 * 16; }
+
+// Work split of a GEMM: R row tiles per workgroup, S workgroups along K (partials summed by
+// batch_reduce_kernel), so that about kGemmTargetGrid workgroups share the weight stream and each
+// wave keeps at least two blocks.
+struct GemmPlan {
+    uint32_t R, S;
+};
+GemmPlan gemm_plan(uint32_t rows, uint32_t blocks) {
+    const uint32_t tiles = (rows + 15) / 16;
+    const uint32_t R = tiles >= kGemmTargetGrid ? 2 : 1;
+    const uint32_t wgs = (tiles + R - 1) / R;
+    uint32_t S = std::max<uint32_t>(1, std::min<uint32_t>(8, kGemmTargetGrid / wgs));
+    S = std::max<uint32_t>(1, std::min(S, blocks / 8));
+    return GemmPlan{R, S};
 }
 
 }  // namespace
 
 // ---- digit images of a batch --------------------------------------------------------------------
 
-// One workgroup per token t.  The input vector of the GEMV that follows:
+// One workgroup per token t < Tp (tokens T..Tp-1 write zeros).  The input vector of the GEMV that
+// follows:
 //   BI_PLAIN: x_t;
 //   BI_RESID: v_t = (f32(rms(x_t) w_a) + res_t) * scale (w_a null: (x_t + res_t) * scale), stored to
 //             x_out_t (the residual stream), then f32(rms(v_t) w_n);
 //   BI_EMBED: v_t = table row ids[pos0 + t] * emb_scale, stored to x_out_t, then f32(rms(v_t) w_n).
 // RMSNorm sums of squares and products in double, f32 results (crates/domain/src/rms_norm.rs:24-41).
-// The image: for block b (32 elements) of token t, digit plane i at img[((b T + t) 4 + i) 32], then
-// after all planes the block's BlockTab {s 2^-14, s 2^-21, -8 sum_j x_j} at tabs[b T + t]; blocks
-// past the vector (up to nb) are zero.
 __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
     extern __shared__ __align__(16) float xs[];  // [K]
     __shared__ double red[8];
-    const uint32_t t = blockIdx.x, tid = threadIdx.x, K = in.K, T = in.T;
-    const float* x = in.x ? in.x + (size_t)t * in.stride : nullptr;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, K = in.K, nb = K / 32, Tp = gridDim.x;
+    int8_t* planes = in.img;
+    float2* tabs = reinterpret_cast<float2*>(in.img + (size_t)nb * 4 * Tp * 32);
+    if (t >= in.T) {
+        for (uint32_t o = tid; o < nb * 4; o += blockDim.x) {
+            const uint32_t b = o >> 2, p = o & 3;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                *reinterpret_cast<v2u*>(planes + (((size_t)b * 4 + i) * Tp + t) * 32 + 8 * p) = v2u{0u, 0u};
+            if (p == 0) tabs[(size_t)b * Tp + t] = make_float2(0.0f, 0.0f);
+        }
+        return;
+    }
     if (in.mode == BI_EMBED) {
-        embed_row_at(in.table, gp(in.ids)[in.pos0 + t], in.emb_scale, xs, tid, kThreads);
+        embed_row_at(in.table, gp(in.ids)[in.pos0 + t], in.emb_scale, xs, tid, blockDim.x);
     } else {
-        for (uint32_t i = tid; i < K; i += kThreads) xs[i] = x[i];
+        const float* x = in.x + (size_t)t * in.stride;
+        for (uint32_t i = tid; i < K; i += blockDim.x) xs[i] = x[i];
     }
     __syncthreads();
     if (in.mode == BI_RESID) {
         double ra = 1.0;
         if (in.w_a) {
             double sa = 0.0;
-            for (uint32_t i = tid; i < K; i += kThreads) sa += (double)xs[i] * (double)xs[i];
+            for (uint32_t i = tid; i < K; i += blockDim.x) sa += (double)xs[i] * (double)xs[i];
             ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
         }
         const float* res = in.res + (size_t)t * in.stride;
-        for (uint32_t i = tid; i < K; i += kThreads) {
+        for (uint32_t i = tid; i < K; i += blockDim.x) {
             const float u = in.w_a ? norm_apply(xs[i], ra, in.w_a[i]) : xs[i];
             xs[i] = __fmul_rn(__fadd_rn(u, res[i]), in.scale);
         }
@@ -68,7 +97,7 @@ __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
     }
     if (in.mode != BI_PLAIN) {
         float* xo = in.x_out + (size_t)t * in.stride;
-        for (uint32_t i = tid; i < K; i += kThreads) {
+        for (uint32_t i = tid; i < K; i += blockDim.x) {
             xo[i] = xs[i];
             if (in.snap) in.snap[(size_t)t * in.snap_stride + i] = xs[i];
         }
@@ -76,145 +105,264 @@ __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
     double rn = 1.0;
     if (in.w_n) {
         double ss = 0.0;
-        for (uint32_t i = tid; i < K; i += kThreads) ss += (double)xs[i] * (double)xs[i];
+        for (uint32_t i = tid; i < K; i += blockDim.x) ss += (double)xs[i] * (double)xs[i];
         rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
     }
     // each quad of threads holds one 32-element block (8 consecutive elements per thread)
-    int8_t* planes = in.img;
-    BlockTab* tabs = reinterpret_cast<BlockTab*>(in.img + (size_t)in.nb * T * 128);
-    for (uint32_t o = tid; o < in.nb * 4; o += kThreads) {
+    for (uint32_t o = tid; o < nb * 4; o += blockDim.x) {
         const uint32_t b = o >> 2, p = o & 3;
         float v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const uint32_t e = 8 * o + k;
-            const float u = e < K ? xs[e] : 0.0f;
-            v[k] = e < K && in.w_n ? norm_apply(u, rn, in.w_n[e]) : u;
-        }
+        for (int k = 0; k < 8; ++k) v[k] = in.w_n ? norm_apply(xs[8 * o + k], rn, in.w_n[8 * o + k]) : xs[8 * o + k];
         float m, sum;
         quad_stats(v, m, sum);
         uint32_t w[4][2];
         digit_words(v, m, w);
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<v2u*>(planes + (((size_t)b * T + t) * 4 + i) * 32 + 8 * p) = v2u{w[i][0], w[i][1]};
-        if (p == 0) tabs[(size_t)b * T + t] = block_tab_of(m, sum);
+            *reinterpret_cast<v2u*>(planes + (((size_t)b * 4 + i) * Tp + t) * 32 + 8 * p) = v2u{w[i][0], w[i][1]};
+        if (p == 0) tabs[(size_t)b * Tp + t] = block_tab(m, sum);
     }
+}
+
+// BI_PLAIN inputs (no norm, no residual): one thread per 8-element octet, grid (Tp, octets / 256).
+__global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
+    const uint32_t t = blockIdx.x, o = blockIdx.y * 256 + threadIdx.x, nb = in.K / 32, Tp = gridDim.x;
+    if (o >= nb * 4) return;  // whole quads: nb * 4 is a multiple of 4
+    const uint32_t b = o >> 2, p = o & 3;
+    int8_t* planes = in.img;
+    float2* tabs = reinterpret_cast<float2*>(in.img + (size_t)nb * 4 * Tp * 32);
+    float v[8];
+    if (t < in.T) {
+        const float4* x = reinterpret_cast<const float4*>(in.x + (size_t)t * in.stride) + 2 * o;
+        const float4 u0 = x[0], u1 = x[1];
+        v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
+        v[4] = u1.x; v[5] = u1.y; v[6] = u1.z; v[7] = u1.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = 0.0f;
+    }
+    float m, sum;
+    quad_stats(v, m, sum);
+    uint32_t w[4][2];
+    digit_words(v, m, w);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<v2u*>(planes + (((size_t)b * 4 + i) * Tp + t) * 32 + 8 * p) = v2u{w[i][0], w[i][1]};
+    if (p == 0) tabs[(size_t)b * Tp + t] = block_tab(m, sum);
 }
 
 // ---- Q4_0 GEMM over a batch ---------------------------------------------------------------------
 
-// One workgroup per 16-row tile (for a gate/up pair, the same tile of both matrices); its eight
-// waves split the tile's super-tiles.  Lane l holds, per group of four tokens, the partial dot
-// product of token 4 g + l / 16 with row l % 16.  P: matrices (1, or 2 for gate/up); G: token groups.
-template <int P, int G>
-__global__ __launch_bounds__(512) void batch_gemm_kernel(BatchGemm a) {
-    __shared__ float red[8][P][4 * G][16];
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-    const uint32_t rt = blockIdx.x, nst = a.w.nst, T = a.T;
-    const uint32_t per = (nst + 7) / 8, st0 = min(nst, wave * per), st1 = min(nst, st0 + per);
-    const uint32_t row = lane & 15, kq = lane >> 4;        // B operand: column row, k-range 8 kq
-    const uint32_t ta = (lane & 15) >> 2, ia = lane & 3;   // A operand: token 4 g + ta, digit ia
-    const uint32_t tl = lane >> 4;                         // D: token 4 g + tl of row `row`
+namespace {
+
+// One block's operands for a wave: the four digit planes of its G token groups (lane l: token
+// 16 g + l % 16, elements 8 (l / 16) .. + 7), the table entries of the four tokens whose outputs the
+// lane folds (16 g + 4 (l / 16) + e), and the codes and scales of R row tiles of P matrices (lane l:
+// row l % 16, bytes 8 ((l / 16) & 1) .. + 7 of the block's 16 code bytes).
+template <int P, int G, int R>
+struct BlockOps {
+    v2u a[4][G];
+    v4f tab[G][2];
+    uint2 code[R][P];
+    uint16_t d[R][P];
+};
+
+template <int P, int G, int R>
+__device__ __forceinline__ void load_block(BlockOps<P, G, R>& o, const BatchGemm& a, uint32_t b, uint32_t rt0,
+                                           uint32_t last_tile, uint32_t lane) {
+    constexpr uint32_t Tp = 16 * G;
+    const uint32_t m = lane & 15, kq = lane >> 4;
     const int8_t* planes = a.img;
-    const BlockTab* tabs = reinterpret_cast<const BlockTab*>(a.img + (size_t)nst * 4 * T * 128);
-    float acc[P][G];
+    const float2* tabs = reinterpret_cast<const float2*>(a.img + (size_t)a.w.blocks * 4 * Tp * 32);
 #pragma unroll
-    for (int q = 0; q < P; ++q)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int g = 0; g < G; ++g) acc[q][g] = 0.0f;
-    for (uint32_t st = st0; st < st1; ++st) {
+        for (int g = 0; g < G; ++g)
+            o.a[i][g] = *gp(reinterpret_cast<const v2u*>(planes + (((size_t)b * 4 + i) * Tp + 16 * g + m) * 32 + 8 * kq));
 #pragma unroll
-        for (uint32_t blk = 0; blk < 4; ++blk) {
-            const uint32_t b = st * 4 + blk;
-            long B[P];
-            float d[P];
-#pragma unroll
-            for (int q = 0; q < P; ++q) {
-                const Q4View& m = q ? a.w2 : a.w;
-                const size_t rec = ((size_t)rt * nst + st) * 4 + blk;
-                const v2u c = *gp(reinterpret_cast<const v2u*>(m.codes + rec * 256 + row * 16 + 8 * (kq & 1)));
-                const uint32_t sh = kq >= 2 ? 4u : 0u;
-                const uint32_t lo = (c.x >> sh) & 0x0F0F0F0Fu, hi = (c.y >> sh) & 0x0F0F0F0Fu;
-                B[q] = (long)(((uint64_t)hi << 32) | lo);
-                d[q] = h2f(gp(m.scales)[rec * 16 + row]);
-            }
-#pragma unroll
-            for (int g = 0; g < G; ++g) {
-                const uint32_t tA = 4 * g + ta, tD = 4 * g + tl;
-                long A = 0;
-                if (tA < T) {
-                    const v2u v = *gp(reinterpret_cast<const v2u*>(planes + (((size_t)b * T + tA) * 4 + ia) * 32 + 8 * kq));
-                    A = (long)(((uint64_t)v.y << 32) | v.x);
-                }
-                const BlockTab tb = tD < T ? tabs[(size_t)b * T + tD] : BlockTab{0.0f, 0.0f, 0.0f, 0.0f};
-                const v4i zero4 = {0, 0, 0, 0};
-#pragma unroll
-                for (int q = 0; q < P; ++q) {
-                    const v4i D = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B[q], zero4, 0, 0, 0);
-                    // 2^14 D0 + 2^7 D1 + D2 is exact in int32 (|D_i| <= 32 * 15 * 64)
-                    const int I = (D[0] << 14) + (D[1] << 7) + D[2];
-                    float in = fmaf((float)I, tb.s14, tb.nbias);
-                    in = fmaf((float)D[3], tb.s21, in);
-                    acc[q][g] = fmaf(d[q], in, acc[q][g]);
-                }
-            }
-        }
+    for (int g = 0; g < G; ++g) {
+        const v4f* tp = reinterpret_cast<const v4f*>(tabs + (size_t)b * Tp + 16 * g + 4 * kq);
+        o.tab[g][0] = *gp(tp);
+        o.tab[g][1] = *gp(tp + 1);
     }
+    const uint32_t per_tile = a.w.nst * 4;  // block records per row tile (tiled layout, Q4View)
 #pragma unroll
-    for (int q = 0; q < P; ++q)
-#pragma unroll
-        for (int g = 0; g < G; ++g) red[wave][q][4 * g + tl][row] = acc[q][g];
-    __syncthreads();
-    // one thread per (token, row): the waves' partials in wave order, then the epilogue
-    for (uint32_t i = tid; i < T * 16; i += kThreads) {
-        const uint32_t t = i >> 4, r = i & 15, y_row = rt * 16 + r;
-        float v[P];
+    for (int r = 0; r < R; ++r) {
+        const size_t rec = (size_t)min(rt0 + r, last_tile) * per_tile + b;
 #pragma unroll
         for (int q = 0; q < P; ++q) {
-            float s = red[0][q][t][r];
-#pragma unroll
-            for (int w = 1; w < 8; ++w) s += red[w][q][t][r];
-            v[q] = s;
+            const Q4View& w = q ? a.w2 : a.w;
+            o.code[r][q] = ld_stream(reinterpret_cast<const uint2*>(w.codes + rec * 256 + m * 16 + 8 * (kq & 1)));
+            o.d[r][q] = gp(w.scales)[rec * 16 + m];
         }
-        if (y_row >= a.rows) continue;
-        float* y = a.y + (size_t)t * a.y_stride + y_row;
-        if constexpr (P == 2) *y = gelu_mul(v[0], v[1]);
-        else if (a.add) *y = __fadd_rn(v[0], a.add[(size_t)t * a.y_stride + y_row]);
-        else *y = v[0];
     }
+}
+
+template <int P, int G, int R>
+__device__ __forceinline__ void mfma_block(const BlockOps<P, G, R>& o, uint32_t kq, float (&acc)[R][P][G][4]) {
+    const uint32_t sh = kq >= 2 ? 4u : 0u;  // k 0..15: low nibbles, 16..31: high nibbles
+    const v4i zero = {0, 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < P; ++q) {
+            const uint32_t lo = (o.code[r][q].x >> sh) & 0x0F0F0F0Fu, hi = (o.code[r][q].y >> sh) & 0x0F0F0F0Fu;
+            const long B = (long)(((uint64_t)hi << 32) | lo);
+            const float d = h2f(o.d[r][q]);
+#pragma unroll
+            for (int g = 0; g < G; ++g) {
+                v4i D[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const long A = (long)(((uint64_t)o.a[i][g].y << 32) | o.a[i][g].x);
+                    D[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
+                }
+                const float tb[8] = {o.tab[g][0].x, o.tab[g][0].y, o.tab[g][0].z, o.tab[g][0].w,
+                                     o.tab[g][1].x, o.tab[g][1].y, o.tab[g][1].z, o.tab[g][1].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    // exact: |I| < 2^30 (|D_i| <= 32 * 15 * 64)
+                    const int I = (int)(((uint32_t)D[0][e] << 14) + ((uint32_t)D[1][e] << 7) + (uint32_t)D[2][e]);
+                    float in = fmaf((float)D[3][e], tb[2 * e] * 0.0078125f, tb[2 * e + 1]);  // s 2^-21 D3 + bias
+                    in = fmaf((float)I, tb[2 * e], in);
+                    acc[r][q][g][e] = fmaf(d, in, acc[r][q][g][e]);
+                }
+            }
+        }
+}
+
+template <int P>
+__device__ __forceinline__ void gemm_epilogue(const BatchGemm& a, uint32_t t, uint32_t row, const float (&v)[P]) {
+    float* y = a.y + (size_t)t * a.y_stride + row;
+    if constexpr (P == 2) *y = gelu_mul(v[0], v[1]);
+    else if (a.add) *y = __fadd_rn(v[0], a.add[(size_t)t * a.y_stride + row]);
+    else *y = v[0];
+}
+
+}  // namespace
+
+// Grid (ceil(tiles / R), S): workgroup (x, s) takes row tiles R x .. R x + R - 1 (for a gate/up pair,
+// those tiles of both matrices) over K range s of S; its four waves split the range's blocks and add
+// their partials in LDS in wave order.  Each wave streams its blocks through a two-stage register
+// pipeline (the next block's loads in flight while the current block's MFMAs run).  With S = 1 the
+// workgroup writes y; otherwise it writes its partials for batch_reduce_kernel.
+template <int P, int G, int R>
+__global__ __launch_bounds__(256) void batch_gemm_kernel(BatchGemm a) {
+    constexpr uint32_t Tp = 16 * G;
+    __shared__ float red[4][R][P][Tp][16];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id(), kq = lane >> 4;
+    const uint32_t tiles = (a.w.rows + 15) / 16, rt0 = blockIdx.x * R, S = gridDim.y, split = blockIdx.y;
+    const uint32_t nb = a.w.blocks;
+    const uint32_t s0 = nb * split / S, s1 = nb * (split + 1) / S;
+    const uint32_t b0 = s0 + (s1 - s0) * wave / 4, b1 = s0 + (s1 - s0) * (wave + 1) / 4;
+    float acc[R][P][G][4];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[r][q][g][e] = 0.0f;
+    BlockOps<P, G, R> x0, x1;
+    if (b0 < b1) load_block(x0, a, b0, rt0, tiles - 1, lane);
+    for (uint32_t b = b0; b < b1; b += 2) {
+        if (b + 1 < b1) load_block(x1, a, b + 1, rt0, tiles - 1, lane);
+        mfma_block(x0, kq, acc);
+        if (b + 1 >= b1) break;
+        if (b + 2 < b1) load_block(x0, a, b + 2, rt0, tiles - 1, lane);
+        mfma_block(x1, kq, acc);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int q = 0; q < P; ++q)
+#pragma unroll
+            for (int g = 0; g < G; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[wave][r][q][16 * g + 4 * kq + e][lane & 15] = acc[r][q][g][e];
+    __syncthreads();
+    const size_t prow = (size_t)tiles * 16;
+    for (uint32_t i = tid; i < R * Tp * 16; i += kGemmThreads) {
+        const uint32_t r = i / (Tp * 16), t = (i / 16) % Tp, n = i & 15;
+        const uint32_t tile = rt0 + r, row = tile * 16 + n;
+        if (tile >= tiles || t >= a.T) continue;
+        float v[P];
+#pragma unroll
+        for (int q = 0; q < P; ++q) v[q] = ((red[0][r][q][t][n] + red[1][r][q][t][n]) + red[2][r][q][t][n]) + red[3][r][q][t][n];
+        if (S > 1) {
+#pragma unroll
+            for (int q = 0; q < P; ++q) a.part[((size_t)(split * P + q) * Tp + t) * prow + row] = v[q];
+        } else if (row < a.w.rows) {
+            gemm_epilogue<P>(a, t, row, v);
+        }
+    }
+}
+
+// y from the S split-K partials of batch_gemm_kernel, summed in split order; one thread per (t, row).
+template <int P>
+__global__ __launch_bounds__(256) void batch_reduce_kernel(BatchGemm a, uint32_t S, uint32_t Tp) {
+    const uint32_t rows = a.w.rows, i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= a.T * rows) return;
+    const uint32_t t = i / rows, row = i % rows;
+    const size_t prow = (size_t)(rows + 15) / 16 * 16;
+    float v[P];
+#pragma unroll
+    for (int q = 0; q < P; ++q) {
+        float s = a.part[((size_t)q * Tp + t) * prow + row];
+        for (uint32_t k = 1; k < S; ++k) s += a.part[((size_t)(k * P + q) * Tp + t) * prow + row];
+        v[q] = s;
+    }
+    gemm_epilogue<P>(a, t, row, v);
 }
 
 // ---- launchers ----------------------------------------------------------------------------------
 
-size_t batch_image_bytes(uint32_t nst, uint32_t tokens) { return (size_t)nst * 4 * tokens * (128 + 16); }
-
-hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
-    if (in.T == 0 || in.T > kBatchMax || in.K > 16384 || in.nb * 32 < in.K) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(batch_digits_kernel, dim3(in.T), dim3(kThreads), (size_t)in.K * 4, s, in);
-    return hipGetLastError();
+size_t batch_image_bytes(uint32_t blocks, uint32_t tokens) {
+    return (size_t)blocks * padded_tokens(tokens) * (4 * 32 + 8);
 }
 
-template <int P>
-static hipError_t gemm_launch(const BatchGemm& a, hipStream_t s) {
-    const dim3 grid((a.rows + 15) / 16);
-    switch ((a.T + 3) / 4) {
-        case 1: hipLaunchKernelGGL((batch_gemm_kernel<P, 1>), grid, dim3(kThreads), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((batch_gemm_kernel<P, 2>), grid, dim3(kThreads), 0, s, a); break;
-        case 3:
-        case 4: hipLaunchKernelGGL((batch_gemm_kernel<P, 4>), grid, dim3(kThreads), 0, s, a); break;
-        case 5:
-        case 6:
-        case 7:
-        case 8: hipLaunchKernelGGL((batch_gemm_kernel<P, 8>), grid, dim3(kThreads), 0, s, a); break;
-        default: return hipErrorInvalidValue;
+size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair) {
+    const GemmPlan p = gemm_plan(rows, blocks);
+    if (p.S == 1) return 0;
+    return (size_t)p.S * (gelu_pair ? 2 : 1) * padded_tokens(tokens) * ((rows + 15) / 16 * 16) * 4;
+}
+
+hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
+    if (in.T == 0 || in.T > kBatchMax || in.K == 0 || in.K > 16384 || in.K % 32) return hipErrorInvalidValue;
+    if (in.mode == BI_PLAIN && !in.w_n) {
+        if (in.stride % 4 || reinterpret_cast<uintptr_t>(in.x) % 16) return hipErrorInvalidValue;
+        const uint32_t octets = in.K / 8;
+        hipLaunchKernelGGL(batch_plain_digits_kernel, dim3(padded_tokens(in.T), (octets + 255) / 256), dim3(256), 0, s,
+                           in);
+    } else {
+        hipLaunchKernelGGL(batch_digits_kernel, dim3(padded_tokens(in.T)), dim3(512), (size_t)in.K * 4, s, in);
     }
     return hipGetLastError();
 }
 
+template <int P, int G>
+static hipError_t gemm_launch(const BatchGemm& a, hipStream_t s) {
+    const GemmPlan p = gemm_plan(a.w.rows, a.w.blocks);
+    const uint32_t tiles = (a.w.rows + 15) / 16;
+    const dim3 grid((tiles + p.R - 1) / p.R, p.S);
+    if (p.S > 1 && !a.part) return hipErrorInvalidValue;
+    if (p.R == 2) hipLaunchKernelGGL((batch_gemm_kernel<P, G, 2>), grid, dim3(kGemmThreads), 0, s, a);
+    else hipLaunchKernelGGL((batch_gemm_kernel<P, G, 1>), grid, dim3(kGemmThreads), 0, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || p.S == 1) return e;
+    const uint32_t n = a.T * a.w.rows;
+    hipLaunchKernelGGL((batch_reduce_kernel<P>), dim3((n + 255) / 256), dim3(256), 0, s, a, p.S, 16u * G);
+    return hipGetLastError();
+}
+
 hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s) {
-    if (a.T == 0 || a.T > kBatchMax || a.rows == 0) return hipErrorInvalidValue;
-    return gelu_pair ? gemm_launch<2>(a, s) : gemm_launch<1>(a, s);
+    if (a.T == 0 || a.T > kBatchMax || a.w.rows == 0 || a.w.blocks == 0) return hipErrorInvalidValue;
+    if (gelu_pair && (a.w2.rows != a.w.rows || a.w2.blocks != a.w.blocks)) return hipErrorInvalidValue;
+    const bool two = a.T > 16;
+    if (gelu_pair) return two ? gemm_launch<2, 2>(a, s) : gemm_launch<2, 1>(a, s);
+    return two ? gemm_launch<1, 2>(a, s) : gemm_launch<1, 1>(a, s);
 }
 
 }  // namespace af

@@ -401,7 +401,10 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
 
 // ---- GQA decode attention ---------------------------------------------------------------------
 //
-// Grid (cmax, kv_heads), 256 threads.  Each block takes one chunk of the
+// Grid (cmax, kv_heads * query groups, tokens), D threads; grid z indexes the tokens of a batch
+// (positions position + z, rows z * in_stride of q/k/v and z * out_stride of out).  Modes: ATT_DECODE
+// appends the new K/V and attends; ATT_APPEND only normalises, rotates and appends K/V (grid x 1);
+// ATT_ATTEND attends with every position's K/V already in the cache.  Each block takes one chunk of the
 // visible range [max(0, pos + 1 - window), pos] for one KV head and its GQ
 // query heads.  Prologue: q-norm + NeoX RoPE of the query heads (double angle,
 // double rotation, f32 result); the block whose chunk ends at pos also
@@ -428,7 +431,12 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     if (a.state && a.state[ST_STOP]) return;
-    const uint32_t pos = a.state ? a.state[ST_POS] : a.position;
+    const uint32_t z = blockIdx.z;
+    const uint32_t pos = (a.state ? a.state[ST_POS] : a.position) + z;
+    const float* q_raw = a.q_raw + (size_t)z * a.in_stride;
+    const float* k_raw = a.k_raw + (size_t)z * a.in_stride;
+    const float* v_raw = a.v_raw + (size_t)z * a.in_stride;
+    float* out = a.out + (size_t)z * a.out_stride;
     const uint32_t nvis = a.window ? min(pos + 1, a.window) : pos + 1;
     const uint32_t start = pos + 1 - nvis;
     uint32_t chunks = min(a.cmax, (nvis + a.min_chunk - 1) / a.min_chunk);
@@ -438,20 +446,21 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     const uint32_t qgroups = a.group / G;
     const uint32_t c = blockIdx.x, kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
     const uint32_t qh0 = kvh * a.group + qg * G;
-    if (c >= chunks) return;
+    if (a.mode == ATT_APPEND ? qg != 0 : c >= chunks) return;
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
     const uint32_t n = t1 - t0;
     const uint32_t ring = a.ring;
-    const bool has_new = t1 == pos + 1;      // this chunk holds the new token (its K and V computed here)
+    // this chunk holds the new token (its K and V computed here)
+    const bool has_new = a.mode == ATT_APPEND || (a.mode == ATT_DECODE && t1 == pos + 1);
     const bool append = has_new && qg == 0;  // and this block stores them in the cache
     const int nh = has_new ? NH : G;
 
     // ---- prologue: RMSNorm of the query heads (and new K, V) with one block reduction, then RoPE
     float raw[NH];
 #pragma unroll
-    for (int h = 0; h < G; ++h) raw[h] = a.q_raw[(size_t)(qh0 + h) * D + tid];
-    raw[G] = has_new ? a.k_raw[(size_t)kvh * D + tid] : 0.0f;
-    raw[G + 1] = has_new ? a.v_raw[(size_t)kvh * D + tid] : 0.0f;
+    for (int h = 0; h < G; ++h) raw[h] = q_raw[(size_t)(qh0 + h) * D + tid];
+    raw[G] = has_new ? k_raw[(size_t)kvh * D + tid] : 0.0f;
+    raw[G + 1] = has_new ? v_raw[(size_t)kvh * D + tid] : 0.0f;
     double sn = 0.0, cs = 1.0;
     if (tid < D / 2) sincos((double)pos * a.inv_freq[tid], &sn, &cs);
 #pragma unroll
@@ -501,6 +510,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         a.kcache[slot + tid] = knew[tid];
         a.vcache[slot + tid] = vnew[tid];
     }
+    if (a.mode == ATT_APPEND) return;
 
     // ---- scores: LK lanes per token (16 channels each), TG token groups, two tokens in flight
     {
@@ -516,7 +526,8 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
             for (int u = 0; u < 2; ++u) {
                 const uint32_t t = tb + TG * u;
                 const uint32_t tt = t < t1 ? t : tb;
-                const uint16_t* kp = (tt == pos ? knew : a.kcache + ((size_t)kvh * ring + tt % ring) * D) + 16 * j;
+                const uint16_t* kp =
+                    (has_new && tt == pos ? knew : a.kcache + ((size_t)kvh * ring + tt % ring) * D) + 16 * j;
                 k[u][0] = *reinterpret_cast<const uint4*>(kp);
                 k[u][1] = *reinterpret_cast<const uint4*>(kp + 8);
             }
@@ -576,7 +587,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
             for (int u = 0; u < 2; ++u) {
                 const uint32_t t = tb + 8 * u;
                 const uint32_t tt = t < t1 ? t : tb;
-                const uint16_t* vp = tt == pos ? vnew : a.vcache + ((size_t)kvh * ring + tt % ring) * D;
+                const uint16_t* vp = has_new && tt == pos ? vnew : a.vcache + ((size_t)kvh * ring + tt % ring) * D;
                 vv[u] = *reinterpret_cast<const uint4*>(vp + 8 * dl);
             }
 #pragma unroll
@@ -614,13 +625,13 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     }
     if (chunks == 1) {
 #pragma unroll
-        for (int gi = 0; gi < G; ++gi) a.out[(size_t)(qh0 + gi) * D + tid] = o[gi] / l[gi];
+        for (int gi = 0; gi < G; ++gi) out[(size_t)(qh0 + gi) * D + tid] = o[gi] / l[gi];
         return;
     }
 
     // ---- split-K merge: the last block of this (KV head, query group) combines the chunk partials
     const size_t stride = (size_t)G * (D + 2);
-    const uint32_t slot = blockIdx.y;  // (KV head, query group)
+    const uint32_t slot = blockIdx.z * gridDim.y + blockIdx.y;  // (token, KV head, query group)
     float* mine = a.part + ((size_t)slot * a.cmax + c) * stride;
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
@@ -666,7 +677,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         float acc = 0.0f;
 #pragma unroll 8
         for (uint32_t k = 0; k < chunks; ++k) acc = fmaf(cw[gi][k], all[k * stride + gi * (D + 2) + tid], acc);
-        a.out[(size_t)(qh0 + gi) * D + tid] = acc / L[gi];
+        out[(size_t)(qh0 + gi) * D + tid] = acc / L[gi];
     }
     if (tid == 0) a.counters[slot] = 0u;
 }
@@ -677,10 +688,10 @@ uint32_t attention_block_heads(uint32_t group, uint32_t head_width) {
     return head_width == 256 ? group : std::min<uint32_t>(group, 2u);
 }
 
-hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s) {
+hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s, uint32_t tokens) {
     const uint32_t G = attention_block_heads(group, head_width);
-    if (a.group != group || group % G) return hipErrorInvalidValue;
-    const dim3 grid(a.cmax, a.kv_heads * (group / G));
+    if (a.group != group || group % G || tokens == 0) return hipErrorInvalidValue;
+    const dim3 grid(a.mode == ATT_APPEND ? 1 : a.cmax, a.kv_heads * (group / G), tokens);
     if (head_width == 256) {
         switch (G) {
             case 1: hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a); break;
