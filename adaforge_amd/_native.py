@@ -130,6 +130,7 @@ SIGNATURES = {
     "af_session_generate": (i32, [P, u32p, sz, u32p, sz, u32, TOKEN_FN, P, u32p, ctypes.POINTER(sz),
                                   ctypes.POINTER(i32), ctypes.POINTER(GenerationStats)]),
     "af_session_reset": (i32, [P]),
+    "af_session_speculation": (i32, [P, ctypes.POINTER(u64), ctypes.POINTER(u64), ctypes.POINTER(u64)]),
     "af_session_close": (None, [P]),
     "af_generate": (i32, [ctypes.POINTER(LayerDesc), u32, ctypes.POINTER(HeadDesc), u32p, sz, u32p, sz, u32, u32p,
                           ctypes.POINTER(sz), ctypes.POINTER(i32), ctypes.POINTER(GenerationStats)]),

@@ -180,6 +180,12 @@ class HipGenerationSession:
     def reset(self):
         check(N.lib().af_session_reset(self._h))
 
+    def speculation(self):
+        """(verification passes, draft tokens, accepted draft tokens) since open."""
+        p, d, a = N.u64(), N.u64(), N.u64()
+        check(N.lib().af_session_speculation(self._h, ctypes.byref(p), ctypes.byref(d), ctypes.byref(a)))
+        return int(p.value), int(d.value), int(a.value)
+
     def profile(self, prompt, max_new):
         """Decode with per-kernel event timing (ADAFORGE_TIMING_DECODE, stack.rs:1245-1251):
         returns (ids, {kind: (launches, total_ms, bytes_per_launch)})."""

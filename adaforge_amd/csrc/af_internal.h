@@ -185,7 +185,8 @@ int set_error(int code, std::string msg);
 // GEMV, s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21), s = 2^(ilogb(max |x_b|) - 5):
 //   planes img[((b 4 + i) Tp + t) 32 + j]   digit i of element j
 //   tabs   float2 at img + nb 4 Tp 32, [b Tp + t] = {s 2^-14, -8 sum_j x_j}
-constexpr uint32_t kBatchMax = 32;  // tokens per batch (crates/cuda-backend/src/batch.rs MAX_BATCH)
+constexpr uint32_t kBatchMax = 32;   // tokens per batch (crates/cuda-backend/src/batch.rs:10 MAX_BATCH)
+constexpr uint32_t kVerifyMax = 16;  // tokens per speculative verification pass (batch.rs:13 MAX_VERIFY)
 
 enum BatchInputKind : int { BI_PLAIN = 0, BI_RESID = 1, BI_EMBED = 2 };
 

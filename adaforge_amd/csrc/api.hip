@@ -926,6 +926,12 @@ struct af_session {
     // (AF_PREFILL_BATCH, default kBatchMax; 0 or 1 prefills one position per step-kernel launch);
     // trace_batch: the same for af_session_trace (AF_TRACE_BATCH, default 0: the step kernel).
     uint32_t prefill_batch = kBatchMax, trace_batch = 0;
+    // Greedy speculative decoding with prompt-lookup drafts (AF_SPECULATIVE=1; AF_SPEC_DEPTH draft
+    // tokens at most, default 11, at most kVerifyMax - 1): the draft and the pending token run through
+    // the batched layers in one pass and the head checks each position.
+    bool speculative = false;
+    uint32_t spec_depth = 11;
+    uint64_t spec_passes = 0, spec_drafted = 0, spec_accepted = 0;  // since open (af_session_speculation)
     uint32_t max_qh = 0, max_qh_part = 0;
     DevMem XB, HB, QKVB, ATTB, PROJB, ACTB, DB, BIMG, BGEMM, BPART, BCOUNT;
 
@@ -1549,6 +1555,9 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         s->prefill_batch = std::min<uint32_t>((uint32_t)std::strtoul(pb, nullptr, 10), kBatchMax);
     if (const char* tb = std::getenv("AF_TRACE_BATCH"))
         s->trace_batch = std::min<uint32_t>((uint32_t)std::strtoul(tb, nullptr, 10), kBatchMax);
+    if (const char* sp = std::getenv("AF_SPECULATIVE")) s->speculative = std::strcmp(sp, "1") == 0;
+    if (const char* sd = std::getenv("AF_SPEC_DEPTH"))
+        s->spec_depth = std::max<uint32_t>(1, std::min<uint32_t>((uint32_t)std::strtoul(sd, nullptr, 10), kVerifyMax - 1));
     HIP_OK(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "session stream");
 
     uint32_t max_kv = 0, max_q = 0, max_group = 1, max_qh_part = 0, max_qh = 0;
@@ -1674,6 +1683,14 @@ int af_session_open(const af_layer_weights* layers, uint32_t n_layers, const af_
 
 void af_session_close(af_session* s) { delete s; }
 
+int af_session_speculation(const af_session* s, uint64_t* passes, uint64_t* drafted, uint64_t* accepted) {
+    if (!s || !passes || !drafted || !accepted) return fail(AF_ERR_INVALID, "null argument");
+    *passes = s->spec_passes;
+    *drafted = s->spec_drafted;
+    *accepted = s->spec_accepted;
+    return AF_OK;
+}
+
 int af_session_reset(af_session* s) {
     if (!s) return fail(AF_ERR_INVALID, "null session");
     if (s->poisoned) return fail(AF_ERR_POISONED, "invalid HIP session; restart the chat");
@@ -1685,6 +1702,162 @@ int af_session_reset(af_session* s) {
 }  // extern "C"
 
 namespace {
+
+// Prompt-lookup draft (crates/cuda-backend/src/stack.rs:1491-1511): the tokens that followed the most
+// recent earlier occurrence of the history's last 3 tokens, at most `limit` of them.
+std::vector<uint32_t> draft_lookup(const std::vector<uint32_t>& h, size_t limit) {
+    constexpr size_t gram = 3;
+    if (h.size() <= gram || limit == 0) return {};
+    const size_t tail = h.size() - gram;
+    for (size_t start = tail; start-- > 0;) {
+        if (std::equal(h.begin() + start, h.begin() + start + gram, h.begin() + tail)) {
+            const size_t from = start + gram, end = std::min(from + limit, h.size());
+            if (from < end) return std::vector<uint32_t>(h.begin() + from, h.begin() + end);
+        }
+    }
+    return {};
+}
+
+// The decode loop of GenerationSession::generate with speculation (stack.rs:1252-1338), after the
+// prefill has left position P - 1 (or, with nothing pending, the last consumed position's head input)
+// to run.  Each round emits the pending greedy token; with a draft, the token and its draft go through
+// the batched layers at once, the head runs on each position until the first prediction that
+// differs from the draft, the matching draft tokens are emitted, and the caches keep only their
+// positions (the rest are overwritten later: a local ring holds window + kBatchMax slots).  The
+// emitted ids are the greedy ids of plain decoding, up to the arithmetic of the batched layers.
+int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop, size_t n_stop,
+              uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out, size_t* n_out,
+              int32_t* stopped_out, af_generation_stats* stats, Clock::time_point started, double prefill_ms,
+              size_t cached_tokens) {
+    hipStream_t st = s->stream;
+    const size_t H = s->hidden;
+    const uint32_t P = (uint32_t)n_prompt;
+    int rc;
+    if ((rc = s->ensure_batch())) return rc;
+    auto is_stop = [&](uint32_t id) { return std::find(stop, stop + n_stop, id) != stop + n_stop; };
+    // One decode step on the token at `pos` (already in IDS): step kernel and head in step mode (no
+    // stop ids on the device); returns the head's id for pos + 1.
+    uint32_t pos = 0;
+    auto step = [&](uint32_t& out) -> int {
+        for (int attempt = 0; attempt < 2; ++attempt) {
+            int r = s->set_state(pos, 0);
+            if (r) return r;
+            HIP_OK(s->run_step(true), "decode step");
+            HIP_OK(hipStreamSynchronize(st), "decode step");
+            const volatile StepRecord* vr = s->records + pos + 1;
+            if (vr->done) {
+                if (vr->bad) return fail(AF_ERR_NONFINITE, "non-finite logits or invalid greedy id");
+                out = vr->id;
+                ++pos;
+                return AF_OK;
+            }
+            bool timed_out = false;
+            if ((r = s->step_timed_out(timed_out, nullptr))) return r;
+            if (!timed_out || attempt) break;
+            if ((r = s->fall_back())) return r;
+        }
+        return fail(AF_ERR_DEVICE, "decode step did not complete");
+    };
+    // The head on hidden state x (down output) and residual h; non-step mode, result in RESULT.
+    auto head = [&](const float* x, const float* h, uint32_t& out) -> int {
+        HeadArgs a = s->head_args(false, false);
+        a.in.x = x;
+        a.in.res = h;
+        HIP_OK(launch_head(a, IN_RESID, s->head_blocks, st), "head");
+        uint32_t res[2] = {0, 0};
+        HIP_OK(hipMemcpyAsync(res, s->RESULT.p, sizeof(res), hipMemcpyDeviceToHost, st), "head result");
+        HIP_OK(hipStreamSynchronize(st), "head");
+        if (res[1]) return fail(AF_ERR_NONFINITE, "non-finite logits or invalid greedy id");
+        out = res[0];
+        return AF_OK;
+    };
+    uint32_t next = 0;
+    if (P == s->consumed) {  // nothing pending: the head on the last consumed position's state
+        pos = s->consumed;
+        if ((rc = head(s->D.as<float>(), s->H.as<float>(), next))) return rc;
+    } else {
+        pos = P - 1;
+        if ((rc = step(next))) return rc;
+    }
+    std::vector<uint32_t> history(prompt, prompt + n_prompt), ids, batch;
+    bool stopped = false;
+    double first_ms = 0, last_ms = 0;
+    auto emit = [&](uint32_t id) {
+        const double t = ms_since(started);
+        if (ids.empty()) first_ms = t;
+        last_ms = t;
+        ids.push_back(id);
+        history.push_back(id);
+        if (on_token) on_token(user, id);
+    };
+    while (ids.size() < max_new) {
+        if (is_stop(next)) {
+            stopped = true;
+            break;
+        }
+        emit(next);
+        const size_t remaining = max_new - ids.size();
+        const size_t room = s->capacity > pos + 1 ? s->capacity - (pos + 1) : 0;
+        const size_t limit = std::min({remaining, room, (size_t)s->spec_depth, (size_t)kVerifyMax - 1});
+        const std::vector<uint32_t> draft = draft_lookup(history, limit);
+        if (draft.empty()) {
+            HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + pos, &next, 4, hipMemcpyHostToDevice, st), "id upload");
+            if ((rc = step(next))) return rc;
+            if (remaining == 0) break;
+            continue;
+        }
+        const uint32_t base = pos, T = (uint32_t)draft.size() + 1;
+        batch.assign(1, next);
+        batch.insert(batch.end(), draft.begin(), draft.end());
+        HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + base, batch.data(), (size_t)T * 4, hipMemcpyHostToDevice, st),
+               "draft upload");
+        HIP_OK(s->enqueue_batch(base, T, nullptr), "verification pass");
+        // position i's prediction, until the first that differs from draft[i]
+        size_t keep = 0;
+        uint32_t predicted = 0;
+        for (uint32_t i = 0; i < T; ++i) {
+            if ((rc = head(s->DB.as<float>() + i * H, s->HB.as<float>() + i * H, predicted))) return rc;
+            if (i == draft.size() || predicted != draft[i]) break;
+            ++keep;
+        }
+        size_t emitted = 0;
+        for (; emitted < keep; ++emitted) {
+            if (is_stop(draft[emitted])) {
+                stopped = true;
+                break;
+            }
+            emit(draft[emitted]);
+        }
+        // the state after position base + emitted, where the next step or head continues
+        pos = base + 1 + (uint32_t)emitted;
+        HIP_OK(hipMemcpyAsync(s->D.p, s->DB.as<float>() + emitted * H, H * 4, hipMemcpyDeviceToDevice, st), "state");
+        HIP_OK(hipMemcpyAsync(s->H.p, s->HB.as<float>() + emitted * H, H * 4, hipMemcpyDeviceToDevice, st), "state");
+        HIP_OK(hipStreamSynchronize(st), "verification pass");
+        s->spec_drafted += draft.size();
+        s->spec_accepted += keep;
+        ++s->spec_passes;
+        if (stopped) break;
+        next = predicted;
+    }
+    for (size_t i = 0; i < ids.size(); ++i) ids_out[i] = ids[i];
+    s->cached.assign(prompt, prompt + n_prompt);
+    s->cached.insert(s->cached.end(), ids.begin(), ids.end());
+    s->consumed = pos;
+    s->poisoned = false;
+    if (n_out) *n_out = ids.size();
+    if (stopped_out) *stopped_out = stopped;
+    if (stats) {
+        stats->prompt_tokens = n_prompt - cached_tokens;
+        stats->cached_tokens = cached_tokens;
+        stats->prefill_ms = prefill_ms;
+        stats->has_first_token = !ids.empty();
+        stats->first_token_ms = ids.empty() ? 0.0 : first_ms;
+        stats->decode_tokens = ids.empty() ? 0 : ids.size() - 1;
+        stats->decode_ms = ids.empty() ? 0.0 : last_ms - first_ms;
+        stats->total_ms = ms_since(started);
+    }
+    return AF_OK;
+}
 
 // GenerationSession::generate (crates/cuda-backend/src/stack.rs:1171-1386).  With a timer the
 // decode steps are launched directly with an event pair around every kernel (no stop ids).
@@ -1737,6 +1910,9 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
         }
     }
     const double prefill_ms = ms_since(started);
+    if (s->speculative && !timer)
+        return speculate(s, prompt, n_prompt, stop, n_stop, max_new, on_token, user, ids_out, n_out, stopped_out, stats,
+                         started, prefill_ms, cached_tokens);
     const double start_offset = ms_since(started);
     HIP_OK(hipEventRecord(s->ev_start, st), "event");
     // Enqueue the decode steps from k0 on; each step's head writes its id and flags to mapped host

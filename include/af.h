@@ -241,12 +241,20 @@ int af_session_open(const af_layer_weights* layers, uint32_t n_layers, const af_
                     uint32_t capacity, af_session** out);
 /* GenerationSession::generate / generate_stream (stack.rs:1171-1386): prompt must extend the
  * session's cached tokens; at most max_new (1..AF_MAX_NEW_TOKENS) greedy ids, stopping before
- * any id in `stop` (non-empty).  on_token may be NULL.  ids_out holds >= max_new ids. */
+ * any id in `stop` (non-empty).  on_token may be NULL.  ids_out holds >= max_new ids.
+ * Environment switches read at af_session_open: AF_PREFILL_BATCH (prompt positions per batched
+ * pass, default 32; 0 or 1: one decode step per position, as ADAFORGE_BATCH_PREFILL=0,
+ * stack.rs:982-987); AF_SPECULATIVE=1 with AF_SPEC_DEPTH (default 11, at most 15): greedy
+ * speculative decoding with prompt-lookup drafts verified in one batched pass (ADAFORGE_SPECULATIVE,
+ * ADAFORGE_SPEC_DEPTH, stack.rs:1252-1338, 1485-1511); the ids are the greedy ids either way. */
 int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop,
                         size_t n_stop, uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out,
                         size_t* n_out, int32_t* stopped, af_generation_stats* stats);
 /* GenerationSession::reset (stack.rs:1469-1480). */
 int af_session_reset(af_session* s);
+/* Speculative decoding counters since open: verification passes, draft tokens, accepted draft tokens
+ * (the ADAFORGE_DIAGNOSTICS "SPECULATIVE" line, stack.rs:1332-1337). */
+int af_session_speculation(const af_session* s, uint64_t* passes, uint64_t* drafted, uint64_t* accepted);
 void af_session_close(af_session* s);
 
 /* Per-kernel decode timing, the event-based ADAFORGE_TIMING_DECODE diagnostic
