@@ -166,6 +166,7 @@ struct AttnArgs {
     int mode;                // AttnMode
     size_t in_stride;        // batch: floats between the tokens' q / k / v rows
     size_t out_stride;       // batch: floats between the tokens' outputs
+    float* q_out;            // ATT_APPEND: the normalised, rotated queries [tokens][q_heads][head_width]
 };
 
 enum AttnMode : int {
@@ -221,7 +222,25 @@ struct BatchGemm {
     float* part;            // split-K partials (batch_gemm_part_bytes)
 };
 
+// Attention of a batch over the KV cache after the append pass (batch_attention_kernel): the
+// tokens' queries q[t][q_heads][D], token t at position pos0 + t seeing keys [max(0, pos0 + t + 1 -
+// window), pos0 + t] (window 0: from 0).  Keys [klo, pos0 + T) go in nchunks chunks of span keys
+// (a multiple of the kernel's sub-chunk); chunk partials (sum p v, max, sum p) per (token, head).
+struct BatchAttn {
+    const float* q;
+    const uint16_t* kcache;
+    const uint16_t* vcache;
+    uint32_t ring, window, T, pos0, kv_heads, group;
+    float scale;
+    uint32_t klo, span, nchunks;
+    float* part;             // [T q_heads][nchunks][D + 2]
+    float* out;              // [T][out_stride]: head qh at qh D
+    size_t out_stride;
+};
+constexpr uint32_t kBatchAttnChunks = 32;  // chunk partials per (token, head) at most
+
 size_t batch_image_bytes(uint32_t blocks, uint32_t tokens);
+hipError_t launch_batch_attention(BatchAttn a, uint32_t head_width, hipStream_t s);
 size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair);
 hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s);
 hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s);

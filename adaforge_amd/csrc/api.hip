@@ -933,7 +933,7 @@ struct af_session {
     uint32_t spec_depth = 11;
     uint64_t spec_passes = 0, spec_drafted = 0, spec_accepted = 0;  // since open (af_session_speculation)
     uint32_t max_qh = 0, max_qh_part = 0;
-    DevMem XB, HB, QKVB, ATTB, PROJB, ACTB, DB, BIMG, BGEMM, BPART, BCOUNT;
+    DevMem XB, HB, QKVB, QB, ATTB, PROJB, ACTB, DB, BIMG, BGEMM, BPART, BCOUNT;
 
     // Launches f(); when profiling, brackets it with an event pair tagged with its kind and bytes.
     template <typename F>
@@ -1225,10 +1225,6 @@ struct af_session {
         return AF_OK;
     }
 
-    // Attention chunks of a batch: the tokens already spread the grid, so each (token, KV head)
-    // splits its visible range only past kBatchMinChunk positions, into at most kBatchCmax chunks
-    // (kBatchCmax * kAttnMaxChunkLen covers AF_MAX_CONTEXT).
-    static constexpr uint32_t kBatchCmax = 16, kBatchMinChunk = 256;
 
     int ensure_batch() {
         if (XB.p) return AF_OK;
@@ -1246,9 +1242,10 @@ struct af_session {
             size_t bytes;
         } bufs[] = {
             {&XB, T * hidden * 4},        {&HB, T * hidden * 4},  {&QKVB, T * max_qkv * 4},
-            {&ATTB, T * max_q * 4},       {&PROJB, T * hidden * 4}, {&ACTB, T * intermediate * 4},
+            {&ATTB, T * max_q * 4},       {&QB, T * max_q * 4},   {&PROJB, T * hidden * 4},
+            {&ACTB, T * intermediate * 4},
             {&DB, T * hidden * 4},        {&BIMG, batch_image_bytes(blocks, kBatchMax)}, {&BGEMM, part},
-            {&BPART, T * kBatchCmax * max_qh_part * 4}, {&BCOUNT, T * std::max<uint32_t>(max_qh, 64) * 4},
+            {&BPART, T * kBatchAttnChunks * max_qh_part * 4}, {&BCOUNT, T * std::max<uint32_t>(max_qh, 64) * 4},
         };
         for (auto& b : bufs) {
             int rc = dev_alloc(*b.m, b.bytes, "batch buffer");
@@ -1338,14 +1335,28 @@ struct af_session {
             aa.out_stride = L.qn;
             aa.part = BPART.as<float>();
             aa.counters = BCOUNT.as<uint32_t>();
-            aa.cmax = kBatchCmax;
-            aa.min_chunk = kBatchMinChunk;
+            aa.cmax = 1;  // the append pass: one block per (token, KV head, query group)
+            aa.min_chunk = kAttnMinChunk;
             aa.kv_heads = L.kv_heads;
             aa.group = L.q_heads / L.kv_heads;
             aa.mode = ATT_APPEND;
+            aa.q_out = QB.as<float>();
             if ((e = launch_attention(aa, aa.group, L.width, stream, T)) != hipSuccess) return e;
-            aa.mode = ATT_ATTEND;
-            if ((e = launch_attention(aa, aa.group, L.width, stream, T)) != hipSuccess) return e;
+            BatchAttn ba{};
+            ba.q = QB.as<float>();
+            ba.kcache = L.kcache.as<uint16_t>();
+            ba.vcache = L.vcache.as<uint16_t>();
+            ba.ring = L.ring;
+            ba.window = L.window;
+            ba.T = T;
+            ba.pos0 = p0;
+            ba.kv_heads = L.kv_heads;
+            ba.group = L.q_heads / L.kv_heads;
+            ba.scale = L.scale;
+            ba.part = BPART.as<float>();
+            ba.out = ATTB.as<float>();
+            ba.out_stride = L.qn;
+            if ((e = launch_batch_attention(ba, L.width, stream)) != hipSuccess) return e;
 
             in = batch_in(BI_PLAIN, T, L.qn, ATTB.as<float>(), L.qn);
             if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;

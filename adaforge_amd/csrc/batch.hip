@@ -156,21 +156,29 @@ __global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
 
 namespace {
 
-// One block's operands for a wave: the four digit planes of its G token groups (lane l: token
-// 16 g + l % 16, elements 8 (l / 16) .. + 7), the table entries of the four tokens whose outputs the
-// lane folds (16 g + 4 (l / 16) + e), and the codes and scales of R row tiles of P matrices (lane l:
-// row l % 16, bytes 8 ((l / 16) & 1) .. + 7 of the block's 16 code bytes).
-template <int P, int G, int R>
-struct BlockOps {
+// A block's input operands for a wave: the four digit planes of its G token groups (lane l: token
+// 16 g + l % 16, elements 8 (l / 16) .. + 7) and the table entries of the four tokens whose outputs
+// the lane folds (16 g + 4 (l / 16) + e).  They come from L2 (the image is shared by all workgroups)
+// and are loaded one block ahead.
+template <int G>
+struct InOps {
     v2u a[4][G];
     v4f tab[G][2];
+};
+
+// A block's weights for R row tiles of P matrices (lane l: row l % 16, bytes 8 ((l / 16) & 1) .. + 7 of
+// the block's 16 code bytes, and the row's fp16 scale).  They stream from HBM and are loaded
+// kCodeAhead blocks ahead.
+template <int P, int R>
+struct WOps {
     uint2 code[R][P];
     uint16_t d[R][P];
 };
 
-template <int P, int G, int R>
-__device__ __forceinline__ void load_block(BlockOps<P, G, R>& o, const BatchGemm& a, uint32_t b, uint32_t rt0,
-                                           uint32_t last_tile, uint32_t lane) {
+constexpr int kCodeAhead = 8;
+
+template <int G>
+__device__ __forceinline__ void load_in(InOps<G>& o, const BatchGemm& a, uint32_t b, uint32_t lane) {
     constexpr uint32_t Tp = 16 * G;
     const uint32_t m = lane & 15, kq = lane >> 4;
     const int8_t* planes = a.img;
@@ -186,6 +194,12 @@ __device__ __forceinline__ void load_block(BlockOps<P, G, R>& o, const BatchGemm
         o.tab[g][0] = *gp(tp);
         o.tab[g][1] = *gp(tp + 1);
     }
+}
+
+template <int P, int R>
+__device__ __forceinline__ void load_w(WOps<P, R>& o, const BatchGemm& a, uint32_t b, uint32_t rt0, uint32_t last_tile,
+                                       uint32_t lane) {
+    const uint32_t m = lane & 15, kq = lane >> 4;
     const uint32_t per_tile = a.w.nst * 4;  // block records per row tile (tiled layout, Q4View)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
@@ -200,26 +214,27 @@ __device__ __forceinline__ void load_block(BlockOps<P, G, R>& o, const BatchGemm
 }
 
 template <int P, int G, int R>
-__device__ __forceinline__ void mfma_block(const BlockOps<P, G, R>& o, uint32_t kq, float (&acc)[R][P][G][4]) {
+__device__ __forceinline__ void mfma_block(const InOps<G>& x, const WOps<P, R>& w, uint32_t kq,
+                                           float (&acc)[R][P][G][4]) {
     const uint32_t sh = kq >= 2 ? 4u : 0u;  // k 0..15: low nibbles, 16..31: high nibbles
     const v4i zero = {0, 0, 0, 0};
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int q = 0; q < P; ++q) {
-            const uint32_t lo = (o.code[r][q].x >> sh) & 0x0F0F0F0Fu, hi = (o.code[r][q].y >> sh) & 0x0F0F0F0Fu;
+            const uint32_t lo = (w.code[r][q].x >> sh) & 0x0F0F0F0Fu, hi = (w.code[r][q].y >> sh) & 0x0F0F0F0Fu;
             const long B = (long)(((uint64_t)hi << 32) | lo);
-            const float d = h2f(o.d[r][q]);
+            const float d = h2f(w.d[r][q]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
                 v4i D[4];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    const long A = (long)(((uint64_t)o.a[i][g].y << 32) | o.a[i][g].x);
+                    const long A = (long)(((uint64_t)x.a[i][g].y << 32) | x.a[i][g].x);
                     D[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
                 }
-                const float tb[8] = {o.tab[g][0].x, o.tab[g][0].y, o.tab[g][0].z, o.tab[g][0].w,
-                                     o.tab[g][1].x, o.tab[g][1].y, o.tab[g][1].z, o.tab[g][1].w};
+                const float tb[8] = {x.tab[g][0].x, x.tab[g][0].y, x.tab[g][0].z, x.tab[g][0].w,
+                                     x.tab[g][1].x, x.tab[g][1].y, x.tab[g][1].z, x.tab[g][1].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     // exact: |I| < 2^30 (|D_i| <= 32 * 15 * 64)
@@ -265,14 +280,22 @@ __global__ __launch_bounds__(256) void batch_gemm_kernel(BatchGemm a) {
             for (int g = 0; g < G; ++g)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[r][q][g][e] = 0.0f;
-    BlockOps<P, G, R> x0, x1;
-    if (b0 < b1) load_block(x0, a, b0, rt0, tiles - 1, lane);
-    for (uint32_t b = b0; b < b1; b += 2) {
-        if (b + 1 < b1) load_block(x1, a, b + 1, rt0, tiles - 1, lane);
-        mfma_block(x0, kq, acc);
-        if (b + 1 >= b1) break;
-        if (b + 2 < b1) load_block(x0, a, b + 2, rt0, tiles - 1, lane);
-        mfma_block(x1, kq, acc);
+    // weights kCodeAhead blocks ahead in a register ring, inputs one block ahead (ping-pong)
+    WOps<P, R> wr[kCodeAhead];
+    InOps<G> xi[2];
+    const uint32_t last_b = nb - 1;
+#pragma unroll
+    for (int u = 0; u < kCodeAhead; ++u) load_w(wr[u], a, min(b0 + u, last_b), rt0, tiles - 1, lane);
+    if (b0 < b1) load_in(xi[0], a, b0, lane);
+    for (uint32_t b = b0; b < b1; b += kCodeAhead) {
+#pragma unroll
+        for (int u = 0; u < kCodeAhead; ++u) {
+            const uint32_t bb = b + u;
+            if (bb >= b1) break;
+            if (bb + 1 < b1) load_in(xi[(u + 1) & 1], a, bb + 1, lane);
+            mfma_block(xi[u & 1], wr[u], kq, acc);
+            load_w(wr[u], a, min(bb + kCodeAhead, last_b), rt0, tiles - 1, lane);
+        }
     }
 #pragma unroll
     for (int r = 0; r < R; ++r)
@@ -317,7 +340,228 @@ __global__ __launch_bounds__(256) void batch_reduce_kernel(BatchGemm a, uint32_t
     gemm_epilogue<P>(a, t, row, v);
 }
 
+// ---- attention of a batch ----------------------------------------------------------------------
+//
+// Grid (nchunks, kv_heads, query tiles): workgroup (c, h, j) takes query tile j of KV head h (queries
+// i = t group + g of its tokens t and query heads h group + g, 16 per tile) against chunk c of the
+// keys, streamed in sub-chunks of KC keys through LDS, with an online softmax.  Both products run
+// on the fp16 matrix cores (v_mfma_f32_16x16x32_f16, fp32 accumulation): the cached K and V are
+// fp16 already, and the fp32 queries and probabilities enter as fp16 pairs hi + lo (hi = f16(x),
+// lo = f16(x - hi)) after scaling by a power of two (queries to below 32 in magnitude, probabilities
+// by 2^14), so each operand keeps about 22 significant bits and every product is exact in fp32.
+
+namespace {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
+    hi = (_Float16)x;
+    lo = (_Float16)(x - (float)hi);  // exact in fp32: hi is the nearest fp16 to x
+}
+
+}  // namespace
+
+template <int D, int KC>
+__global__ __launch_bounds__(256) void batch_attention_kernel(BatchAttn a) {
+    constexpr int KP = D + 8;         // row stride of K and of the query planes (halves)
+    constexpr int VP = KC + 8;        // row stride of V^T and of the probability planes (halves)
+    constexpr int KT = KC / 16;       // 16-key score tiles
+    constexpr int DH = 4 / KT;        // head-width parts per score tile (four waves)
+    constexpr int DS = D / 32 / DH;   // MFMA steps per part
+    constexpr int NT = D / 64;        // 16-channel output tiles per wave
+    __shared__ __align__(16) _Float16 qh[16 * KP], ql[16 * KP];
+    __shared__ __align__(16) _Float16 ks[KC * KP];
+    __shared__ __align__(16) _Float16 vt[D * VP];
+    __shared__ __align__(16) _Float16 ph[16 * VP], pl[16 * VP];
+    __shared__ float sc[DH][16][KC];
+    __shared__ float qscale[16], mrun[16], lrun[16], alpha[16];
+    __shared__ int tok[16], lo_q[16], hi_q[16];
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, m = lane & 15, kq = lane >> 4;
+    const uint32_t c = blockIdx.x, h = blockIdx.y, qt = blockIdx.z;
+    const uint32_t q_heads = a.kv_heads * a.group, nq = a.T * a.group;
+    if (tid < 16) {
+        const uint32_t qi = 16 * qt + tid;
+        const bool ok = qi < nq;
+        const int p = (int)(a.pos0 + (ok ? qi / a.group : 0));
+        tok[tid] = ok ? (int)(qi / a.group) : -1;
+        hi_q[tid] = ok ? p : -1;
+        lo_q[tid] = a.window ? max(0, p + 1 - (int)a.window) : 0;
+        mrun[tid] = -INFINITY;
+        lrun[tid] = 0.0f;
+    }
+    // the tile's queries as scaled fp16 pairs (wave w: rows 4 w .. 4 w + 3)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t r = 4 * wave + i, qi = 16 * qt + r;
+        float v[D / 64];
+        const bool ok = qi < nq;
+        const float* src = a.q + ((size_t)(ok ? qi / a.group : 0) * q_heads + h * a.group + qi % a.group) * D;
+        float mx = 0.0f;
+#pragma unroll
+        for (int j = 0; j < D / 64; ++j) {
+            v[j] = ok ? src[lane + 64 * j] : 0.0f;
+            mx = fmaxf(mx, fabsf(v[j]));
+        }
+        mx = wave_max(mx);
+        const float s = mx > 0.0f ? ldexpf(1.0f, 4 - ilogbf(mx)) : 1.0f;  // |q s| < 32
+#pragma unroll
+        for (int j = 0; j < D / 64; ++j) split_f16(v[j] * s, qh[r * KP + lane + 64 * j], ql[r * KP + lane + 64 * j]);
+        if (lane == 0) qscale[r] = 1.0f / s;
+    }
+    const uint32_t k_begin = a.klo + c * a.span, k_end = min(k_begin + a.span, a.pos0 + a.T);
+    v4f acc[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) acc[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    for (uint32_t k0 = k_begin; k0 < k_end; k0 += KC) {
+        __syncthreads();  // the last sub-chunk's K, V^T, probabilities and alpha are read
+        const uint32_t kn = min((uint32_t)KC, k_end - k0);
+        for (uint32_t i = tid; i < KC * D / 8; i += 256) {  // K rows, 16-byte pieces
+            const uint32_t row = i / (D / 8), pc = i % (D / 8);
+            v4u val = {0u, 0u, 0u, 0u};
+            if (row < kn) val = *gp(reinterpret_cast<const v4u*>(a.kcache + ((size_t)h * a.ring + (k0 + row) % a.ring) * D + 8 * pc));
+            *reinterpret_cast<v4u*>(ks + row * KP + 8 * pc) = val;
+        }
+        for (uint32_t i = tid; i < KC / 2 * (D / 8); i += 256) {  // V rows 2j, 2j + 1 -> V^T
+            const uint32_t j = i / (D / 8), pc = i % (D / 8);
+            v4u v0 = {0u, 0u, 0u, 0u}, v1 = {0u, 0u, 0u, 0u};
+            if (2 * j < kn)
+                v0 = *gp(reinterpret_cast<const v4u*>(a.vcache + ((size_t)h * a.ring + (k0 + 2 * j) % a.ring) * D + 8 * pc));
+            if (2 * j + 1 < kn)
+                v1 = *gp(reinterpret_cast<const v4u*>(a.vcache + ((size_t)h * a.ring + (k0 + 2 * j + 1) % a.ring) * D + 8 * pc));
+            const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {  // channel 8 pc + e: (key 2j, key 2j + 1)
+                const uint32_t d = (e & 1) ? __builtin_amdgcn_perm(w1[e / 2], w0[e / 2], 0x07060302u)
+                                           : __builtin_amdgcn_perm(w1[e / 2], w0[e / 2], 0x05040100u);
+                *reinterpret_cast<uint32_t*>(vt + (8 * pc + e) * VP + 2 * j) = d;
+            }
+        }
+        __syncthreads();
+        {  // scores: wave w -> key tile w % KT, head-width part w / KT; lane: S[4 kq + i][16 kt + m]
+            const uint32_t kt = wave % KT, dp = wave / KT;
+            v4f sv = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int d = 0; d < DS; ++d) {
+                const uint32_t k = 32 * (dp * DS + d) + 8 * kq;
+                const v8h B = *reinterpret_cast<const v8h*>(ks + (16 * kt + m) * KP + k);
+                sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const v8h*>(qh + m * KP + k), B, sv, 0, 0, 0);
+                sv = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const v8h*>(ql + m * KP + k), B, sv, 0, 0, 0);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sc[dp][4 * kq + i][16 * kt + m] = sv[i];
+        }
+        __syncthreads();
+        // online softmax, wave w: queries 4 w .. 4 w + 3, lane = key
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = 4 * wave + i, key = k0 + lane;
+            float s = -INFINITY;
+            if (lane < (uint32_t)KC && tok[r] >= 0 && key < k_end && (int)key >= lo_q[r] && (int)key <= hi_q[r]) {
+                float v = sc[0][r][lane];
+#pragma unroll
+                for (int dp = 1; dp < DH; ++dp) v += sc[dp][r][lane];
+                s = v * qscale[r] * a.scale;
+            }
+            const float mo = mrun[r], mn = fmaxf(mo, wave_max(s));
+            const float p = s == -INFINITY ? 0.0f : expf(s - mn);
+            const float al = mn == -INFINITY ? 1.0f : expf(mo - mn);
+            const float sum = wave_sum(p);
+            if (lane < (uint32_t)KC) split_f16(p * 16384.0f, ph[r * VP + lane], pl[r * VP + lane]);
+            if (lane == 0) {
+                mrun[r] = mn;
+                lrun[r] = fmaf(lrun[r], al, sum);
+                alpha[r] = al;
+            }
+        }
+        __syncthreads();
+        {  // values: wave w -> channel tiles w NT + j; lane: O[4 kq + i][16 (w NT + j) + m]
+            float al[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) al[i] = alpha[4 * kq + i];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[j][i] *= al[i];
+                const uint32_t dim = 16 * (wave * NT + j) + m;
+#pragma unroll
+                for (int kk = 0; kk < KC / 32; ++kk) {
+                    const uint32_t k = 32 * kk + 8 * kq;
+                    const v8h B = *reinterpret_cast<const v8h*>(vt + dim * VP + k);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const v8h*>(ph + m * VP + k), B, acc[j], 0, 0, 0);
+                    acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(*reinterpret_cast<const v8h*>(pl + m * VP + k), B, acc[j], 0, 0, 0);
+                }
+            }
+        }
+    }
+    __syncthreads();
+    // chunk partials: sum p v (the probabilities' 2^14 removed), max, sum p
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = 4 * kq + i;
+            if (tok[r] < 0) continue;
+            const uint32_t qi = 16 * qt + r, row = (uint32_t)tok[r] * q_heads + h * a.group + qi % a.group;
+            a.part[((size_t)row * a.nchunks + c) * (D + 2) + 16 * (wave * NT + j) + m] = acc[j][i] * (1.0f / 16384.0f);
+        }
+    if (tid < 16 && tok[tid] >= 0) {
+        const uint32_t qi = 16 * qt + tid, row = (uint32_t)tok[tid] * q_heads + h * a.group + qi % a.group;
+        float* pr = a.part + ((size_t)row * a.nchunks + c) * (D + 2);
+        pr[D] = mrun[tid];
+        pr[D + 1] = lrun[tid];
+    }
+}
+
+// out[t][qh] = sum_c w_c o_c / sum_c w_c l_c, w_c = exp(m_c - max_c m_c), chunks in order; one
+// workgroup per (token, query head), one thread per channel.
+template <int D>
+__global__ __launch_bounds__(D) void batch_attention_merge_kernel(BatchAttn a) {
+    const uint32_t row = blockIdx.x, q_heads = a.kv_heads * a.group, t = row / q_heads, qh = row % q_heads;
+    const float* pr = a.part + (size_t)row * a.nchunks * (D + 2);
+    float M = -INFINITY;
+    for (uint32_t c = 0; c < a.nchunks; ++c) M = fmaxf(M, pr[c * (D + 2) + D]);
+    float L = 0.0f, acc = 0.0f;
+    for (uint32_t c = 0; c < a.nchunks; ++c) {
+        const float mc = pr[c * (D + 2) + D];
+        const float w = mc == -INFINITY ? 0.0f : expf(mc - M);
+        L = fmaf(w, pr[c * (D + 2) + D + 1], L);
+        acc = fmaf(w, pr[c * (D + 2) + threadIdx.x], acc);
+    }
+    a.out[(size_t)t * a.out_stride + (size_t)qh * D + threadIdx.x] = acc / L;
+}
+
 // ---- launchers ----------------------------------------------------------------------------------
+
+// Chunks of the batch's key range: about one per 64 keys, at most kBatchAttnChunks (a chunk then
+// spans several sub-chunks).
+hipError_t launch_batch_attention(BatchAttn a, uint32_t head_width, hipStream_t s) {
+    if (a.T == 0 || a.T > kBatchMax || a.kv_heads == 0 || a.group == 0) return hipErrorInvalidValue;
+    const uint32_t KC = head_width == 256 ? 64 : 32;
+    const int64_t lo = a.window ? std::max<int64_t>(0, (int64_t)a.pos0 + 1 - a.window) : 0;
+    const uint32_t keys = a.pos0 + a.T - (uint32_t)lo;
+    const uint32_t sub = (keys + KC - 1) / KC;
+    const uint32_t per = (sub + kBatchAttnChunks - 1) / kBatchAttnChunks;
+    a.klo = (uint32_t)lo;
+    a.span = per * KC;
+    a.nchunks = (keys + a.span - 1) / a.span;
+    const uint32_t tiles = (a.T * a.group + 15) / 16;
+    const dim3 grid(a.nchunks, a.kv_heads, tiles);
+    if (head_width == 256) {
+        hipLaunchKernelGGL((batch_attention_kernel<256, 64>), grid, dim3(256), 0, s, a);
+        if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+        hipLaunchKernelGGL((batch_attention_merge_kernel<256>), dim3(a.T * a.kv_heads * a.group), dim3(256), 0, s, a);
+    } else if (head_width == 512) {
+        hipLaunchKernelGGL((batch_attention_kernel<512, 32>), grid, dim3(256), 0, s, a);
+        if (hipGetLastError() != hipSuccess) return hipErrorLaunchFailure;
+        hipLaunchKernelGGL((batch_attention_merge_kernel<512>), dim3(a.T * a.kv_heads * a.group), dim3(512), 0, s, a);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 
 size_t batch_image_bytes(uint32_t blocks, uint32_t tokens) {
     return (size_t)blocks * padded_tokens(tokens) * (4 * 32 + 8);

@@ -446,7 +446,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     const uint32_t qgroups = a.group / G;
     const uint32_t c = blockIdx.x, kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
     const uint32_t qh0 = kvh * a.group + qg * G;
-    if (a.mode == ATT_APPEND ? qg != 0 : c >= chunks) return;
+    if (a.mode == ATT_APPEND ? qg != 0 && !a.q_out : c >= chunks) return;
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
     const uint32_t n = t1 - t0;
     const uint32_t ring = a.ring;
@@ -510,7 +510,14 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         a.kcache[slot + tid] = knew[tid];
         a.vcache[slot + tid] = vnew[tid];
     }
-    if (a.mode == ATT_APPEND) return;
+    if (a.mode == ATT_APPEND) {
+        if (a.q_out) {
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi)
+                a.q_out[((size_t)z * a.kv_heads * a.group + qh0 + gi) * D + tid] = qs[gi][tid];
+        }
+        return;
+    }
 
     // ---- scores: LK lanes per token (16 channels each), TG token groups, two tokens in flight
     {
