@@ -38,11 +38,14 @@ uint32_t padded_tokens(uint32_t T) { return (T + 15) / 16 * 16; }
 struct GemmPlan {
     uint32_t R, S;
 };
-GemmPlan gemm_plan(uint32_t rows, uint32_t blocks) {
-    const uint32_t tiles = (rows + 15) / 16;
-    const uint32_t R = tiles >= kGemmTargetGrid ? 2 : 1;
+// The digit image is read by every workgroup of a K range, R row tiles at a time, so R sets its
+// reuse: up to 8 tiles (4 of each matrix of a gate/up pair) while at least 32 row groups remain.
+GemmPlan gemm_plan(uint32_t rows, uint32_t blocks, bool pair) {
+    const uint32_t tiles = (rows + 15) / 16, r_max = pair ? 4 : 8;
+    uint32_t R = 1;
+    while (R < r_max && tiles >= 64 * R) R *= 2;
     const uint32_t wgs = (tiles + R - 1) / R;
-    uint32_t S = std::max<uint32_t>(1, std::min<uint32_t>(8, kGemmTargetGrid / wgs));
+    uint32_t S = std::max<uint32_t>(1, std::min<uint32_t>(32, (kGemmTargetGrid + wgs - 1) / wgs));
     S = std::max<uint32_t>(1, std::min(S, blocks / 8));
     return GemmPlan{R, S};
 }
@@ -175,7 +178,9 @@ struct WOps {
     uint16_t d[R][P];
 };
 
-constexpr int kCodeAhead = 8;
+// weight blocks in flight per wave: 8, or 2 when a block spans 4 or more tiles
+template <int P, int R>
+constexpr int code_ahead() { return R * P >= 4 ? 2 : 8; }
 
 template <int G>
 __device__ __forceinline__ void load_in(InOps<G>& o, const BatchGemm& a, uint32_t b, uint32_t lane) {
@@ -281,6 +286,7 @@ __global__ __launch_bounds__(256) void batch_gemm_kernel(BatchGemm a) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[r][q][g][e] = 0.0f;
     // weights kCodeAhead blocks ahead in a register ring, inputs one block ahead (ping-pong)
+    constexpr int kCodeAhead = code_ahead<P, R>();
     WOps<P, R> wr[kCodeAhead];
     InOps<G> xi[2];
     const uint32_t last_b = nb - 1;
@@ -568,7 +574,7 @@ size_t batch_image_bytes(uint32_t blocks, uint32_t tokens) {
 }
 
 size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair) {
-    const GemmPlan p = gemm_plan(rows, blocks);
+    const GemmPlan p = gemm_plan(rows, blocks, gelu_pair);
     if (p.S == 1) return 0;
     return (size_t)p.S * (gelu_pair ? 2 : 1) * padded_tokens(tokens) * ((rows + 15) / 16 * 16) * 4;
 }
@@ -588,12 +594,18 @@ hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
 
 template <int P, int G>
 static hipError_t gemm_launch(const BatchGemm& a, hipStream_t s) {
-    const GemmPlan p = gemm_plan(a.w.rows, a.w.blocks);
+    const GemmPlan p = gemm_plan(a.w.rows, a.w.blocks, P == 2);
     const uint32_t tiles = (a.w.rows + 15) / 16;
     const dim3 grid((tiles + p.R - 1) / p.R, p.S);
     if (p.S > 1 && !a.part) return hipErrorInvalidValue;
-    if (p.R == 2) hipLaunchKernelGGL((batch_gemm_kernel<P, G, 2>), grid, dim3(kGemmThreads), 0, s, a);
-    else hipLaunchKernelGGL((batch_gemm_kernel<P, G, 1>), grid, dim3(kGemmThreads), 0, s, a);
+    switch (p.R) {
+        case 1: hipLaunchKernelGGL((batch_gemm_kernel<P, G, 1>), grid, dim3(kGemmThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((batch_gemm_kernel<P, G, 2>), grid, dim3(kGemmThreads), 0, s, a); break;
+        case 4: hipLaunchKernelGGL((batch_gemm_kernel<P, G, 4>), grid, dim3(kGemmThreads), 0, s, a); break;
+        default:
+            if constexpr (P == 1) hipLaunchKernelGGL((batch_gemm_kernel<P, G, 8>), grid, dim3(kGemmThreads), 0, s, a);
+            break;
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.S == 1) return e;
     const uint32_t n = a.T * a.w.rows;
