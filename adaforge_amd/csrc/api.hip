@@ -1801,6 +1801,10 @@ int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint
         history.push_back(id);
         if (on_token) on_token(user, id);
     };
+    // A verification pass costs a few decode steps, so after a pass that accepts nothing the next
+    // `skip` tokens are decoded without drafting (doubling on each further miss, reset by a hit);
+    // the ids are the same either way.
+    uint32_t skip = 0, backoff = 0;
     while (ids.size() < max_new) {
         if (is_stop(next)) {
             stopped = true;
@@ -1810,7 +1814,9 @@ int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint
         const size_t remaining = max_new - ids.size();
         const size_t room = s->capacity > pos + 1 ? s->capacity - (pos + 1) : 0;
         const size_t limit = std::min({remaining, room, (size_t)s->spec_depth, (size_t)kVerifyMax - 1});
-        const std::vector<uint32_t> draft = draft_lookup(history, limit);
+        std::vector<uint32_t> draft;
+        if (skip) --skip;
+        else draft = draft_lookup(history, limit);
         if (draft.empty()) {
             HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + pos, &next, 4, hipMemcpyHostToDevice, st), "id upload");
             if ((rc = step(next))) return rc;
@@ -1847,6 +1853,12 @@ int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint
         s->spec_drafted += draft.size();
         s->spec_accepted += keep;
         ++s->spec_passes;
+        if (keep == 0) {
+            backoff = std::min<uint32_t>(2 * backoff + 2, 32);
+            skip = backoff;
+        } else {
+            backoff = 0;
+        }
         if (stopped) break;
         next = predicted;
     }
