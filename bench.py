@@ -22,7 +22,13 @@ kernel reads slower here than in the rocprofv3 kernel trace under profiles/).
 CPU baseline: the C oracle (a port of the reference's FP64 CPU path), on this host: config 4 on
 all of the box's CPU share (16 threads at most) and on one core, configs 0-3 in both modes.
 
-    python bench.py [--gpus 1] [--steps 240] [--warmup 16] [--no-cpu] [--no-configs]
+Beside the headline (`prefill` and `speculative` in the JSON line): a 512-id prompt prefilled on
+the config-4 model through the batched layers (32 positions per weight pass) and one step-kernel
+launch per position; and greedy speculative decoding with prompt-lookup drafts on a copying
+workload (config-4 shapes, local layers only, a prompt that repeats the model's own continuation),
+against plain decoding of the same prompt.
+
+    python bench.py [--gpus 1] [--steps 240] [--warmup 16] [--no-cpu] [--no-configs] [--no-extras]
 """
 import argparse
 import ctypes
@@ -290,7 +296,7 @@ def cpu_decode(model, prompt, tokens, threads):
 
 # ---- the headline: config 4 -------------------------------------------------------------------------
 
-def measured_traffic(kernel="void af::decode_step_kernel<2>(af::StepArgs)"):
+def measured_traffic(kernel="void af::decode_step_kernel<2, true>(af::StepArgs)"):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
     (profiles/traffic_config4.json, calibrated against a copy of known size), or None."""
     path = os.path.join(ROOT, "profiles", "traffic_config4.json")
@@ -310,6 +316,75 @@ def kv_read_bytes(model, tokens):
     return total
 
 
+def open_env(model, capacity, **env):
+    """A session opened with the given AF_* switches set (restored afterwards)."""
+    from adaforge_amd.backend import HipDiagnostics
+    saved = {k: os.environ.get(k) for k in env}
+    os.environ.update({k: str(v) for k, v in env.items()})
+    try:
+        return HipDiagnostics().open_session(model, capacity)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                del os.environ[k]
+            else:
+                os.environ[k] = v
+
+
+def prefill_leg(model, stop, tokens=512):
+    """Prefill of a `tokens`-id prompt on the config-4 model: batched (32 positions per weight pass,
+    the default) against one step-kernel launch per position (AF_PREFILL_BATCH=0); the first generated
+    id must agree."""
+    from adaforge_amd import synth
+    prompt = [int(i) for i in synth.prompt_ids(tokens, model.vocabulary, name="config4.prefill")]
+    out = {"prompt_tokens": tokens}
+    first = {}
+    for name, batch in (("batched", 32), ("stepwise", 0)):
+        with open_env(model, tokens + 8, AF_PREFILL_BATCH=batch) as s:
+            s.generate(prompt[:40], stop, 1)  # allocations and graph warm-up
+            s.reset()
+            r = s.generate(prompt, stop, 1)
+        ms = r.stats.prefill_ms
+        first[name] = r.ids
+        out[name] = {"ms": round(ms, 2), "tok_s": round((tokens - 1) / ms * 1000.0, 1)}
+        log(f"prefill {tokens} tokens ({name}): {ms:.1f} ms -> {out[name]['tok_s']} tok/s")
+    out["same_first_id"] = first["batched"] == first["stepwise"]
+    return out
+
+
+def speculative_leg(lead_tokens=160, new_tokens=128):
+    """Greedy speculative decoding (AF_SPECULATIVE=1) on a copying workload: the config-4 shapes
+    with every layer local (window 4, so each position depends on at most the 145 before it), and a
+    prompt lead + G + lead where G is the model's own greedy continuation of lead, so that the
+    continuation repeats G and prompt lookup drafts it.  Decode tok/s with and without speculation;
+    the ids must agree."""
+    from adaforge_amd import synth
+    model = synth.model(name="config4-local", window=4, global_every=1000)
+    stop = [model.vocabulary - 1]
+    lead = [int(i) for i in synth.prompt_ids(lead_tokens, model.vocabulary, name="spec.lead")]
+    cap = 2 * lead_tokens + 2 * new_tokens + 8
+    with open_env(model, cap) as s:
+        g = s.generate(lead, stop, new_tokens).ids
+    prompt = lead + g + lead
+    out = {"workload": f"48 local layers (window 4) of the config-4 shapes, prompt = {lead_tokens} ids + the "
+                       f"model's {new_tokens}-id greedy continuation of them + the {lead_tokens} ids again, "
+                       f"{new_tokens} new ids"}
+    ids = {}
+    for name, spec in (("plain", 0), ("speculative", 1)):
+        with open_env(model, cap, AF_SPECULATIVE=spec) as s:
+            r = s.generate(prompt, stop, new_tokens)
+            st = s.speculation()
+        tok_s = r.stats.decode_tokens / r.stats.decode_ms * 1000.0
+        ids[name] = r.ids
+        out[name] = {"decode_tok_s": round(tok_s, 1)}
+        if spec:
+            out[name].update({"passes": st[0], "drafted": st[1], "accepted": st[2]})
+        log(f"copying workload ({name}): {tok_s:.1f} tok/s {out[name]}")
+    out["same_ids"] = ids["plain"] == ids["speculative"]
+    out["speedup"] = round(out["speculative"]["decode_tok_s"] / out["plain"]["decode_tok_s"], 2)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -319,6 +394,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true", help="skip the configs 0-3 operator legs")
     ap.add_argument("--configs-only", action="store_true", help="only the configs 0-3 GPU legs (profiling)")
+    ap.add_argument("--no-extras", action="store_true", help="skip the prefill and speculative-decoding legs")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
@@ -398,6 +474,11 @@ def main():
     if not a.no_configs:
         configs = gpu_configs()
 
+    prefill = spec = None
+    if not a.no_extras:
+        prefill = prefill_leg(model, stop)
+        spec = speculative_leg()
+
     cpu = None
     if not a.no_cpu:
         threads = host_threads()
@@ -457,6 +538,8 @@ def main():
             "timeline_avg_us": round(1000.0 * tms / max(tn, 1), 2),
         },
         "configs": configs,
+        "prefill": prefill,
+        "speculative": spec,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
