@@ -7,85 +7,164 @@
 
 namespace af {
 
+// ---- Q4_0 GEMV: persistent, one workgroup per CU ----------------------------------------------
+//
+// The output rows come in units of one 16-row tile (T = 2: the same tile of the gate and the up
+// matrix).  Workgroup b takes units b, b + G, ... (G = grid size); the super-tiles of its units,
+// flattened in (unit, matrix, super-tile) order, are dealt round-robin to its 8 waves, so every
+// wave streams one sequence of records across tile boundaries.  Each wave keeps kGemvRing records
+// in flight in registers: it folds a record, then requests the one kGemvRing places further on,
+// with the same two load instructions whether that record exists or not (past the end the
+// buffer's range is 0 and the load returns zeros without a memory access), so the compiler's
+// wait for each record is an exact count.  The first records are requested before the prologue
+// builds the input's digit image, which thus runs while they are in flight.  A wave adds each
+// tile's row sums to LDS once, when its records move on to the next tile; the epilogue adds the
+// 8 waves' partials of a row in wave order.
+constexpr int kGemvRing = 8;             // records in flight per wave
+constexpr uint32_t kGemvMaxUnits = 8;    // units per workgroup (more units: a larger grid)
+constexpr uint32_t kGemvWaves = 8;
+
+struct GemvCursor {
+    uint32_t j, k, st;  // unit of the workgroup, matrix, super-tile (wave-uniform)
+};
+
+__device__ __forceinline__ void gemv_advance(GemvCursor& c, uint32_t nst, uint32_t T) {
+    c.st += kGemvWaves;
+    while (c.st >= nst) {
+        c.st -= nst;
+        if (++c.k == T) {
+            c.k = 0;
+            ++c.j;
+        }
+    }
+}
+
 template <int T, int IN, int OUT, int Q>
-__global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_rows) {
+__global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_rows, uint32_t units) {
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[8];
-    __shared__ float part[T][8][16];
+    __shared__ float part[kGemvWaves][kGemvMaxUnits * T][16];
 
     if (a.state && a.state[ST_STOP]) return;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-    const uint32_t S = a.slices, tile = wave / S, sl = wave % S;
-    const Q4View& m = (T == 2 && tile == 1) ? a.w2 : a.w;
+    const uint32_t G = gridDim.x, b = blockIdx.x;
     const uint32_t B = a.w.blocks, K = B * 32, nst = a.w.nst;
-    const uint32_t per = (nst + S - 1) / S, st0 = min(nst, sl * per), st1 = min(nst, st0 + per);
-    const uint32_t q = lane >> 4, n = lane & 15;  // D tile: rows 4q..4q+3, column n
+    const uint32_t nu = (units - b + G - 1) / G;  // the grid never exceeds the units
+    const uint32_t N = nu * T * nst;               // records of this workgroup
+    const uint32_t n_w = N > wave ? (N - wave + kGemvWaves - 1) / kGemvWaves : 0;
 
-    const uint4* codes = reinterpret_cast<const uint4*>(m.codes);
-    const uint2* scales = reinterpret_cast<const uint2*>(m.scales);
-    auto load = [&](Q4Tile (&buf)[kQ4Ahead], uint32_t c0) {
-#pragma unroll
-        for (int u = 0; u < kQ4Ahead; ++u) {
-            const uint32_t st = c0 + u;
-            if (st < st1) q4_tile_load(codes, scales, blockIdx.x, nst, st, lane, buf[u]);
+    // record r = wave + 8 i of the workgroup's sequence
+    GemvCursor ld{0, 0, wave};
+    while (ld.st >= nst) {  // more waves than one tile's super-tiles
+        ld.st -= nst;
+        if (++ld.k == (uint32_t)T) {
+            ld.k = 0;
+            ++ld.j;
         }
+    }
+    GemvCursor cs = ld;
+    const uint32_t code_off = lane * 16, scale_off = ((((lane & 15) >> 2) * 4) + (lane >> 4)) * 8;
+    v4u rc[kGemvRing];
+    v2u rsc[kGemvRing];
+    auto request = [&](int u, const GemvCursor& c, bool ok) {
+        const bool second = T == 2 && c.k == 1;
+        const uint8_t* codes = second ? a.w2.codes : a.w.codes;
+        const uint16_t* scales = second ? a.w2.scales : a.w.scales;
+        const size_t rec = (size_t)(b + c.j * G) * nst + c.st;
+        const __amdgpu_buffer_rsrc_t rcode =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(codes) + rec * 1024, 0, ok ? 1024 : 0, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rscale =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(scales) + rec * 64, 0, ok ? 128 : 0, 0x00020000);
+        rc[u] = __builtin_amdgcn_raw_buffer_load_b128(rcode, code_off, 0, 2);
+        rsc[u] = __builtin_amdgcn_raw_buffer_load_b64(rscale, scale_off, 0, 2);
     };
+
     InputRegs<IN, Q> g;
     input_load<IN, Q>(a.in, K, nst, g);  // inputs first (see input_load)
     __builtin_amdgcn_sched_barrier(0);
-    Q4Tile buf[kQ4Ahead];
-    load(buf, st0);
+#pragma unroll
+    for (int u = 0; u < kGemvRing; ++u) {
+        request(u, ld, (uint32_t)u < n_w);
+        gemv_advance(ld, nst, T);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
     const size_t xs_bytes = IN == IN_EMBED ? (size_t)K * 4 : 0;
     int8_t* dig = reinterpret_cast<int8_t*>(smem + xs_bytes);
     DigitTab* tab = reinterpret_cast<DigitTab*>(smem + xs_bytes + (size_t)nst * 512);
     input_digits<IN, Q>(a.in, K, nst, g, reinterpret_cast<float*>(smem), dig, tab, red);
+    float* pflat = &part[0][0][0];
+    for (uint32_t i = tid; i < kGemvWaves * kGemvMaxUnits * T * 16; i += blockDim.x) pflat[i] = 0.0f;
     __syncthreads();
 
+    const uint32_t q = lane >> 4, n = lane & 15;  // D tile: rows 4q..4q+3, column n
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t c0 = st0; c0 < st1; c0 += kQ4Ahead) {
+    uint32_t cur = cs.j * T + cs.k;
+    auto flush = [&]() {
+        q4_row_sums(acc);
+        if (n == 0) {
 #pragma unroll
-        for (int u = 0; u < kQ4Ahead; ++u) {
-            const uint32_t st = c0 + u;
-            if (st >= st1) break;
-            q4_mfma_tile(buf[u], st, dig, tab, lane, acc);
+            for (int i = 0; i < 4; ++i) part[wave][cur][4 * q + i] = acc[i];
         }
-        if (c0 + kQ4Ahead < st1) load(buf, c0 + kQ4Ahead);
-    }
-    // sum the 16 columns of each row, then the slices
-    q4_row_sums(acc);
-    if (n == 0) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) part[tile][sl][4 * q + i] = acc[i];
+        for (int i = 0; i < 4; ++i) acc[i] = 0.f;
+    };
+    for (uint32_t i0 = 0; i0 < n_w; i0 += kGemvRing) {
+#pragma unroll
+        for (int u = 0; u < kGemvRing; ++u) {
+            const uint32_t i = i0 + u;
+            if (i < n_w) {
+                const uint32_t sl = cs.j * T + cs.k;
+                if (sl != cur) {
+                    flush();
+                    cur = sl;
+                }
+                const Q4Tile w{make_uint4(rc[u].x, rc[u].y, rc[u].z, rc[u].w), make_uint2(rsc[u].x, rsc[u].y)};
+                q4_mfma_tile(w, cs.st, dig, tab, lane, acc);
+                gemv_advance(cs, nst, T);
+            }
+            request(u, ld, i + kGemvRing < n_w);
+            gemv_advance(ld, nst, T);
+        }
     }
+    if (n_w > 0) flush();
     __syncthreads();
-    if (tid < 16) {
+
+    for (uint32_t i = tid; i < nu * 16; i += blockDim.x) {
+        const uint32_t j = i >> 4, r = i & 15, row = (b + j * G) * 16 + r;
+        if (row >= out_rows) continue;
         float v[T];
 #pragma unroll
         for (int k = 0; k < T; ++k) {
-            float s = part[k][0][tid];
-            for (uint32_t j = 1; j < S; ++j) s += part[k][j][tid];
+            float s = part[0][j * T + k][r];
+            for (uint32_t w = 1; w < kGemvWaves; ++w) s += part[w][j * T + k][r];
             v[k] = s;
         }
-        const uint32_t row = blockIdx.x * 16 + tid;
-        if (row < out_rows) {
-            if constexpr (OUT == OUT_GELU) a.y[row] = gelu_mul(v[0], v[T - 1]);
-            else if constexpr (OUT == OUT_ADD) a.y[row] = __fadd_rn(v[0], a.add[row]);
-            else a.y[row] = v[0];
-        }
+        if constexpr (OUT == OUT_GELU) a.y[row] = gelu_mul(v[0], v[T - 1]);
+        else if constexpr (OUT == OUT_ADD) a.y[row] = __fadd_rn(v[0], a.add[row]);
+        else a.y[row] = v[0];
     }
 }
 
-// Every GEMV block has 512 threads: T row tiles, each split over 8 / T waves by super-tile.
 constexpr uint32_t kQ4Threads = 512;
+
+// One workgroup per CU, more when the units would exceed kGemvMaxUnits per workgroup.
+static uint32_t gemv_grid(uint32_t units) {
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const uint32_t need = (units + kGemvMaxUnits - 1) / kGemvMaxUnits;
+    return min(units, max((uint32_t)cus, need));
+}
 
 template <int T, int IN, int OUT, int Q>
 static hipError_t q4_launch3(Q4Args a, uint32_t out_rows, hipStream_t st) {
-    const uint32_t tiles = (out_rows + 15) / 16;
-    a.slices = kQ4Threads / 64 / T;
+    const uint32_t units = (out_rows + 15) / 16;
+    if (units == 0) return hipSuccess;
+    a.slices = kGemvWaves;
     const size_t lds = (IN == IN_EMBED ? (size_t)a.w.blocks * 32 * 4 : 0) + (size_t)a.w.nst * (512 + 128);
-    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT, Q>), dim3(tiles), dim3(kQ4Threads), lds, st, a, out_rows);
+    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT, Q>), dim3(gemv_grid(units)), dim3(kQ4Threads), lds, st, a, out_rows,
+                       units);
     return hipGetLastError();
 }
 
