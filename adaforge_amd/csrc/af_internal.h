@@ -156,7 +156,7 @@ struct AttnArgs {
     const uint32_t* state;   // non-null: position = state[ST_POS]
     uint32_t position;
     float* out;              // [q_heads][head_width]
-    float* part;             // [tokens][kv_heads * group / G][cmax][G][head_width + 2] (G: attention_block_heads)
+    float* part;             // [tokens][kv_heads * group / G][cmax][G][attn_part_row(head_width)] (G: attention_block_heads)
     uint32_t* counters;      // [tokens][kv_heads * group / G], zero between launches
     int8_t* dig_out;         // digit image of `out` for the output projection (may be null)
     uint32_t cmax;
@@ -260,6 +260,9 @@ hipError_t launch_zero_words(uint32_t* p, uint32_t n, hipStream_t s);
 uint32_t head_grid(uint32_t rows);
 
 constexpr uint32_t kAttnMinChunk = 32;
+// A query head's chunk partial in attention_kernel's split-K scratch: D sums, the chunk's max and
+// sum, padded so that every row starts on a 16-byte boundary.
+__host__ __device__ constexpr uint32_t attn_part_row(uint32_t D) { return D + 4; }
 constexpr uint32_t kAttnMaxChunkLen = 2048;
 constexpr uint32_t kAttnMaxChunks = 64;  // cmax bound: capacity <= 64 * kAttnMaxChunkLen
 constexpr uint32_t kHeadRows = 4;  // rows per wave iteration in the head kernel

@@ -760,7 +760,7 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     if (nvis > kAttnMaxChunks * kAttnMaxChunkLen) return fail(AF_ERR_INVALID, "visible range above 131072 tokens");
     const uint32_t cmax = kAttnMaxChunks;
     std::lock_guard<std::mutex> lock(g_scratch.mu);
-    if ((rc = grow(g_scratch.attn_part, (size_t)p->config.kv_heads * cmax * group * (D + 2) * 4, false, "attention scratch")))
+    if ((rc = grow(g_scratch.attn_part, (size_t)p->config.kv_heads * cmax * group * attn_part_row(D) * 4, false, "attention scratch")))
         return rc;
     if ((rc = grow(g_scratch.attn_counters, (size_t)std::max<uint32_t>(64, p->config.q_heads) * 4, true,
                    "attention counters")))
@@ -1619,7 +1619,8 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         max_kv = std::max(max_kv, L.kv_heads);
         max_q = std::max(max_q, L.qn);
         max_group = std::max(max_group, L.q_heads / L.kv_heads);
-        max_qh_part = std::max(max_qh_part, L.q_heads * (L.width + 2));  // attention_kernel's partials per chunk
+        // per chunk: attention_kernel's partials (attn_part_row), at least the batched attention's (width + 2)
+        max_qh_part = std::max(max_qh_part, L.q_heads * attn_part_row(L.width));
         max_qh = std::max(max_qh, L.q_heads);
         s->max_qkv = std::max(s->max_qkv, L.qkv.rows);
         s->max_kv_rows = std::max(s->max_kv_rows, L.kn);

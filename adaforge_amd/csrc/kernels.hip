@@ -7,6 +7,14 @@
 
 namespace af {
 
+// Cross-workgroup partials (argmax, attention chunks) are combined by the last workgroup to finish.
+// The workgroups run on all 8 XCDs, whose L2s are not coherent with each other, so the partials
+// are stored through to the memory side (policy sc1) and waited for before an agent-scope ticket,
+// and the last workgroup reads them from the memory side: no device-scope fence, which would write
+// back and invalidate the L2.
+constexpr int kPartSC1 = 16;       // buffer access policy sc1: through to (or from) the memory side
+constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), expcnt and lgkmcnt unconstrained
+
 // ---- Q4_0 GEMV: persistent, one workgroup per CU ----------------------------------------------
 //
 // The output rows come in units of one 16-row tile (T = 2: the same tile of the gate and the up
@@ -390,18 +398,20 @@ __global__ __launch_bounds__(512) void q6_head_kernel(HeadArgs a) {
             }
             bad |= wb[w];
         }
-        a.partial[blockIdx.x] = make_uint4(__float_as_uint(bv), bi, bad, 0u);
-        __threadfence();
-        const uint32_t ticket = atomicAdd(a.counter, 1u);
+        __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(bv), bi, bad, 0u},
+                                               __builtin_amdgcn_make_buffer_rsrc(a.partial, 0, 0x7FFFFFFF, 0x00020000),
+                                               blockIdx.x * 16, 0, kPartSC1);
+        __builtin_amdgcn_s_waitcnt(kWaitVm0);
+        const uint32_t ticket = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = ticket == gridDim.x - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(a.partial, 0, 0x7FFFFFFF, 0x00020000);
     float v = -INFINITY;
     uint32_t id = 0xFFFFFFFFu, flag = 0;
     for (uint32_t b = threadIdx.x; b < gridDim.x; b += blockDim.x) {
-        const uint4 p = a.partial[b];
+        const v4u p = __builtin_amdgcn_raw_buffer_load_b128(prs, b * 16, 0, kPartSC1);
         const float pv = __uint_as_float(p.x);
         if (better(pv, p.y, v, id)) {
             v = pv;
@@ -456,7 +466,7 @@ __global__ __launch_bounds__(512) void q6_head_kernel(HeadArgs a) {
                 a.records[pos + 1] = rc;
             }
         }
-        *a.counter = 0u;
+        __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -499,10 +509,12 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     constexpr int W = D / 64;     // waves
     constexpr int LK = D / 16;    // lanes per token in the score loop (16 channels each)
     constexpr int TG = D / LK;    // token groups in the score loop (16)
+    constexpr int UK = 8;         // cached K rows in flight per score-loop lane group
+    constexpr int UV = 8;         // cached V rows in flight per value-loop lane group
     __shared__ float nrm[NH][D];
     __shared__ float qs[G][D];
     __shared__ float scores[G][kAttnMaxChunkLen];
-    __shared__ float vred[8][G][D];
+    __shared__ __align__(16) float vred[8][G][D];
     __shared__ double dred[W][NH];
     __shared__ float fred[8];
     __shared__ float cw[G][kAttnMaxChunks];
@@ -534,14 +546,35 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     const bool append = has_new && qg == 0;  // and this block stores them in the cache
     const int nh = has_new ? NH : G;
 
-    // ---- prologue: RMSNorm of the query heads (and new K, V) with one block reduction, then RoPE
+    // The prologue's inputs are requested first (vector loads return in issue order), then the
+    // score loop's first batch of cached K rows, which the prologue's arithmetic does not wait for:
+    // UK tokens per lane group, rows past the chunk clamped to its last one (the new token's row is
+    // read from LDS instead; its cache slot may be written meanwhile).
     float raw[NH];
 #pragma unroll
     for (int h = 0; h < G; ++h) raw[h] = q_raw[(size_t)(qh0 + h) * D + tid];
     raw[G] = has_new ? k_raw[(size_t)kvh * D + tid] : 0.0f;
     raw[G + 1] = has_new ? v_raw[(size_t)kvh * D + tid] : 0.0f;
+    const float qnw = a.q_norm[tid], knw = has_new ? a.k_norm[tid] : 0.0f;
+    const double ifreq = tid < D / 2 ? a.inv_freq[tid] : 0.0;
+    __builtin_amdgcn_sched_barrier(0);
+    const uint32_t grp = tid / LK, j = tid % LK;
+    uint4 kb[UK][2];
+    auto load_k = [&](uint32_t tb) {
+#pragma unroll
+        for (int u = 0; u < UK; ++u) {
+            const uint32_t tt = min(tb + TG * u, t1 - 1);
+            const uint4* kp = reinterpret_cast<const uint4*>(a.kcache + ((size_t)kvh * ring + tt % ring) * D + 16 * j);
+            kb[u][0] = kp[0];
+            kb[u][1] = kp[1];
+        }
+    };
+    if (a.mode != ATT_APPEND) load_k(t0 + grp);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- prologue: RMSNorm of the query heads (and new K, V) with one block reduction, then RoPE
     double sn = 0.0, cs = 1.0;
-    if (tid < D / 2) sincos((double)pos * a.inv_freq[tid], &sn, &cs);
+    if (tid < D / 2) sincos((double)pos * ifreq, &sn, &cs);
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         const double v = wave_sum((double)raw[h] * (double)raw[h]);
@@ -558,8 +591,8 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
             ss = ((dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h])) +
                  ((dred[4][h] + dred[5][h]) + (dred[6][h] + dred[7][h]));
         }
-        if (h < G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.q_eps), a.q_norm[tid]);
-        else if (h == G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.k_eps), a.k_norm[tid]);
+        if (h < G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.q_eps), qnw);
+        else if (h == G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.k_eps), knw);
         else nrm[h][tid] = a.v_norm ? (float)__dmul_rn((double)raw[h], inv_rms(ss, D, a.v_eps)) : raw[h];
     }
     __syncthreads();
@@ -598,30 +631,25 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         return;
     }
 
-    // ---- scores: LK lanes per token (16 channels each), TG token groups, two tokens in flight
+    // ---- scores: LK lanes per token (16 channels each), TG token groups, UK tokens per group in flight
     {
-        const uint32_t grp = tid / LK, j = tid % LK;
         float qr[G][16];
 #pragma unroll
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 16; ++e) qr[gi][e] = qs[gi][16 * j + e];
-        for (uint32_t tb = t0 + grp; tb < t1; tb += 2 * TG) {
-            uint4 k[2][2];
+        for (uint32_t tb = t0 + grp; tb < t1; tb += UK * TG) {
+            if (tb != t0 + grp) load_k(tb);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < UK; ++u) {
                 const uint32_t t = tb + TG * u;
-                const uint32_t tt = t < t1 ? t : tb;
-                const uint16_t* kp =
-                    (has_new && tt == pos ? knew : a.kcache + ((size_t)kvh * ring + tt % ring) * D) + 16 * j;
-                k[u][0] = *reinterpret_cast<const uint4*>(kp);
-                k[u][1] = *reinterpret_cast<const uint4*>(kp + 8);
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t t = tb + TG * u;
-                const uint32_t kw[8] = {k[u][0].x, k[u][0].y, k[u][0].z, k[u][0].w,
-                                        k[u][1].x, k[u][1].y, k[u][1].z, k[u][1].w};
+                if (t >= t1) break;
+                uint4 k0 = kb[u][0], k1 = kb[u][1];
+                if (has_new && t == pos) {
+                    k0 = *reinterpret_cast<const uint4*>(knew + 16 * j);
+                    k1 = *reinterpret_cast<const uint4*>(knew + 16 * j + 8);
+                }
+                const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
                 float kf[16];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -635,52 +663,75 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
                     for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
                     d = row_sum(d);
                     if constexpr (LK == 32) d += __shfl_xor(d, 16);  // the token's second row of 16 lanes
-                    if (j == 0 && t < t1) scores[gi][t - t0] = d * a.scale;
+                    if (j == 0) scores[gi][t - t0] = d * a.scale;
                 }
             }
         }
     }
     __syncthreads();
 
+    // the value loop's first batch of cached V rows, in flight during the softmax
+    constexpr uint32_t LV = D / 8;
+    const uint32_t tg = tid / LV, dl = tid % LV;
+    uint4 vb[UV];
+    auto load_v = [&](uint32_t tb) {
+#pragma unroll
+        for (int u = 0; u < UV; ++u) {
+            const uint32_t tt = min(tb + 8 * u, t1 - 1);
+            vb[u] = *reinterpret_cast<const uint4*>(a.vcache + ((size_t)kvh * ring + tt % ring) * D + 8 * dl);
+        }
+    };
+    load_v(t0 + tg);
+
+    // softmax over the chunk: wave maxima of every query head, one barrier, then the exponentials
+    // and wave sums, one barrier; waves combined in index order
+    __shared__ float smx[G][W], ssum[G][W];
     float m[G], l[G];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
         float mx = -INFINITY;
         for (uint32_t i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, scores[gi][i]);
-        m[gi] = block_max_f(mx, fred);
+        mx = wave_max(mx);
+        if (lane == 0) smx[gi][wave] = mx;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        float mx = smx[gi][0];
+        for (int w = 1; w < W; ++w) mx = fmaxf(mx, smx[gi][w]);
+        m[gi] = mx;
         float sum = 0.0f;
         for (uint32_t i = tid; i < n; i += blockDim.x) {
-            const float p = expf(scores[gi][i] - m[gi]);
+            const float p = expf(scores[gi][i] - mx);
             scores[gi][i] = p;
             sum += p;
         }
-        l[gi] = block_sum_f(sum, fred);
+        sum = wave_sum(sum);
+        if (lane == 0) ssum[gi][wave] = sum;
     }
     __syncthreads();
+#pragma unroll
+    for (int gi = 0; gi < G; ++gi) {
+        float t = 0.0f;
+        for (int w = 0; w < W; ++w) t += ssum[gi][w];
+        l[gi] = t;
+    }
 
-    // ---- values: D / 8 lanes per token row (8 channels each), 8 token groups, 2 rows in flight
+    // ---- values: D / 8 lanes per token row (8 channels each), 8 token groups, UV rows per group in flight
     {
-        constexpr uint32_t LV = D / 8;
-        const uint32_t tg = tid / LV, dl = tid % LV;
         float acc[G][8];
 #pragma unroll
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[gi][e] = 0.0f;
-        for (uint32_t tb = t0 + tg; tb < t1; tb += 16) {
-            uint4 vv[2];
+        for (uint32_t tb = t0 + tg; tb < t1; tb += 8 * UV) {
+            if (tb != t0 + tg) load_v(tb);
 #pragma unroll
-            for (int u = 0; u < 2; ++u) {
-                const uint32_t t = tb + 8 * u;
-                const uint32_t tt = t < t1 ? t : tb;
-                const uint16_t* vp = has_new && tt == pos ? vnew : a.vcache + ((size_t)kvh * ring + tt % ring) * D;
-                vv[u] = *reinterpret_cast<const uint4*>(vp + 8 * dl);
-            }
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
+            for (int u = 0; u < UV; ++u) {
                 const uint32_t t = tb + 8 * u;
                 if (t >= t1) break;
-                const uint32_t vw[4] = {vv[u].x, vv[u].y, vv[u].z, vv[u].w};
+                const uint4 v = has_new && t == pos ? *reinterpret_cast<const uint4*>(vnew + 8 * dl) : vb[u];
+                const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
                 float vf[8];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -716,32 +767,38 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     }
 
     // ---- split-K merge: the last block of this (KV head, query group) combines the chunk partials
-    const size_t stride = (size_t)G * (D + 2);
+    // (a query head's partial row: D sums, max, sum, padding to whole 16-byte pieces)
+    constexpr uint32_t R = attn_part_row(D);
+    const size_t stride = (size_t)G * R;
     const uint32_t slot = blockIdx.z * gridDim.y + blockIdx.y;  // (token, KV head, query group)
-    float* mine = a.part + ((size_t)slot * a.cmax + c) * stride;
+    // The blocks of a KV head may run on different XCDs, whose L2s are not coherent with each
+    // other: the partials are stored through to the memory side (sc1) and waited for, the ticket is
+    // an agent-scope atomic, and the last block reads the partials from the memory side, so no
+    // L2 write-back or invalidation (a device-scope fence) is needed.
+    const __amdgpu_buffer_rsrc_t prs =
+        __builtin_amdgcn_make_buffer_rsrc(a.part + (size_t)slot * a.cmax * stride, 0, 0x7FFFFFFF, 0x00020000);
+    const uint32_t mine = c * (uint32_t)stride * 4;  // this chunk's byte offset
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-        mine[gi * (D + 2) + tid] = o[gi];
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[gi]), prs, mine + (gi * R + tid) * 4, 0, kPartSC1);
         if (tid == 0) {
-            mine[gi * (D + 2) + D] = m[gi];
-            mine[gi * (D + 2) + D + 1] = l[gi];
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m[gi]), prs, mine + (gi * R + D) * 4, 0, kPartSC1);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l[gi]), prs, mine + (gi * R + D + 1) * 4, 0, kPartSC1);
         }
     }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     if (tid == 0) {
-        __threadfence();
-        const uint32_t ticket = atomicAdd(a.counters + slot, 1u);
+        const uint32_t ticket = __hip_atomic_fetch_add(a.counters + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         last = ticket == chunks - 1;
     }
     __syncthreads();
     if (!last) return;
-    __threadfence();
-    const float* all = a.part + (size_t)slot * a.cmax * stride;
     // chunk maxima and sums into LDS (one load per thread), then the weights exp(m_c - M)
     for (uint32_t i = tid; i < chunks * G; i += blockDim.x) {
-        const uint32_t k = i / G, gi = i % G;
-        cw[gi][k] = all[k * stride + gi * (D + 2) + D];
-        vred[0][gi][k] = all[k * stride + gi * (D + 2) + D + 1];
+        const uint32_t k = i / G, gi = i % G, off = (k * (uint32_t)stride + gi * R + D) * 4;
+        cw[gi][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, off, 0, kPartSC1));
+        vred[0][gi][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, off + 4, 0, kPartSC1));
     }
     __syncthreads();
     float M[G], L[G];
@@ -760,12 +817,54 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     for (int gi = 0; gi < G; ++gi) {
         L[gi] = 0.0f;
         for (uint32_t k = 0; k < chunks; ++k) L[gi] = fmaf(cw[gi][k], vred[0][gi][k], L[gi]);
-        float acc = 0.0f;
-#pragma unroll 8
-        for (uint32_t k = 0; k < chunks; ++k) acc = fmaf(cw[gi][k], all[k * stride + gi * (D + 2) + tid], acc);
-        out[(size_t)(qh0 + gi) * D + tid] = acc / L[gi];
     }
-    if (tid == 0) a.counters[slot] = 0u;
+    // weighted sums: thread tid takes 16-byte piece f of the G query heads' sums in every P-th chunk
+    // (chunks ph, ph + P, ..., MU of them in flight), then the P phases are added in order
+    constexpr uint32_t NF = G * D / 4, P = D / NF, MU = 16;
+    const uint32_t f = tid % NF, ph = tid / NF, fg = f / (D / 4), f4 = f % (D / 4);
+    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t k0 = ph; k0 < chunks; k0 += MU * P) {
+        float4 pv[MU];
+#pragma unroll
+        for (uint32_t u = 0; u < MU; ++u) {
+            const uint32_t k = min(k0 + u * P, chunks - 1);
+            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(prs, (k * (uint32_t)stride + fg * R + 4 * f4) * 4, 0, kPartSC1);
+            pv[u] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < MU; ++u) {
+            const uint32_t k = k0 + u * P;
+            if (k < chunks) {
+                const float w = cw[fg][k];
+                acc4.x = fmaf(w, pv[u].x, acc4.x);
+                acc4.y = fmaf(w, pv[u].y, acc4.y);
+                acc4.z = fmaf(w, pv[u].z, acc4.z);
+                acc4.w = fmaf(w, pv[u].w, acc4.w);
+            }
+        }
+    }
+    float4* red4 = reinterpret_cast<float4*>(&vred[0][0][0]);  // [P][NF], after L is read
+    __syncthreads();
+    red4[ph * NF + f] = acc4;
+    __syncthreads();
+    if (tid < NF) {
+        float4 t = red4[f];
+        for (uint32_t q = 1; q < P; ++q) {
+            const float4 r = red4[q * NF + f];
+            t.x += r.x;
+            t.y += r.y;
+            t.z += r.z;
+            t.w += r.w;
+        }
+        const float il = L[fg];
+        float4 y;
+        y.x = t.x / il;
+        y.y = t.y / il;
+        y.z = t.z / il;
+        y.w = t.w / il;
+        *reinterpret_cast<float4*>(out + (size_t)(qh0 + fg) * D + 4 * f4) = y;
+    }
+    if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Query heads per attention block: all of a KV head's at width 256 (1, 2 or 4), two at width 512

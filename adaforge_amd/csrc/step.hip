@@ -188,8 +188,9 @@ __device__ __forceinline__ void tagged_boundary(Grid& g) {
 // Last workgroup out resets the barrier words for the next launch; with `advance` it also moves
 // the session position (a step without the head), unless a workgroup failed: then the position
 // stays at the failed step, which the host runs again on the per-operation kernels.  A failing
-// workgroup's state stores are ordered before its exit arrival (release), and the last arrival
-// (acquire) reads them.
+// workgroup's state stores (agent scope: through to the memory side) complete before its exit
+// arrival, and the last arrival reads them with an agent-scope load after its own arrival, so no
+// L2 write-back or invalidation (an acquire-release at device scope) is needed.
 __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance, bool failed) {
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -198,7 +199,8 @@ __device__ __forceinline__ void grid_exit(Grid& g, uint32_t* state, bool advance
             __hip_atomic_store(state + ST_BAD, 2u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(state + ST_STOP, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        const uint32_t old = __hip_atomic_fetch_add(g.bar + kBarExit, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        wait_vm();
+        const uint32_t old = __hip_atomic_fetch_add(g.bar + kBarExit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == gridDim.x - 1) {
             for (uint32_t i = 0; i < 10; ++i)
                 __hip_atomic_store(g.bar + 32 * i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
