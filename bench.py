@@ -22,11 +22,13 @@ kernel reads slower here than in the rocprofv3 kernel trace under profiles/).
 CPU baseline: the C oracle (a port of the reference's FP64 CPU path), on this host: config 4 on
 all of the box's CPU share (16 threads at most) and on one core, configs 0-3 in both modes.
 
-Beside the headline (`prefill` and `speculative` in the JSON line): a 512-id prompt prefilled on
-the config-4 model through the batched layers (32 positions per weight pass) and one step-kernel
-launch per position; and greedy speculative decoding with prompt-lookup drafts on a copying
+Beside the headline (`prefill`, `speculative` and `gemma4` in the JSON line): a 512-id prompt
+prefilled on the config-4 model through the batched layers (32 positions per weight pass) and one
+step-kernel launch per position; greedy speculative decoding with prompt-lookup drafts on a copying
 workload (config-4 shapes, local layers only, a prompt that repeats the model's own continuation),
-against plain decoding of the same prompt.
+against plain decoding of the same prompt; and a full-size Gemma-4-shaped model (the reference's own
+model family: 512-wide global layers with one KV head and K as V), prefilled and decoded on the
+per-operation kernels.
 
     python bench.py [--gpus 1] [--steps 240] [--warmup 16] [--no-cpu] [--no-configs] [--no-extras]
 """
@@ -385,6 +387,42 @@ def speculative_leg(lead_tokens=160, new_tokens=128):
     return out
 
 
+def gemma4_leg(new_tokens=256):
+    """The reference's own model family at full size: a 48-layer Gemma-4-shaped model with seeded
+    random weights (local layers as config 4; every sixth layer global with 16 query heads on one KV
+    head of width 512, K reused as V, proportional RoPE; attention scale 1, V-norm, softcap 30).  Its
+    512-wide global layers are outside the persistent step kernel's limits, so it decodes on the
+    per-operation kernels (one hipGraph per token).  Batched prefill of 128 ids, then greedy decode
+    in 128-token turns; decode tok/s over the turns."""
+    from adaforge_amd import synth
+    model = synth.gemma4_model(name="gemma4-bench", layers=48, hidden=HIDDEN, intermediate=INTER,
+                               local_q=(16, 8, 256), global_q=(16, 1, 512), vocabulary=VOCAB, window=1024)
+    stop = [model.vocabulary - 1]
+    prompt = [int(i) for i in synth.prompt_ids(PROMPT, model.vocabulary, name="gemma4-bench.prompt")]
+    with open_env(model, PROMPT + new_tokens + 32) as s:
+        r = s.generate(prompt, stop, 16)
+        prefill_ms = r.stats.prefill_ms
+        cached = prompt + r.ids
+        produced, t0 = 0, time.perf_counter()
+        while produced < new_tokens:
+            r = s.generate(cached, stop, min(128, new_tokens - produced))
+            cached += r.ids
+            produced += len(r.ids)
+            if r.stopped:
+                break
+        dt = time.perf_counter() - t0
+    out = {"workload": "48-layer Gemma-4-shaped model (local layers 16 q / 8 kv x 256, window 1024; every "
+                       "sixth layer global: 16 q / 1 kv x 512, K as V, proportional RoPE; scale 1, V-norm, "
+                       "softcap 30), Q4_0 projections, tied Q6_K table (vocab 262144); per-operation "
+                       "kernels in one hipGraph per token",
+           "prompt_tokens": PROMPT, "prefill_ms": round(prefill_ms, 2),
+           "prefill_tok_s": round((PROMPT - 1) / prefill_ms * 1000.0, 1),
+           "decode_tokens": produced, "decode_tok_s": round(produced / dt, 1)}
+    log(f"gemma4-shaped model: prefill {PROMPT} in {prefill_ms:.1f} ms, decode {produced} tokens -> "
+        f"{out['decode_tok_s']} tok/s")
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -474,10 +512,11 @@ def main():
     if not a.no_configs:
         configs = gpu_configs()
 
-    prefill = spec = None
+    prefill = spec = gemma4 = None
     if not a.no_extras:
         prefill = prefill_leg(model, stop)
         spec = speculative_leg()
+        gemma4 = gemma4_leg()
 
     cpu = None
     if not a.no_cpu:
@@ -540,6 +579,7 @@ def main():
         "configs": configs,
         "prefill": prefill,
         "speculative": spec,
+        "gemma4": gemma4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
