@@ -664,7 +664,7 @@ int af_rmsnorm_run(const float* weights, uint32_t width, float eps, const float*
 
 struct af_ffn {
     Q4Dev gate, up, down;
-    DevMem pre, post, act, mid;
+    DevMem pre, post, act, act_img, mid;  // act_img: the down GEMV's input as its digit image
     float pre_eps = 0, post_eps = 0, scale = 1;
     bool has_post = false;
     uint32_t hidden = 0, intermediate = 0;
@@ -697,6 +697,9 @@ int af_ffn_create(const af_ffn_weights* w, af_ffn** out) {
     if ((rc = dev_upload(f->pre, w->pre.weights, (size_t)hidden * 4, "FFN norm"))) return rc;
     if (has_post && (rc = dev_upload(f->post, w->post.weights, (size_t)hidden * 4, "FFN norm"))) return rc;
     if ((rc = dev_alloc(f->act, (size_t)inter * 4, "FFN activations"))) return rc;
+    const size_t img = (size_t)(inter + 127) / 128 * 640;  // blocks past the activations stay zero
+    if ((rc = dev_alloc(f->act_img, img, "FFN activation digits"))) return rc;
+    HIP_OK(hipMemset(f->act_img.p, 0, img), "FFN activation digits clear");
     if ((rc = dev_alloc(f->mid, (size_t)hidden * 4, "FFN down output"))) return rc;
     f->pre_eps = w->pre.epsilon;
     f->post_eps = w->post.epsilon;
@@ -720,18 +723,19 @@ int af_ffn_run(af_ffn* f, const float* x, float* y, void* stream) {
     g.in.w_n = f->pre.as<float>();
     g.in.eps_n = f->pre_eps;
     g.y = f->act.as<float>();
+    g.dig_out = f->act_img.as<int8_t>();  // the down GEMV's input, as its digit image
     HIP_OK(launch_q4_gemv(g, IN_NORM, OUT_GELU, f->intermediate, s), "FFN gate/up launch");
     Q4Args d{};
     d.w = f->down.view();
-    d.in.x = f->act.as<float>();
+    d.in.dig = f->act_img.as<int8_t>();
     if (!f->has_post && f->scale == 1.0f) {  // down + residual in the GEMV epilogue
         d.y = y;
         d.add = x;
-        HIP_OK(launch_q4_gemv(d, IN_PLAIN, OUT_ADD, f->hidden, s), "FFN down launch");
+        HIP_OK(launch_q4_gemv(d, IN_DIGITS, OUT_ADD, f->hidden, s), "FFN down launch");
         return AF_OK;
     }
     d.y = f->mid.as<float>();
-    HIP_OK(launch_q4_gemv(d, IN_PLAIN, OUT_PLAIN, f->hidden, s), "FFN down launch");
+    HIP_OK(launch_q4_gemv(d, IN_DIGITS, OUT_PLAIN, f->hidden, s), "FFN down launch");
     InputStage r{};
     r.x = f->mid.as<float>();
     r.res = x;
@@ -897,7 +901,8 @@ struct af_session {
     float final_eps = 0, emb_scale = 1, cap = 0;
     uint32_t hidden = 0, intermediate = 0, vocabulary = 0, capacity = 0;
     uint32_t max_qkv = 0, max_q = 0, cmax = 0, head_blocks = 0;
-    DevMem X, H, QKV, ATT, PROJ, ACT, D, QKVT, PROJT, DT, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS, RESULT, SNAP, KVSNAP;
+    DevMem X, H, QKV, ATT, PROJ, ACT, ACTIMG, D, QKVT, PROJT, DT, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS,
+        RESULT, SNAP, KVSNAP;
     // persistent step kernel: layer table, digit images, barrier words
     DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
@@ -1049,6 +1054,7 @@ struct af_session {
         ga.in.eps_n = L.ffn_eps;
         ga.in.x_out = H.as<float>();
         ga.y = ACT.as<float>();
+        ga.dig_out = ACTIMG.as<int8_t>();  // the down GEMV's input, as its digit image
         ga.state = st;
         if ((e = timed(K_GATEUP, q4_bytes(L.gate) + q4_bytes(L.up) + 4.0 * (3.0 * hidden + intermediate),
                        [&] { return launch_q4_gemv(ga, IN_RESID, OUT_GELU, intermediate, stream); })) != hipSuccess)
@@ -1056,11 +1062,11 @@ struct af_session {
 
         Q4Args da{};
         da.w = L.down.view();
-        da.in.x = ACT.as<float>();
+        da.in.dig = ACTIMG.as<int8_t>();
         da.y = D.as<float>();
         da.state = st;
         return timed(K_DOWN, q4_bytes(L.down) + 4.0 * (intermediate + hidden),
-                     [&] { return launch_q4_gemv(da, IN_PLAIN, OUT_PLAIN, hidden, stream); });
+                     [&] { return launch_q4_gemv(da, IN_DIGITS, OUT_PLAIN, hidden, stream); });
     }
 
     HeadArgs head_args(bool step, bool with_logits) {
@@ -1644,6 +1650,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         {&s->ATT, (size_t)max_q * 4, true},
         {&s->PROJ, (size_t)hidden * 4, true},
         {&s->ACT, (size_t)inter * 4, true},
+        {&s->ACTIMG, (size_t)(inter + 127) / 128 * 640, true},  // the down GEMV's input digit image
         {&s->D, (size_t)hidden * 4, true},
         {&s->QKVT, (size_t)s->max_qkv * 8, true},  // (value, tag) pairs: tag 0 is never current
         {&s->PROJT, (size_t)hidden * 8, true},

@@ -18,7 +18,10 @@ constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), expcnt and lgkmcnt unc
 // ---- Q4_0 GEMV: persistent, one workgroup per CU ----------------------------------------------
 //
 // The output rows come in units of one 16-row tile (T = 2: the same tile of the gate and the up
-// matrix).  Workgroup b takes units b, b + G, ... (G = grid size); the super-tiles of its units,
+// matrix), taken in groups of UG consecutive units: workgroup b takes groups b, b + G, ... (G = grid
+// size).  UG = 2 (UGS = 1) when the GELU epilogue also writes the digit image of its output (a.dig_out, the
+// next GEMV's IN_DIGITS input), so that every 32-element block of it belongs to one workgroup.  The
+// super-tiles of a workgroup's units,
 // flattened in (unit, matrix, super-tile) order, are dealt round-robin to its 8 waves, so every
 // wave streams one sequence of records across tile boundaries.  Each wave keeps kGemvRing records
 // in flight in registers: it folds a record, then requests the one kGemvRing places further on,
@@ -47,8 +50,9 @@ __device__ __forceinline__ void gemv_advance(GemvCursor& c, uint32_t nst, uint32
     }
 }
 
-template <int T, int IN, int OUT, int Q>
+template <int T, int IN, int OUT, int Q, int UGS>
 __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_rows, uint32_t units) {
+    constexpr uint32_t ugs = UGS;
     extern __shared__ __align__(16) uint8_t smem[];
     __shared__ double red[8];
     __shared__ float part[kGemvWaves][kGemvMaxUnits * T][16];
@@ -57,7 +61,9 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t G = gridDim.x, b = blockIdx.x;
     const uint32_t B = a.w.blocks, K = B * 32, nst = a.w.nst;
-    const uint32_t nu = (units - b + G - 1) / G;  // the grid never exceeds the units
+    // groups of UG = 2^UGS units: the grid never exceeds the groups, and UG divides the units
+    const uint32_t nu = ((units >> ugs) - b + G - 1) / G << ugs;
+    auto unit_of = [&](uint32_t j) { return ((b + (j >> ugs) * G) << ugs) + (j & ((1u << ugs) - 1)); };
     const uint32_t N = nu * T * nst;               // records of this workgroup
     const uint32_t n_w = N > wave ? (N - wave + kGemvWaves - 1) / kGemvWaves : 0;
 
@@ -78,7 +84,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
         const bool second = T == 2 && c.k == 1;
         const uint8_t* codes = second ? a.w2.codes : a.w.codes;
         const uint16_t* scales = second ? a.w2.scales : a.w.scales;
-        const size_t rec = (size_t)(b + c.j * G) * nst + c.st;
+        const size_t rec = (size_t)unit_of(c.j) * nst + c.st;
         const __amdgpu_buffer_rsrc_t rcode =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(codes) + rec * 1024, 0, ok ? 1024 : 0, 0x00020000);
         const __amdgpu_buffer_rsrc_t rscale =
@@ -138,8 +144,38 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
     if (n_w > 0) flush();
     __syncthreads();
 
+    if constexpr (OUT == OUT_GELU) {
+        if constexpr (UGS == 1) {  // the rows' GELU products, one per thread, then a digit block per 32-row group
+            __shared__ float act_l[kGemvMaxUnits * 16];
+            for (uint32_t i = tid; i < nu * 16; i += blockDim.x) {
+                const uint32_t j = i >> 4, r = i & 15;
+                float gs = part[0][j * T][r], us = part[0][j * T + 1][r];
+                for (uint32_t w = 1; w < kGemvWaves; ++w) {
+                    gs += part[w][j * T][r];
+                    us += part[w][j * T + 1][r];
+                }
+                const float v = gelu_mul(gs, us);
+                act_l[i] = v;
+                a.y[unit_of(j) * 16 + r] = v;
+            }
+            __syncthreads();
+            int8_t* img = a.dig_out;
+            DigitTab* otab = reinterpret_cast<DigitTab*>(img + (size_t)(out_rows / 128 + (out_rows % 128 != 0)) * 512);
+            for (uint32_t i = tid; i < nu / 2 * 4; i += blockDim.x) {  // quads: 8 rows each of a group's 32
+                const uint32_t jg = i >> 2, p = i & 3, blk = b + jg * G;
+                float v[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = act_l[jg * 32 + 8 * p + e];
+                float m, sum;
+                quad_stats(v, m, sum);
+                digits8(v, m, img, blk, p);
+                if (p == 0) digit_tab(otab, blk, m, sum);
+            }
+            return;
+        }
+    }
     for (uint32_t i = tid; i < nu * 16; i += blockDim.x) {
-        const uint32_t j = i >> 4, r = i & 15, row = (b + j * G) * 16 + r;
+        const uint32_t j = i >> 4, r = i & 15, row = unit_of(j) * 16 + r;
         if (row >= out_rows) continue;
         float v[T];
 #pragma unroll
@@ -156,13 +192,13 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
 
 constexpr uint32_t kQ4Threads = 512;
 
-// One workgroup per CU, more when the units would exceed kGemvMaxUnits per workgroup.
-static uint32_t gemv_grid(uint32_t units) {
+// One workgroup per CU, more when the groups would exceed kGemvMaxUnits units per workgroup.
+static uint32_t gemv_grid(uint32_t groups, uint32_t ug) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         cus = 256;
-    const uint32_t need = (units + kGemvMaxUnits - 1) / kGemvMaxUnits;
-    return min(units, max((uint32_t)cus, need));
+    const uint32_t per = kGemvMaxUnits / ug, need = (groups + per - 1) / per;
+    return min(groups, max((uint32_t)cus, need));
 }
 
 template <int T, int IN, int OUT, int Q>
@@ -171,8 +207,16 @@ static hipError_t q4_launch3(Q4Args a, uint32_t out_rows, hipStream_t st) {
     if (units == 0) return hipSuccess;
     a.slices = kGemvWaves;
     const size_t lds = (IN == IN_EMBED ? (size_t)a.w.blocks * 32 * 4 : 0) + (size_t)a.w.nst * (512 + 128);
-    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT, Q>), dim3(gemv_grid(units)), dim3(kQ4Threads), lds, st, a, out_rows,
-                       units);
+    if constexpr (OUT == OUT_GELU) {
+        if (a.dig_out) {  // a digit image of the output needs whole 32-row blocks per workgroup
+            if (out_rows % 32) return hipErrorInvalidValue;
+            hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT, Q, 1>), dim3(gemv_grid(units / 2, 2)), dim3(kQ4Threads), lds,
+                               st, a, out_rows, units);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((q4_gemv_kernel<T, IN, OUT, Q, 0>), dim3(gemv_grid(units, 1)), dim3(kQ4Threads), lds, st, a,
+                       out_rows, units);
     return hipGetLastError();
 }
 
