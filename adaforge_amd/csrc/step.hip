@@ -1085,20 +1085,26 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     if (!__builtin_amdgcn_readfirstlane(*flag)) return;
 
     // merge (last chunk of this head): M = max_c m_c, w_c = exp(m_c - M), output
-    // sum_c w_c o_c / sum_c w_c l_c, in chunk order
+    // sum_c w_c o_c / sum_c w_c l_c, in chunk order; the weights once per (query head, chunk)
     float* mrg = reinterpret_cast<float*>(lds);  // [chunks][stride]
     float* outv = mrg + chunks * stride;        // [GQ][D]
+    float* wts = outv + GQ * D;                 // [GQ][chunks]
     dma_all<kPol>(head_part, chunks * stride * 4, lds, wave, lane);
     wait_vm();
     __syncthreads();
+    if (wave < (uint32_t)GQ) {
+        float M = -INFINITY;
+        for (uint32_t k = lane; k < chunks; k += 64) M = fmaxf(M, mrg[k * stride + wave * (D + 2) + D]);
+        M = wave_max(M);
+        for (uint32_t k = lane; k < chunks; k += 64) wts[wave * chunks + k] = expf(mrg[k * stride + wave * (D + 2) + D] - M);
+    }
+    __syncthreads();
     for (uint32_t i = tid; i < GQ * D; i += kThreads) {
         const uint32_t q = i / D, d = i % D;
-        float M = -INFINITY;
-        for (uint32_t k = 0; k < chunks; ++k) M = fmaxf(M, mrg[k * stride + q * (D + 2) + D]);
         float Lq = 0.0f, acc = 0.0f;
         for (uint32_t k = 0; k < chunks; ++k) {
             const float* pk = mrg + k * stride + q * (D + 2);
-            const float w = expf(pk[D] - M);
+            const float w = wts[q * chunks + k];
             Lq = fmaf(w, pk[D + 1], Lq);
             acc = fmaf(w, pk[d], acc);
         }
@@ -1535,7 +1541,8 @@ hipError_t step_xcd_map(uint32_t grid, uint32_t* xcc, hipStream_t s) {
 }
 
 uint32_t step_merge_chunks(uint32_t group, size_t lds) {
-    const size_t out = (size_t)group * 256 * 4, per = (size_t)step_part_stride(group) * 4;
+    // per chunk: its partials and one weight per query head
+    const size_t out = (size_t)group * 256 * 4, per = ((size_t)step_part_stride(group) + group) * 4;
     return lds > out ? (uint32_t)((lds - out) / per) : 0u;
 }
 
