@@ -22,9 +22,10 @@ kernel reads slower here than in the rocprofv3 kernel trace under profiles/).
 CPU baseline: the C oracle (a port of the reference's FP64 CPU path), on this host: config 4 on
 all of the box's CPU share (16 threads at most) and on one core, configs 0-3 in both modes.
 
-Beside the headline (`prefill`, `speculative` and `gemma4` in the JSON line): a 512-id prompt
-prefilled on the config-4 model through the batched layers (32 positions per weight pass) and one
-step-kernel launch per position; greedy speculative decoding with prompt-lookup drafts on a copying
+Beside the headline (`prefill`, `long_context`, `speculative` and `gemma4` in the JSON line): a
+512-id prompt prefilled on the config-4 model through the batched layers (32 positions per weight
+pass) and one step-kernel launch per position; config-4 decode after a 7620-id prompt; greedy
+speculative decoding with prompt-lookup drafts on a copying
 workload (config-4 shapes, local layers only, a prompt that repeats the model's own continuation),
 against plain decoding of the same prompt; and a full-size Gemma-4-shaped model (the reference's own
 model family: 512-wide global layers with one KV head and K as V), prefilled and decoded on the
@@ -387,6 +388,27 @@ def speculative_leg(lead_tokens=160, new_tokens=128):
     return out
 
 
+def long_context_leg(model, stop, tokens=7620, new_tokens=64):
+    """Decode on the config-4 model at a long context: a `tokens`-id prompt prefilled through the
+    batched layers, then greedy decode (the global layers attend over every position, the local
+    ones over their 1024-token window); prefill tok/s and decode tok/s."""
+    from adaforge_amd import synth
+    prompt = [int(i) for i in synth.prompt_ids(tokens, model.vocabulary, name="config4.long")]
+    with open_env(model, tokens + new_tokens + 32) as s:
+        r = s.generate(prompt, stop, 8)
+        prefill_ms = r.stats.prefill_ms
+        cached = prompt + r.ids
+        t0 = time.perf_counter()
+        r = s.generate(cached, stop, new_tokens)
+        dt = time.perf_counter() - t0
+    out = {"prompt_tokens": tokens, "prefill_ms": round(prefill_ms, 1),
+           "prefill_tok_s": round((tokens - 1) / prefill_ms * 1000.0, 1),
+           "context": len(cached), "decode_tokens": len(r.ids), "decode_tok_s": round(len(r.ids) / dt, 1)}
+    log(f"long context: prefill {tokens} ids in {prefill_ms:.0f} ms, decode {len(r.ids)} tokens at context "
+        f"{len(cached)} -> {out['decode_tok_s']} tok/s")
+    return out
+
+
 def gemma4_leg(new_tokens=256):
     """The reference's own model family at full size: a 48-layer Gemma-4-shaped model with seeded
     random weights (local layers as config 4; every sixth layer global with 16 query heads on one KV
@@ -512,9 +534,10 @@ def main():
     if not a.no_configs:
         configs = gpu_configs()
 
-    prefill = spec = gemma4 = None
+    prefill = spec = gemma4 = longctx = None
     if not a.no_extras:
         prefill = prefill_leg(model, stop)
+        longctx = long_context_leg(model, stop)
         spec = speculative_leg()
         gemma4 = gemma4_leg()
 
@@ -578,6 +601,7 @@ def main():
         },
         "configs": configs,
         "prefill": prefill,
+        "long_context": longctx,
         "speculative": spec,
         "gemma4": gemma4,
         "cpu_baseline": cpu,
