@@ -6,29 +6,25 @@
 // attention of all tokens (attention_kernel with one grid z-slice per token, after a pass that
 // appends every token's K and V).
 //
-// Each token's input is written in the decode step's digit form (digit_words): block b is
-// s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) with s = 2^(ilogb(max |x_b|) - 5), int8 digits, error at most
-// 2^-27 max |x_b|.  The GEMM runs on the int8 matrix cores with the tokens in the MFMA's M
-// dimension: v_mfma_i32_16x16x32_i8 with A = one digit plane of 16 tokens over one 32-weight block
-// (k) and B = the block's raw nibble codes n of 16 weight rows, so D_i[t][r] = sum_j n_rj q_ij(t).
-// Per (token, row, block), I = 2^14 D0 + 2^7 D1 + D2 is exact in int32 and
-//   sum_j (n_rj - 8) x_j = s 2^-14 I + s 2^-21 D3 - 8 sum_j x_j,
-// which each lane folds into its fp32 partial with the block's weight scale d_r.
+// Each token's GEMM input is written as two fp16 halves per 32-element block: with u the block
+// scaled by 2^(14 - e) (e = ilogb of the block's max |x|, so that |u| < 2^15), hi = fp16(u) and
+// lo = fp16(u - hi), both rounded to nearest even; hi + lo holds u to about 2^-23 of the block's max.  The GEMM runs on the
+// fp16 matrix cores with the tokens in the MFMA's M dimension: v_mfma_f32_16x16x32_f16 with A = the
+// hi (then the lo) halves of 16 tokens over one 32-weight block (k) and B = the block's weights
+// n - 8 of 16 rows as fp16 (exact: each nibble placed in the mantissa of 1024 + n, then 1032
+// subtracted), both MFMAs accumulating into one fp32 tile, so D[t][r] = sum_j u_j(t) (n_rj - 8) with
+// every product exact.  Each lane adds d_r 2^(e - 14) D[t][r] to its fp32 partial per block.
 #include "device.h"
 
 namespace af {
+
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 
 namespace {
 
 constexpr uint32_t kGemmThreads = 256;  // four waves splitting the blocks of the workgroup's K range
 constexpr uint32_t kGemmTargetGrid = 512;
-
-// Table entry of a block with max |x| m and element sum `sum` (digit_words' scale s = 2^(ilogb(m) - 5)):
-// {s 2^-14, -8 sum}.
-__device__ __forceinline__ float2 block_tab(float m, float sum) {
-    const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
-    return make_float2(ldexpf(s, -14), -8.0f * sum);
-}
 
 uint32_t padded_tokens(uint32_t T) { return (T + 15) / 16 * 16; }
 
@@ -52,11 +48,37 @@ GemmPlan gemm_plan(uint32_t rows, uint32_t blocks, bool pair) {
 
 }  // namespace
 
-// ---- digit images of a batch --------------------------------------------------------------------
+// ---- input images of a batch --------------------------------------------------------------------
+//
+// Image of K = 32 nb inputs for Tp tokens: hi [nb][Tp][32] fp16, then lo [nb][Tp][32] fp16, then
+// [nb][Tp] floats 2^(e - 14) (0 for an all-zero block and for padding tokens).  A quad of threads
+// (8 elements each) writes one block.
+
+// The halves and the scale of block b of token t from the 8 elements v of part p (all four lanes of
+// the quad take part).
+__device__ __forceinline__ void block_halves(const float (&v)[8], uint32_t b, uint32_t p, uint32_t t, uint32_t Tp,
+                                             _Float16* hi, _Float16* lo, float* inv) {
+    float m, sum;
+    quad_stats(v, m, sum);
+    const int e = m > 0.0f ? ilogbf(m) : 0;
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float u0 = ldexpf(v[2 * k], 14 - e), u1 = ldexpf(v[2 * k + 1], 14 - e);
+        const _Float16 h0 = (_Float16)u0, h1 = (_Float16)u1;
+        const _Float16 l0 = (_Float16)(u0 - (float)h0), l1 = (_Float16)(u1 - (float)h1);
+        hw[k] = (uint32_t)__builtin_bit_cast(uint16_t, h0) | (uint32_t)__builtin_bit_cast(uint16_t, h1) << 16;
+        lw[k] = (uint32_t)__builtin_bit_cast(uint16_t, l0) | (uint32_t)__builtin_bit_cast(uint16_t, l1) << 16;
+    }
+    const size_t at = ((size_t)b * Tp + t) * 32 + 8 * p;
+    *reinterpret_cast<v4u*>(hi + at) = v4u{hw[0], hw[1], hw[2], hw[3]};
+    *reinterpret_cast<v4u*>(lo + at) = v4u{lw[0], lw[1], lw[2], lw[3]};
+    if (p == 0) inv[(size_t)b * Tp + t] = m > 0.0f ? ldexpf(1.0f, e - 14) : 0.0f;
+}
 
 // One workgroup per token t < Tp (tokens T..Tp-1 write zeros).  The input vector of the GEMV that
 // follows:
-//   BI_PLAIN: x_t;
+//   BI_PLAIN: x_t (f32(rms(x_t) w_n) with w_n);
 //   BI_RESID: v_t = (f32(rms(x_t) w_a) + res_t) * scale (w_a null: (x_t + res_t) * scale), stored to
 //             x_out_t (the residual stream), then f32(rms(v_t) w_n);
 //   BI_EMBED: v_t = table row ids[pos0 + t] * emb_scale, stored to x_out_t, then f32(rms(v_t) w_n).
@@ -65,15 +87,16 @@ __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
     extern __shared__ __align__(16) float xs[];  // [K]
     __shared__ double red[8];
     const uint32_t t = blockIdx.x, tid = threadIdx.x, K = in.K, nb = K / 32, Tp = gridDim.x;
-    int8_t* planes = in.img;
-    float2* tabs = reinterpret_cast<float2*>(in.img + (size_t)nb * 4 * Tp * 32);
+    _Float16* hi = reinterpret_cast<_Float16*>(in.img);
+    _Float16* lo = hi + (size_t)nb * Tp * 32;
+    float* inv = reinterpret_cast<float*>(lo + (size_t)nb * Tp * 32);
     if (t >= in.T) {
         for (uint32_t o = tid; o < nb * 4; o += blockDim.x) {
             const uint32_t b = o >> 2, p = o & 3;
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                *reinterpret_cast<v2u*>(planes + (((size_t)b * 4 + i) * Tp + t) * 32 + 8 * p) = v2u{0u, 0u};
-            if (p == 0) tabs[(size_t)b * Tp + t] = make_float2(0.0f, 0.0f);
+            const size_t at = ((size_t)b * Tp + t) * 32 + 8 * p;
+            *reinterpret_cast<v4u*>(hi + at) = v4u{0u, 0u, 0u, 0u};
+            *reinterpret_cast<v4u*>(lo + at) = v4u{0u, 0u, 0u, 0u};
+            if (p == 0) inv[(size_t)b * Tp + t] = 0.0f;
         }
         return;
     }
@@ -113,28 +136,20 @@ __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
     }
     // each quad of threads holds one 32-element block (8 consecutive elements per thread)
     for (uint32_t o = tid; o < nb * 4; o += blockDim.x) {
-        const uint32_t b = o >> 2, p = o & 3;
         float v[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[k] = in.w_n ? norm_apply(xs[8 * o + k], rn, in.w_n[8 * o + k]) : xs[8 * o + k];
-        float m, sum;
-        quad_stats(v, m, sum);
-        uint32_t w[4][2];
-        digit_words(v, m, w);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            *reinterpret_cast<v2u*>(planes + (((size_t)b * 4 + i) * Tp + t) * 32 + 8 * p) = v2u{w[i][0], w[i][1]};
-        if (p == 0) tabs[(size_t)b * Tp + t] = block_tab(m, sum);
+        block_halves(v, o >> 2, o & 3, t, Tp, hi, lo, inv);
     }
 }
 
-// BI_PLAIN inputs (no norm, no residual): one thread per 8-element octet, grid (Tp, octets / 256).
+// BI_PLAIN inputs without a norm: one thread per 8-element octet, grid (Tp, octets / 256).
 __global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
     const uint32_t t = blockIdx.x, o = blockIdx.y * 256 + threadIdx.x, nb = in.K / 32, Tp = gridDim.x;
     if (o >= nb * 4) return;  // whole quads: nb * 4 is a multiple of 4
-    const uint32_t b = o >> 2, p = o & 3;
-    int8_t* planes = in.img;
-    float2* tabs = reinterpret_cast<float2*>(in.img + (size_t)nb * 4 * Tp * 32);
+    _Float16* hi = reinterpret_cast<_Float16*>(in.img);
+    _Float16* lo = hi + (size_t)nb * Tp * 32;
+    float* inv = reinterpret_cast<float*>(lo + (size_t)nb * Tp * 32);
     float v[8];
     if (t < in.T) {
         const float4* x = reinterpret_cast<const float4*>(in.x + (size_t)t * in.stride) + 2 * o;
@@ -145,28 +160,21 @@ __global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) v[k] = 0.0f;
     }
-    float m, sum;
-    quad_stats(v, m, sum);
-    uint32_t w[4][2];
-    digit_words(v, m, w);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-        *reinterpret_cast<v2u*>(planes + (((size_t)b * 4 + i) * Tp + t) * 32 + 8 * p) = v2u{w[i][0], w[i][1]};
-    if (p == 0) tabs[(size_t)b * Tp + t] = block_tab(m, sum);
+    block_halves(v, o >> 2, o & 3, t, Tp, hi, lo, inv);
 }
 
 // ---- Q4_0 GEMM over a batch ---------------------------------------------------------------------
 
 namespace {
 
-// A block's input operands for a wave: the four digit planes of its G token groups (lane l: token
-// 16 g + l % 16, elements 8 (l / 16) .. + 7) and the table entries of the four tokens whose outputs
-// the lane folds (16 g + 4 (l / 16) + e).  They come from L2 (the image is shared by all workgroups)
-// and are loaded one block ahead.
+// A block's input operands for a wave: the hi and lo halves of its G token groups (lane l: token
+// 16 g + l % 16, elements 8 (l / 16) .. + 7) and the block scales of tokens 16 g + 4 (l / 16) + e
+// (the lane's outputs).  They come from L2 (the image is shared by all
+// workgroups) and are loaded one block ahead.
 template <int G>
 struct InOps {
-    v2u a[4][G];
-    v4f tab[G][2];
+    v4u hi[G], lo[G];
+    v4f sc[G];  // the block scales 2^(e - 14) of the four tokens whose outputs the lane folds
 };
 
 // A block's weights for R row tiles of P matrices (lane l: row l % 16, bytes 8 ((l / 16) & 1) .. + 7 of
@@ -186,18 +194,15 @@ template <int G>
 __device__ __forceinline__ void load_in(InOps<G>& o, const BatchGemm& a, uint32_t b, uint32_t lane) {
     constexpr uint32_t Tp = 16 * G;
     const uint32_t m = lane & 15, kq = lane >> 4;
-    const int8_t* planes = a.img;
-    const float2* tabs = reinterpret_cast<const float2*>(a.img + (size_t)a.w.blocks * 4 * Tp * 32);
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-            o.a[i][g] = *gp(reinterpret_cast<const v2u*>(planes + (((size_t)b * 4 + i) * Tp + 16 * g + m) * 32 + 8 * kq));
+    const _Float16* hi = reinterpret_cast<const _Float16*>(a.img);
+    const _Float16* lo = hi + (size_t)a.w.blocks * Tp * 32;
+    const float* inv = reinterpret_cast<const float*>(lo + (size_t)a.w.blocks * Tp * 32);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-        const v4f* tp = reinterpret_cast<const v4f*>(tabs + (size_t)b * Tp + 16 * g + 4 * kq);
-        o.tab[g][0] = *gp(tp);
-        o.tab[g][1] = *gp(tp + 1);
+        const size_t at = ((size_t)b * Tp + 16 * g + m) * 32 + 8 * kq;
+        o.hi[g] = *gp(reinterpret_cast<const v4u*>(hi + at));
+        o.lo[g] = *gp(reinterpret_cast<const v4u*>(lo + at));
+        o.sc[g] = *gp(reinterpret_cast<const v4f*>(inv + (size_t)b * Tp + 16 * g + 4 * kq));
     }
 }
 
@@ -218,36 +223,34 @@ __device__ __forceinline__ void load_w(WOps<P, R>& o, const BatchGemm& a, uint32
     }
 }
 
+// Four nibbles (one per byte of c) as fp16 (n - 8), in two pairs: n into the mantissa of 1024 + n
+// (0x6400 | n), then 1032 subtracted, exactly.
+__device__ __forceinline__ void nibbles_f16(uint32_t c, v2h& p0, v2h& p1) {
+    const v2h bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+    p0 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0u, c, 0x0c010c00u) | 0x64006400u) - bias;
+    p1 = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0u, c, 0x0c030c02u) | 0x64006400u) - bias;
+}
+
 template <int P, int G, int R>
 __device__ __forceinline__ void mfma_block(const InOps<G>& x, const WOps<P, R>& w, uint32_t kq,
                                            float (&acc)[R][P][G][4]) {
     const uint32_t sh = kq >= 2 ? 4u : 0u;  // k 0..15: low nibbles, 16..31: high nibbles
-    const v4i zero = {0, 0, 0, 0};
+    const v4f zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
         for (int q = 0; q < P; ++q) {
-            const uint32_t lo = (w.code[r][q].x >> sh) & 0x0F0F0F0Fu, hi = (w.code[r][q].y >> sh) & 0x0F0F0F0Fu;
-            const long B = (long)(((uint64_t)hi << 32) | lo);
+            v2h f0, f1, f2, f3;
+            nibbles_f16((w.code[r][q].x >> sh) & 0x0F0F0F0Fu, f0, f1);
+            nibbles_f16((w.code[r][q].y >> sh) & 0x0F0F0F0Fu, f2, f3);
+            const v8h B = {f0.x, f0.y, f1.x, f1.y, f2.x, f2.y, f3.x, f3.y};
             const float d = h2f(w.d[r][q]);
 #pragma unroll
             for (int g = 0; g < G; ++g) {
-                v4i D[4];
+                v4f D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, x.hi[g]), B, zero, 0, 0, 0);
+                D = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, x.lo[g]), B, D, 0, 0, 0);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const long A = (long)(((uint64_t)x.a[i][g].y << 32) | x.a[i][g].x);
-                    D[i] = __builtin_amdgcn_mfma_i32_16x16x32_i8(A, B, zero, 0, 0, 0);
-                }
-                const float tb[8] = {x.tab[g][0].x, x.tab[g][0].y, x.tab[g][0].z, x.tab[g][0].w,
-                                     x.tab[g][1].x, x.tab[g][1].y, x.tab[g][1].z, x.tab[g][1].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // exact: |I| < 2^30 (|D_i| <= 32 * 15 * 64)
-                    const int I = (int)(((uint32_t)D[0][e] << 14) + ((uint32_t)D[1][e] << 7) + (uint32_t)D[2][e]);
-                    float in = fmaf((float)D[3][e], tb[2 * e] * 0.0078125f, tb[2 * e + 1]);  // s 2^-21 D3 + bias
-                    in = fmaf((float)I, tb[2 * e], in);
-                    acc[r][q][g][e] = fmaf(d, in, acc[r][q][g][e]);
-                }
+                for (int e = 0; e < 4; ++e) acc[r][q][g][e] = fmaf(d * x.sc[g][e], D[e], acc[r][q][g][e]);
             }
         }
 }
@@ -358,7 +361,6 @@ __global__ __launch_bounds__(256) void batch_reduce_kernel(BatchGemm a, uint32_t
 
 namespace {
 
-typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 
 __device__ __forceinline__ void split_f16(float x, _Float16& hi, _Float16& lo) {
     hi = (_Float16)x;
@@ -570,7 +572,7 @@ hipError_t launch_batch_attention(BatchAttn a, uint32_t head_width, hipStream_t 
 
 
 size_t batch_image_bytes(uint32_t blocks, uint32_t tokens) {
-    return (size_t)blocks * padded_tokens(tokens) * (4 * 32 + 8);
+    return (size_t)blocks * padded_tokens(tokens) * (128 + 4);
 }
 
 size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair) {
