@@ -181,11 +181,10 @@ int set_error(int code, std::string msg);
 
 // ---- batched prefill (batch.hip) ---------------------------------------------------------------
 //
-// Digit image of T vectors of nb 32-element blocks for the batched GEMV, with the tokens padded to
-// Tp = 16 ceil(T / 16) (padding tokens all zero): block b of vector t in the digit form of the decode
-// GEMV, s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21), s = 2^(ilogb(max |x_b|) - 5):
-//   planes img[((b 4 + i) Tp + t) 32 + j]   digit i of element j
-//   tabs   float2 at img + nb 4 Tp 32, [b Tp + t] = {s 2^-14, -8 sum_j x_j}
+// Input image of T vectors of nb 32-element blocks for the batched GEMM, with the tokens padded to
+// Tp = 16 ceil(T / 16) (padding tokens all zero): block b of vector t scaled by 2^(14 - e) (e =
+// ilogb of the block's max |x|) as two fp16 halves, hi = f16(u) and lo = f16(u - hi):
+//   hi  fp16 [nb][Tp][32], then lo fp16 [nb][Tp][32], then the scales 2^(e - 14) as float [nb][Tp]
 constexpr uint32_t kBatchMax = 32;   // tokens per batch (crates/cuda-backend/src/batch.rs:10 MAX_BATCH)
 constexpr uint32_t kVerifyMax = 16;  // tokens per speculative verification pass (batch.rs:13 MAX_VERIFY)
 
@@ -209,6 +208,13 @@ struct BatchIn {
     const uint32_t* ids;
     uint32_t pos0;          // BI_EMBED: vector t is row ids[pos0 + t]
     float emb_scale;
+    // parts > 0: x comes from the split-K partial planes part[(k Tp + t) part_row + i] that
+    // batch_gemm_kernel left (its reduce deferred), summed in split order: BI_RESID, planes
+    // k < parts; BI_PLAIN without w_n, a gate/up pair: x = gelu(sum of gate planes 2 k) * (sum of up
+    // planes 2 k + 1)
+    const float* part;
+    uint32_t parts;
+    size_t part_row;
     int8_t* img;
 };
 
@@ -220,7 +226,11 @@ struct BatchGemm {
     size_t y_stride;
     const float* add;       // optional residual added to y (same layout)
     float* part;            // split-K partials (batch_gemm_part_bytes)
+    bool defer;             // no add: with a split-K plan of at most kDeferParts (a single matrix)
+                            // or kDeferPairParts (a gate/up pair) splits, leave the partials for
+                            // the input kernel of the next GEMM (no y)
 };
+constexpr uint32_t kDeferParts = 16, kDeferPairParts = 4;
 
 // Attention of a batch over the KV cache after the append pass (batch_attention_kernel): the
 // tokens' queries q[t][q_heads][D], token t at position pos0 + t seeing keys [max(0, pos0 + t + 1 -
@@ -243,7 +253,8 @@ size_t batch_image_bytes(uint32_t blocks, uint32_t tokens);
 hipError_t launch_batch_attention(BatchAttn a, uint32_t head_width, hipStream_t s);
 size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair);
 hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s);
-hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s);
+// Returns through parts the splits whose partials were left in a.part (0: y written).
+hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s, uint32_t* parts = nullptr);
 
 // ---- launchers (kernels.hip) -----------------------------------------------------------------
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);

@@ -1274,7 +1274,10 @@ struct af_session {
         return in;
     }
 
-    hipError_t batch_gemm(const Q4Dev& m, const Q4Dev* m2, uint32_t T, float* y, size_t y_stride) {
+    // parts non-null: the split-K partials may stay in BGEMM for the next input kernel, which then
+    // sums them; *parts tells it how many (0: y written).
+    hipError_t batch_gemm(const Q4Dev& m, const Q4Dev* m2, uint32_t T, float* y, size_t y_stride,
+                          uint32_t* parts = nullptr) {
         BatchGemm g{};
         g.w = m.view();
         if (m2) g.w2 = m2->view();
@@ -1283,7 +1286,20 @@ struct af_session {
         g.y = y;
         g.y_stride = y_stride;
         g.part = BGEMM.as<float>();
-        return launch_batch_gemm(g, m2 != nullptr, stream);
+        g.defer = parts != nullptr;
+        return launch_batch_gemm(g, m2 != nullptr, stream, parts);
+    }
+
+    // A BI_RESID input whose x is the output y of the GEMM before it: the GEMM's partials when it
+    // deferred its reduce (parts > 0), else y.
+    BatchIn resid_input(uint32_t T, const float* y, uint32_t parts) {
+        BatchIn in = batch_in(BI_RESID, T, hidden, y, hidden);
+        if (parts) {
+            in.part = BGEMM.as<float>();
+            in.parts = parts;
+            in.part_row = (size_t)(hidden + 15) / 16 * 16;
+        }
+        return in;
     }
 
     // Runs positions p0 .. p0 + T - 1 (ids in IDS) through every layer, appending their K/V; leaves
@@ -1293,9 +1309,10 @@ struct af_session {
     hipError_t enqueue_batch(uint32_t p0, uint32_t T, float* snap) {
         const size_t H = hidden, nl = layers.size();
         hipError_t e;
+        uint32_t down_parts = 0;  // the previous layer's down partials left in BGEMM
         for (uint32_t l = 0; l < nl; ++l) {
             LayerDev& L = layers[l];
-            BatchIn in = batch_in(l == 0 ? BI_EMBED : BI_RESID, T, hidden, l ? DB.as<float>() : nullptr, H);
+            BatchIn in = l == 0 ? batch_in(BI_EMBED, T, hidden, nullptr, H) : resid_input(T, DB.as<float>(), down_parts);
             in.w_n = L.input_norm.as<float>();
             in.eps_n = L.input_eps;
             in.x_out = XB.as<float>();
@@ -1366,9 +1383,10 @@ struct af_session {
 
             in = batch_in(BI_PLAIN, T, L.qn, ATTB.as<float>(), L.qn);
             if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
-            if ((e = batch_gemm(L.o, nullptr, T, PROJB.as<float>(), H)) != hipSuccess) return e;
+            uint32_t o_parts = 0;
+            if ((e = batch_gemm(L.o, nullptr, T, PROJB.as<float>(), H, &o_parts)) != hipSuccess) return e;
 
-            in = batch_in(BI_RESID, T, hidden, PROJB.as<float>(), H);
+            in = resid_input(T, PROJB.as<float>(), o_parts);
             in.res = XB.as<float>();
             in.w_a = L.post_attn.as<float>();
             in.eps_a = L.post_attn_eps;
@@ -1376,11 +1394,20 @@ struct af_session {
             in.eps_n = L.ffn_eps;
             in.x_out = HB.as<float>();
             if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
-            if ((e = batch_gemm(L.gate, &L.up, T, ACTB.as<float>(), intermediate)) != hipSuccess) return e;
+            uint32_t ff_parts = 0;
+            if ((e = batch_gemm(L.gate, &L.up, T, ACTB.as<float>(), intermediate, &ff_parts)) != hipSuccess) return e;
 
             in = batch_in(BI_PLAIN, T, intermediate, ACTB.as<float>(), intermediate);
+            if (ff_parts) {
+                in.part = BGEMM.as<float>();
+                in.parts = ff_parts;
+                in.part_row = (size_t)(intermediate + 15) / 16 * 16;
+            }
             if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
-            if ((e = batch_gemm(L.down, nullptr, T, DB.as<float>(), H)) != hipSuccess) return e;
+            // the last layer's down output stays in DB for the caller
+            if ((e = batch_gemm(L.down, nullptr, T, DB.as<float>(), H, l + 1 < nl ? &down_parts : nullptr)) !=
+                hipSuccess)
+                return e;
         }
         if (!snap) return hipSuccess;
         // the last layer's output (its image is not used)

@@ -83,10 +83,15 @@ __device__ __forceinline__ void block_halves(const float (&v)[8], uint32_t b, ui
 //             x_out_t (the residual stream), then f32(rms(v_t) w_n);
 //   BI_EMBED: v_t = table row ids[pos0 + t] * emb_scale, stored to x_out_t, then f32(rms(v_t) w_n).
 // RMSNorm sums of squares and products in double, f32 results (crates/domain/src/rms_norm.rs:24-41).
+// Thread j holds octets j, j + 512, ... (NO of them) in registers, and every global load of the
+// token (x, res and both norm weights) is issued before the first reduction, so the kernel waits
+// for memory once.
+// PS: x comes from in.parts split-K partial planes (NO == 1 only).
+template <int NO, bool PS>
 __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
-    extern __shared__ __align__(16) float xs[];  // [K]
+    extern __shared__ __align__(16) float xs[];  // [K], BI_EMBED only
     __shared__ double red[8];
-    const uint32_t t = blockIdx.x, tid = threadIdx.x, K = in.K, nb = K / 32, Tp = gridDim.x;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, K = in.K, nb = K / 32, no = K / 8, Tp = gridDim.x;
     _Float16* hi = reinterpret_cast<_Float16*>(in.img);
     _Float16* lo = hi + (size_t)nb * Tp * 32;
     float* inv = reinterpret_cast<float*>(lo + (size_t)nb * Tp * 32);
@@ -100,50 +105,130 @@ __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
         }
         return;
     }
-    if (in.mode == BI_EMBED) {
-        embed_row_at(in.table, gp(in.ids)[in.pos0 + t], in.emb_scale, xs, tid, blockDim.x);
-    } else {
-        const float* x = in.x + (size_t)t * in.stride;
-        for (uint32_t i = tid; i < K; i += blockDim.x) xs[i] = x[i];
+    const bool resid = in.mode == BI_RESID, embed = in.mode == BI_EMBED;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 x[NO][2], r[NO][2], wa[NO][2], wn[NO][2];
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+        const uint32_t o = tid + 512 * j;
+        x[j][0] = x[j][1] = r[j][0] = r[j][1] = wa[j][0] = wa[j][1] = wn[j][0] = wn[j][1] = z4;
+        if (o < no) {
+            if constexpr (PS) {
+                // every plane's loads issued first, then the sums in split order
+                const float* p0 = in.part + (size_t)t * in.part_row + 8 * o;
+                const size_t plane = (size_t)gridDim.x * in.part_row;
+                float4 pv[kDeferParts][2];
+#pragma unroll
+                for (int k = 0; k < (int)kDeferParts; ++k) {
+                    if ((uint32_t)k < in.parts) {
+                        pv[k][0] = reinterpret_cast<const float4*>(p0 + k * plane)[0];
+                        pv[k][1] = reinterpret_cast<const float4*>(p0 + k * plane)[1];
+                    }
+                }
+                x[j][0] = pv[0][0];
+                x[j][1] = pv[0][1];
+#pragma unroll
+                for (int k = 1; k < (int)kDeferParts; ++k) {
+                    if ((uint32_t)k < in.parts) {
+#pragma unroll
+                        for (int h = 0; h < 2; ++h) {
+                            x[j][h].x += pv[k][h].x;
+                            x[j][h].y += pv[k][h].y;
+                            x[j][h].z += pv[k][h].z;
+                            x[j][h].w += pv[k][h].w;
+                        }
+                    }
+                }
+            } else if (!embed) {
+                const float4* p = reinterpret_cast<const float4*>(in.x + (size_t)t * in.stride) + 2 * o;
+                x[j][0] = p[0];
+                x[j][1] = p[1];
+            }
+            if (resid) {
+                const float4* p = reinterpret_cast<const float4*>(in.res + (size_t)t * in.stride) + 2 * o;
+                r[j][0] = p[0];
+                r[j][1] = p[1];
+                if (in.w_a) {
+                    wa[j][0] = reinterpret_cast<const float4*>(in.w_a)[2 * o];
+                    wa[j][1] = reinterpret_cast<const float4*>(in.w_a)[2 * o + 1];
+                }
+            }
+            if (in.w_n) {
+                wn[j][0] = reinterpret_cast<const float4*>(in.w_n)[2 * o];
+                wn[j][1] = reinterpret_cast<const float4*>(in.w_n)[2 * o + 1];
+            }
+        }
     }
-    __syncthreads();
-    if (in.mode == BI_RESID) {
+    if (embed) {
+        embed_row_at(in.table, gp(in.ids)[in.pos0 + t], in.emb_scale, xs, tid, blockDim.x);
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NO; ++j) {
+            const uint32_t o = tid + 512 * j;
+            if (o < no) {
+                x[j][0] = reinterpret_cast<const float4*>(xs)[2 * o];
+                x[j][1] = reinterpret_cast<const float4*>(xs)[2 * o + 1];
+            }
+        }
+    }
+    if (resid) {
         double ra = 1.0;
         if (in.w_a) {
             double sa = 0.0;
-            for (uint32_t i = tid; i < K; i += blockDim.x) sa += (double)xs[i] * (double)xs[i];
+#pragma unroll
+            for (int j = 0; j < NO; ++j) sa += sq4(x[j][0]) + sq4(x[j][1]);
             ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
         }
-        const float* res = in.res + (size_t)t * in.stride;
-        for (uint32_t i = tid; i < K; i += blockDim.x) {
-            const float u = in.w_a ? norm_apply(xs[i], ra, in.w_a[i]) : xs[i];
-            xs[i] = __fmul_rn(__fadd_rn(u, res[i]), in.scale);
-        }
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NO; ++j)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                x[j][h] = resid4(in.w_a ? norm4(x[j][h], ra, wa[j][h]) : x[j][h], r[j][h], in.scale);
     }
     if (in.mode != BI_PLAIN) {
-        float* xo = in.x_out + (size_t)t * in.stride;
-        for (uint32_t i = tid; i < K; i += blockDim.x) {
-            xo[i] = xs[i];
-            if (in.snap) in.snap[(size_t)t * in.snap_stride + i] = xs[i];
+#pragma unroll
+        for (int j = 0; j < NO; ++j) {
+            const uint32_t o = tid + 512 * j;
+            if (o >= no) continue;
+            float4* xo = reinterpret_cast<float4*>(in.x_out + (size_t)t * in.stride) + 2 * o;
+            xo[0] = x[j][0];
+            xo[1] = x[j][1];
+            if (in.snap) {
+                float* sp = in.snap + (size_t)t * in.snap_stride + 8 * o;
+                const float* v = reinterpret_cast<const float*>(&x[j][0]);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) sp[k] = v[k];
+            }
         }
     }
     double rn = 1.0;
     if (in.w_n) {
         double ss = 0.0;
-        for (uint32_t i = tid; i < K; i += blockDim.x) ss += (double)xs[i] * (double)xs[i];
+#pragma unroll
+        for (int j = 0; j < NO; ++j) ss += sq4(x[j][0]) + sq4(x[j][1]);
         rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
     }
-    // each quad of threads holds one 32-element block (8 consecutive elements per thread)
-    for (uint32_t o = tid; o < nb * 4; o += blockDim.x) {
+    // a quad of threads holds one 32-element block (no is a multiple of 4: whole quads take part)
+#pragma unroll
+    for (int j = 0; j < NO; ++j) {
+        const uint32_t o = tid + 512 * j;
+        if (o >= no) continue;
         float v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = in.w_n ? norm_apply(xs[8 * o + k], rn, in.w_n[8 * o + k]) : xs[8 * o + k];
+        for (int h = 0; h < 2; ++h) {
+            const float4 u = in.w_n ? norm4(x[j][h], rn, wn[j][h]) : x[j][h];
+            v[4 * h] = u.x;
+            v[4 * h + 1] = u.y;
+            v[4 * h + 2] = u.z;
+            v[4 * h + 3] = u.w;
+        }
         block_halves(v, o >> 2, o & 3, t, Tp, hi, lo, inv);
     }
 }
 
-// BI_PLAIN inputs without a norm: one thread per 8-element octet, grid (Tp, octets / 256).
+// BI_PLAIN inputs without a norm: one thread per 8-element octet, grid (Tp, octets / 256).  PS: the
+// input is gelu(gate) * up from a gate/up pair's deferred split-K partials.
+template <bool PS>
 __global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
     const uint32_t t = blockIdx.x, o = blockIdx.y * 256 + threadIdx.x, nb = in.K / 32, Tp = gridDim.x;
     if (o >= nb * 4) return;  // whole quads: nb * 4 is a multiple of 4
@@ -151,7 +236,43 @@ __global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
     _Float16* lo = hi + (size_t)nb * Tp * 32;
     float* inv = reinterpret_cast<float*>(lo + (size_t)nb * Tp * 32);
     float v[8];
-    if (t < in.T) {
+    if (PS && t < in.T) {
+        // every plane's loads first, then each matrix's sums in split order, then gelu(gate) * up
+        const float* p0 = in.part + (size_t)t * in.part_row + 8 * o;
+        const size_t plane = (size_t)Tp * in.part_row;
+        float4 pv[kDeferPairParts][2][2];
+#pragma unroll
+        for (int k = 0; k < (int)kDeferPairParts; ++k)
+            if ((uint32_t)k < in.parts)
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) pv[k][q][h] = reinterpret_cast<const float4*>(p0 + (2 * k + q) * plane)[h];
+        float s[2][8];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                s[q][4 * h] = pv[0][q][h].x;
+                s[q][4 * h + 1] = pv[0][q][h].y;
+                s[q][4 * h + 2] = pv[0][q][h].z;
+                s[q][4 * h + 3] = pv[0][q][h].w;
+            }
+#pragma unroll
+        for (int k = 1; k < (int)kDeferPairParts; ++k)
+            if ((uint32_t)k < in.parts)
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        s[q][4 * h] += pv[k][q][h].x;
+                        s[q][4 * h + 1] += pv[k][q][h].y;
+                        s[q][4 * h + 2] += pv[k][q][h].z;
+                        s[q][4 * h + 3] += pv[k][q][h].w;
+                    }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = gelu_mul(s[0][i], s[1][i]);
+    } else if (t < in.T) {
         const float4* x = reinterpret_cast<const float4*>(in.x + (size_t)t * in.stride) + 2 * o;
         const float4 u0 = x[0], u1 = x[1];
         v[0] = u0.x; v[1] = u0.y; v[2] = u0.z; v[3] = u0.w;
@@ -586,16 +707,41 @@ hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
     if (in.mode == BI_PLAIN && !in.w_n) {
         if (in.stride % 4 || reinterpret_cast<uintptr_t>(in.x) % 16) return hipErrorInvalidValue;
         const uint32_t octets = in.K / 8;
-        hipLaunchKernelGGL(batch_plain_digits_kernel, dim3(padded_tokens(in.T), (octets + 255) / 256), dim3(256), 0, s,
-                           in);
+        const dim3 g(padded_tokens(in.T), (octets + 255) / 256);
+        if (in.parts) {
+            if (in.parts > kDeferPairParts || reinterpret_cast<uintptr_t>(in.part) % 16 || in.part_row % 4 ||
+                in.part_row < in.K)
+                return hipErrorInvalidValue;
+            hipLaunchKernelGGL(batch_plain_digits_kernel<true>, g, dim3(256), 0, s, in);
+        } else {
+            hipLaunchKernelGGL(batch_plain_digits_kernel<false>, g, dim3(256), 0, s, in);
+        }
     } else {
-        hipLaunchKernelGGL(batch_digits_kernel, dim3(padded_tokens(in.T)), dim3(512), (size_t)in.K * 4, s, in);
+        // float4 access to x, res, x_out and the norm weights
+        const auto a16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+        if (in.stride % 4 || !a16(in.x) || !a16(in.res) || !a16(in.x_out) || !a16(in.w_a) || !a16(in.w_n))
+            return hipErrorInvalidValue;
+        const uint32_t octets = in.K / 8;
+        const dim3 g(padded_tokens(in.T));
+        const size_t lds = in.mode == BI_EMBED ? (size_t)in.K * 4 : 0;
+        if (in.parts) {
+            if (in.mode != BI_RESID || octets > 512 || in.parts > kDeferParts || !a16(in.part) || in.part_row % 4 ||
+                in.part_row < in.K)
+                return hipErrorInvalidValue;
+            hipLaunchKernelGGL((batch_digits_kernel<1, true>), g, dim3(512), 0, s, in);
+        } else if (octets <= 512) {
+            hipLaunchKernelGGL((batch_digits_kernel<1, false>), g, dim3(512), lds, s, in);
+        } else if (octets <= 1024) {
+            hipLaunchKernelGGL((batch_digits_kernel<2, false>), g, dim3(512), lds, s, in);
+        } else {
+            hipLaunchKernelGGL((batch_digits_kernel<4, false>), g, dim3(512), lds, s, in);
+        }
     }
     return hipGetLastError();
 }
 
 template <int P, int G>
-static hipError_t gemm_launch(const BatchGemm& a, hipStream_t s) {
+static hipError_t gemm_launch(const BatchGemm& a, hipStream_t s, uint32_t* parts) {
     const GemmPlan p = gemm_plan(a.w.rows, a.w.blocks, P == 2);
     const uint32_t tiles = (a.w.rows + 15) / 16;
     const dim3 grid((tiles + p.R - 1) / p.R, p.S);
@@ -610,17 +756,22 @@ static hipError_t gemm_launch(const BatchGemm& a, hipStream_t s) {
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || p.S == 1) return e;
+    if (a.defer && !a.add && p.S <= (P == 2 ? kDeferPairParts : kDeferParts)) {
+        if (parts) *parts = p.S;
+        return hipSuccess;
+    }
     const uint32_t n = a.T * a.w.rows;
     hipLaunchKernelGGL((batch_reduce_kernel<P>), dim3((n + 255) / 256), dim3(256), 0, s, a, p.S, 16u * G);
     return hipGetLastError();
 }
 
-hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s) {
+hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s, uint32_t* parts) {
+    if (parts) *parts = 0;
     if (a.T == 0 || a.T > kBatchMax || a.w.rows == 0 || a.w.blocks == 0) return hipErrorInvalidValue;
     if (gelu_pair && (a.w2.rows != a.w.rows || a.w2.blocks != a.w.blocks)) return hipErrorInvalidValue;
     const bool two = a.T > 16;
-    if (gelu_pair) return two ? gemm_launch<2, 2>(a, s) : gemm_launch<2, 1>(a, s);
-    return two ? gemm_launch<1, 2>(a, s) : gemm_launch<1, 1>(a, s);
+    if (gelu_pair) return two ? gemm_launch<2, 2>(a, s, parts) : gemm_launch<2, 1>(a, s, parts);
+    return two ? gemm_launch<1, 2>(a, s, parts) : gemm_launch<1, 1>(a, s, parts);
 }
 
 }  // namespace af
