@@ -304,7 +304,8 @@ struct StepArgs {
     uint32_t* counters;             // attention merge tickets, one per KV head
     uint32_t* bar;                  // grid barrier words (kStepBarBytes, zero between launches)
     const uint8_t* stream;          // every GEMV weight record of a step, one run per streaming wave
-    const uint64_t* stream_off;     // [grid * kStepStreamWaves + 1] byte offset of each wave's run
+    const uint64_t* stream_off;     // [grid * kStepStreamWaves][2]: the byte range [start, end) of each
+                                    // streaming wave's records of this launch's layers
     uint32_t cmax;                  // attention chunks per KV head (at most grid / kv_heads, and
                                     // what the merge can hold in LDS: step_merge_chunks)
     uint32_t advance;               // 1: move ST_POS on at the end (a step without the head)
@@ -318,6 +319,14 @@ struct StepArgs {
     uint32_t xcd_local;             // 1: head group h's qkv rows, attention items and chunk partials all
                                     // live on XCD h (workgroups b with b % 8 == h) and are exchanged
                                     // through that XCD's L2 (step_qkv_tile, step_attn_chunk)
+    // Values handed over by launch layer l carry the tag epoch * tag_stride + 1 + tag_base + l (epoch:
+    // state word ST_EPOCH, one more per launch; tag_base + n_layers <= tag_stride), so that no tag
+    // repeats across the launches of a session.
+    uint32_t tag_stride, tag_base;
+    // Non-null: the launch's layer 0 follows a layer run by the per-operation kernels and takes its
+    // input from D and H as plain floats, with that layer's post-FFN norm and scale.
+    const float* prev_post_ffn;
+    float prev_post_ffn_eps, prev_scale;
 };
 
 // XCD-local layout (StepArgs::xcd_local): eight KV heads of two query heads each, a 256-workgroup

@@ -904,7 +904,7 @@ struct af_session {
     DevMem X, H, QKV, ATT, PROJ, ACT, ACTIMG, D, QKVT, PROJT, DT, LOGITS, PART, COUNTERS, HPART, HCOUNT, STATE, IDS, STOPS,
         RESULT, SNAP, KVSNAP;
     // persistent step kernel: layer table, digit images, barrier words
-    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF;
+    DevMem STEP_LAYERS, ATT_IMG, ACT_IMG, BAR, CLOCK, STREAM, STREAM_OFF, STREAM_RUNS;
     uint32_t clock_steps = 0, clock_used = 0;  // profiling: step timelines in CLOCK
     uint32_t clock_skip = 0;                     // profiling: plain launches before the timelines
     bool use_step = true;     // all layers of a step in one persistent launch
@@ -912,6 +912,18 @@ struct af_session {
     bool xcd_local = false;     // the step kernel's XCD-local layout (setup_step)
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
     size_t step_lds = 0;
+    // The step kernel takes runs of consecutive layers, one launch per run: a single run of every
+    // layer, or, when some layers are outside its limits (Gemma 4's 512-wide global layers), the
+    // runs between those, which the per-operation kernels take.  STEP_LAYERS holds the runs' layers
+    // in order; STREAM_RUNS each run's byte range of every streaming wave's records.
+    struct StepRun {
+        uint32_t first, j0, n;  // first layer, its entry in STEP_LAYERS, layers
+    };
+    std::vector<StepRun> runs;
+    std::vector<int32_t> run_at;   // per layer: the run starting there (-1: none)
+    std::vector<uint8_t> in_step;  // per layer: 1 if a run holds it
+    uint32_t step_q = 0, step_count = 0;  // the runs' query width and layers
+    bool segmented() const { return runs.size() != 1 || runs[0].n != layers.size(); }
     uint32_t max_kv_rows = 0;
     StepRecord* records = nullptr;      // mapped host memory, capacity + 2 entries (host view)
     StepRecord* records_dev = nullptr;  // the same memory as the device addresses it
@@ -1094,10 +1106,13 @@ struct af_session {
         return h;
     }
 
-    StepArgs step_args(bool advance, float* snap) {
+    // Launch arguments of run k.  advance: the launch moves ST_POS on (a single run without the
+    // head); the runs of a segmented step leave that to the end of the step.
+    StepArgs step_args(uint32_t k, bool advance, float* snap) {
+        const StepRun& r = runs[k];
         StepArgs a{};
-        a.layers = STEP_LAYERS.as<StepLayer>();
-        a.n_layers = (uint32_t)layers.size();
+        a.layers = STEP_LAYERS.as<StepLayer>() + r.j0;
+        a.n_layers = r.n;
         a.hidden = hidden;
         a.inter = intermediate;
         a.table = head.view();
@@ -1118,29 +1133,59 @@ struct af_session {
         a.counters = COUNTERS.as<uint32_t>();
         a.bar = BAR.as<uint32_t>();
         a.stream = STREAM.as<uint8_t>();
-        a.stream_off = STREAM_OFF.as<uint64_t>();
+        a.stream_off = STREAM_RUNS.as<uint64_t>() + (size_t)k * step_grid * kStepStreamWaves * 2;
         a.cmax = step_cmax;
-        a.xs_off = step_xs_offset(hidden, intermediate, max_q);
+        a.xs_off = step_xs_offset(hidden, intermediate, step_q);
         a.advance = advance ? 1u : 0u;
         a.snap = snap;
-        a.fail_phase = fail_phase;
+        a.fail_phase = k == 0 ? fail_phase : ~0u;
         a.xcd_local = xcd_local ? 1u : 0u;
+        a.tag_stride = step_count;
+        a.tag_base = r.j0;
+        if (r.first > 0) {  // the layer before is the per-operation kernels'
+            const LayerDev& P = layers[r.first - 1];
+            a.prev_post_ffn = P.post_ffn.as<float>();
+            a.prev_post_ffn_eps = P.post_ffn_eps;
+            a.prev_scale = P.layer_scale;
+        }
         return a;
     }
 
     uint32_t barriers() const { return 5 * (uint32_t)layers.size() - 1; }
     size_t clock_words() const { return (size_t)(barriers() + 1) * kStepMarks * step_grid; }
 
-    double layer_bytes() const {
+    // Weight bytes of run k's layers.
+    double layer_bytes(uint32_t k = 0) const {
         double b = 0;
-        for (const LayerDev& L : layers)
+        for (uint32_t l = runs[k].first; l < runs[k].first + runs[k].n; ++l) {
+            const LayerDev& L = layers[l];
             b += q4_bytes(L.qkv) + q4_bytes(L.o) + q4_bytes(L.gate) + q4_bytes(L.up) + q4_bytes(L.down);
+        }
         return b;
     }
 
+    // Every layer of a step, without the head or the position's advance: the step kernel's runs
+    // and the per-operation kernels of the other layers, in layer order.
+    hipError_t enqueue_layers() {
+        for (uint32_t l = 0; l < layers.size();) {
+            hipError_t e;
+            if (use_step && in_step[l]) {
+                const uint32_t k = (uint32_t)run_at[l];
+                e = timed(K_LAYERS, layer_bytes(k),
+                          [&] { return launch_step(step_args(k, false, nullptr), group, step_grid, step_lds, stream); });
+                l += runs[k].n;
+            } else {
+                e = enqueue_layer(l, true);
+                ++l;
+            }
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
+
     hipError_t enqueue_step(bool with_head) {
-        if (use_step) {
-            StepArgs a = step_args(!with_head, nullptr);
+        if (use_step && !segmented()) {
+            StepArgs a = step_args(0, !with_head, nullptr);
             int kind = K_LAYERS;
             if (timer && clock_skip) {
                 --clock_skip;
@@ -1155,10 +1200,8 @@ struct af_session {
             return timed(K_HEAD, (double)head.rows * (head.columns / 256) * 210.0 + 4.0 * 3.0 * hidden,
                          [&] { return launch_head(head_args(true, false), IN_RESID, head_blocks, stream); });
         }
-        for (uint32_t l = 0; l < layers.size(); ++l) {
-            hipError_t e = enqueue_layer(l, true);
-            if (e != hipSuccess) return e;
-        }
+        hipError_t e = enqueue_layers();
+        if (e != hipSuccess) return e;
         if (with_head)
             return timed(K_HEAD, (double)head.rows * (head.columns / 256) * 210.0 + 4.0 * 3.0 * hidden,
                          [&] { return launch_head(head_args(true, false), IN_RESID, head_blocks, stream); });
@@ -1435,44 +1478,91 @@ struct af_session {
 
 namespace {
 
-// Prepares the persistent step kernel: one launch of one workgroup per CU runs every layer.  A
-// model outside its limits (GEMV rows beyond two units per workgroup, attention chunks beyond
-// its LDS, mixed query groups) keeps the per-operation kernels in a graph instead.
+// Prepares the persistent step kernel: one launch of one workgroup per CU runs a run of layers
+// (every layer when all are within its limits).  Its layers share the attention geometry of the
+// first 256-wide layer (query group, query width); a layer outside its limits (another geometry,
+// GEMV rows beyond two units per workgroup, attention chunks beyond its LDS) runs on the
+// per-operation kernels between two runs, and then every step layer must have the first one's
+// shapes, so that each streaming wave holds the same records per layer.  A model with no such
+// layer keeps the per-operation kernels in a graph.
 int setup_step(af_session& s) {
     if (!s.use_step) return AF_OK;
-    const LayerDev& L0 = s.layers[0];
-    const uint32_t group = L0.q_heads / L0.kv_heads;
-    const size_t lds = step_lds_bytes(s.hidden, s.intermediate, s.max_q, group);
+    const uint32_t nl = (uint32_t)s.layers.size();
+    const LayerDev* R = nullptr;
+    for (const LayerDev& L : s.layers)
+        if (L.width == 256) {
+            R = &L;
+            break;
+        }
+    if (!R) {
+        s.use_step = false;
+        return AF_OK;
+    }
+    const uint32_t group = R->q_heads / R->kv_heads, step_q = R->qn;
+    const size_t lds = step_lds_bytes(s.hidden, s.intermediate, step_q, group);
     uint32_t grid = 0;
     HIP_OK(step_max_grid(group, lds, &grid), "step kernel occupancy");
     bool fits = grid >= 8 && s.hidden <= 4096 && s.hidden % 32 == 0;
+    const auto geometry = [&](const LayerDev& L) {
+        return L.width == 256 && L.q_heads / L.kv_heads == group && L.o.columns == step_q;
+    };
     uint32_t kv_max = 1;
-    for (const LayerDev& L : s.layers) kv_max = std::max(kv_max, L.kv_heads);
+    for (const LayerDev& L : s.layers)
+        if (geometry(L)) kv_max = std::max(kv_max, L.kv_heads);
     const uint32_t cm = std::min(grid / kv_max, step_merge_chunks(group, lds));
-    for (const LayerDev& L : s.layers) {
+    fits = fits && cm >= 1 && cm <= kStepMaxChunks;
+    s.in_step.assign(nl, 0);
+    uint32_t count = 0;
+    for (uint32_t i = 0; i < nl && fits; ++i) {
+        const LayerDev& L = s.layers[i];
         const uint32_t span = L.window ? std::min(L.window, s.capacity) : s.capacity;
-        fits = fits && L.q_heads / L.kv_heads == group && L.width == 256 && cm >= 1 && cm <= kStepMaxChunks &&
-               (span + cm - 1) / cm <= kStepMaxClen && (L.qkv.rows + 15) / 16 <= kStepMaxUnits * grid &&
-               (L.o.rows + 15) / 16 <= kStepMaxUnits * grid && (s.intermediate + 31) / 32 <= kStepMaxUnits * grid &&
-               (L.down.rows + 15) / 16 <= kStepMaxUnits * grid && L.o.columns == s.max_q;
+        if (geometry(L) && (span + cm - 1) / cm <= kStepMaxClen && (L.qkv.rows + 15) / 16 <= kStepMaxUnits * grid &&
+            (L.o.rows + 15) / 16 <= kStepMaxUnits * grid && (s.intermediate + 31) / 32 <= kStepMaxUnits * grid &&
+            (L.down.rows + 15) / 16 <= kStepMaxUnits * grid) {
+            s.in_step[i] = 1;
+            ++count;
+        }
     }
-    if (!fits) {
+    if (count < nl)
+        for (uint32_t i = 0; i < nl; ++i) {
+            const LayerDev& L = s.layers[i];
+            if (s.in_step[i] && !(L.q_heads == R->q_heads && L.kv_heads == R->kv_heads && L.shared_v == R->shared_v &&
+                                  L.qkv.rows == R->qkv.rows && L.o.rows == R->o.rows))
+                fits = false;
+        }
+    if (!fits || count == 0) {
         s.use_step = false;
         return AF_OK;
+    }
+    s.runs.clear();
+    s.run_at.assign(nl, -1);
+    for (uint32_t i = 0, j = 0; i < nl;) {
+        if (!s.in_step[i]) {
+            ++i;
+            continue;
+        }
+        af_session::StepRun r{i, j, 0};
+        for (; i < nl && s.in_step[i]; ++i, ++j) ++r.n;
+        s.run_at[r.first] = (int32_t)s.runs.size();
+        s.runs.push_back(r);
     }
     s.step_grid = grid;
     s.step_cmax = cm;
     s.group = group;
     s.step_lds = lds;
+    s.step_q = step_q;
+    s.step_count = count;
     int rc;
     // XCD-local layout (StepArgs::xcd_local): BASELINE's attention geometry (8 KV heads of two query
     // heads, width 256, separate V) on a 256-workgroup grid whose workgroup b runs on XCD b % 8,
     // which a probe launch checks on this device; AF_STEP_XCD_LOCAL=0 turns it off.
     bool xl = grid == 256 && group == 2 && !(std::getenv("AF_STEP_XCD_LOCAL") &&
                                               std::strcmp(std::getenv("AF_STEP_XCD_LOCAL"), "0") == 0);
-    for (const LayerDev& L : s.layers)
-        xl = xl && L.kv_heads == kXcds && L.q_heads == 2 * kXcds && L.width == 256 && !L.shared_v &&
-             L.qkv.rows == (L.q_heads + 2 * L.kv_heads) * 256u;
+    for (uint32_t i = 0; i < nl; ++i) {
+        const LayerDev& L = s.layers[i];
+        xl = xl && (!s.in_step[i] || (L.kv_heads == kXcds && L.q_heads == 2 * kXcds && L.width == 256 && !L.shared_v &&
+                                      L.qkv.rows == (L.q_heads + 2 * L.kv_heads) * 256u));
+    }
     if (xl) {
         DevMem map;
         if ((rc = dev_alloc(map, (size_t)grid * 4, "XCD map"))) return rc;
@@ -1482,10 +1572,11 @@ int setup_step(af_session& s) {
         for (uint32_t b = 0; b < grid; ++b) xl = xl && xcc[b] == b % kXcds;
     }
     s.xcd_local = xl;
-    std::vector<StepLayer> table(s.layers.size());
-    for (size_t i = 0; i < s.layers.size(); ++i) {
+    std::vector<StepLayer> table;
+    for (uint32_t i = 0; i < nl; ++i) {
+        if (!s.in_step[i]) continue;
         const LayerDev& L = s.layers[i];
-        StepLayer& t = table[i];
+        StepLayer& t = table.emplace_back();
         t.qkv = L.qkv.view();
         t.o = L.o.view();
         t.gate = L.gate.view();
@@ -1539,7 +1630,9 @@ int setup_step(af_session& s) {
     for (uint32_t i = 0; i < nw; ++i) {
         const uint32_t b = i / kStepStreamWaves, w = i % kStepStreamWaves + 1;
         uint64_t recs = 0;
-        for (const LayerDev& L : s.layers) {
+        for (uint32_t li = 0; li < nl; ++li) {
+            if (!s.in_step[li]) continue;
+            const LayerDev& L = s.layers[li];
             recs += step_wave_records((L.qkv.rows + 15) / 16, 1, (L.qkv.columns / 32 + 3) / 4, b, grid, w);
             recs += step_wave_records((L.o.rows + 15) / 16, 1, (L.o.columns / 32 + 3) / 4, b, grid, w);
             recs += step_wave_records((L.gate.rows + 31) / 32, 4, (L.gate.columns / 32 + 3) / 4, b, grid, w);
@@ -1548,9 +1641,19 @@ int setup_step(af_session& s) {
         off[i + 1] = off[i] + recs * kStepRecord;
     }
     if ((rc = dev_upload(s.STREAM_OFF, off.data(), off.size() * 8, "weight stream offsets"))) return rc;
+    // each run's range of every wave's records (the runs' layers have equal shapes when there are
+    // several, so a wave holds (off[i + 1] - off[i]) / count bytes per layer)
+    std::vector<uint64_t> ranges(s.runs.size() * nw * 2);
+    for (size_t k = 0; k < s.runs.size(); ++k)
+        for (uint32_t i = 0; i < nw; ++i) {
+            const uint64_t per = (off[i + 1] - off[i]) / count;
+            ranges[(k * nw + i) * 2] = off[i] + s.runs[k].j0 * per;
+            ranges[(k * nw + i) * 2 + 1] = s.runs.size() == 1 ? off[i + 1] : off[i] + (s.runs[k].j0 + s.runs[k].n) * per;
+        }
+    if ((rc = dev_upload(s.STREAM_RUNS, ranges.data(), ranges.size() * 8, "weight stream ranges"))) return rc;
     if ((rc = dev_alloc(s.STREAM, off.back() + kStepStreamPad, "weight stream"))) return rc;
     HIP_OK(hipMemset(s.STREAM.as<uint8_t>() + off.back(), 0, kStepStreamPad), "weight stream padding");
-    HIP_OK(launch_stream_repack(s.STEP_LAYERS.as<StepLayer>(), (uint32_t)s.layers.size(), grid, s.xcd_local ? 1u : 0u,
+    HIP_OK(launch_stream_repack(s.STEP_LAYERS.as<StepLayer>(), count, grid, s.xcd_local ? 1u : 0u,
                                 s.STREAM.as<uint8_t>(), s.STREAM_OFF.as<uint64_t>(), nullptr),
            "weight stream build");
     HIP_OK(hipDeviceSynchronize(), "weight stream build");
@@ -2078,7 +2181,7 @@ int af_session_profile(af_session* s, const uint32_t* prompt, size_t n_prompt, u
                        size_t* n_out, af_kernel_timing* timings, size_t capacity, size_t* n_timings) {
     if (!timings || !n_timings || capacity < K_KINDS) return fail(AF_ERR_INVALID, "timing output too small");
     KernelTimer timer;
-    if (s && s->use_step && !s->poisoned) {
+    if (s && s->use_step && !s->poisoned && !s->segmented()) {
         const size_t bytes = (size_t)max_new * s->clock_words() * 8;
         if (s->CLOCK.bytes < bytes) {
             int r = dev_alloc(s->CLOCK, bytes, "step timeline");
@@ -2300,12 +2403,14 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     // the whole trace runs again there (it rewrites the same K/V slots).
     for (int attempt = 0; attempt < 2; ++attempt) {
     if ((rc = s->set_state(s->consumed, 0))) return rc;
-    const bool step = s->use_step;
+    // step: one step-kernel launch per position; otherwise the layers one by one (per-operation
+    // kernels, and the step kernel's runs of a segmented session)
+    const bool step = s->use_step && !s->segmented();
     for (size_t i = 0; i < pend; ++i) {
         if (step) {
-            HIP_OK(launch_step(s->step_args(true, nullptr), s->group, s->step_grid, s->step_lds, st), "trace step");
+            HIP_OK(launch_step(s->step_args(0, true, nullptr), s->group, s->step_grid, s->step_lds, st), "trace step");
         } else {
-            for (uint32_t l = 0; l < nl; ++l) HIP_OK(s->enqueue_layer(l, true), "trace layer");
+            HIP_OK(s->enqueue_layers(), "trace layers");
             HIP_OK(launch_advance(s->STATE.as<uint32_t>(), st), "trace advance");
         }
     }
@@ -2332,17 +2437,30 @@ int af_session_trace(af_session* s, const uint32_t* ids, size_t n, float* layer_
     for (size_t t = 0; t < n; ++t) {
         if (step) {
             // the step kernel writes layers 0..L-2's outputs; the last comes from D and H after it
-            HIP_OK(launch_step(s->step_args(true, layer_outputs ? s->SNAP.as<float>() : nullptr), s->group,
+            HIP_OK(launch_step(s->step_args(0, true, layer_outputs ? s->SNAP.as<float>() : nullptr), s->group,
                                s->step_grid, s->step_lds, st),
                    "trace step");
             if (layer_outputs) HIP_OK(snapshot(nl - 1), "trace snapshot");
             if (kv_appended)
                 for (uint32_t l = 0; l < nl; ++l) HIP_OK(kv_copy(l, t), "trace K/V copy");
         } else {
-            for (uint32_t l = 0; l < nl; ++l) {
-                HIP_OK(s->enqueue_layer(l, true), "trace layer");
-                if (kv_appended) HIP_OK(kv_copy(l, t), "trace K/V copy");
-                if (layer_outputs) HIP_OK(snapshot(l), "trace snapshot");
+            for (uint32_t l = 0; l < nl;) {
+                if (s->use_step && s->in_step[l]) {
+                    // a run writes its layers' outputs but the last, which comes from D and H after it
+                    const uint32_t k = (uint32_t)s->run_at[l], n_run = s->runs[k].n;
+                    HIP_OK(launch_step(s->step_args(k, false, layer_outputs ? s->SNAP.as<float>() + l * H : nullptr),
+                                       s->group, s->step_grid, s->step_lds, st),
+                           "trace step");
+                    if (kv_appended)
+                        for (uint32_t j = l; j < l + n_run; ++j) HIP_OK(kv_copy(j, t), "trace K/V copy");
+                    if (layer_outputs) HIP_OK(snapshot(l + n_run - 1), "trace snapshot");
+                    l += n_run;
+                } else {
+                    HIP_OK(s->enqueue_layer(l, true), "trace layer");
+                    if (kv_appended) HIP_OK(kv_copy(l, t), "trace K/V copy");
+                    if (layer_outputs) HIP_OK(snapshot(l), "trace snapshot");
+                    ++l;
+                }
             }
         }
         if (layer_outputs)

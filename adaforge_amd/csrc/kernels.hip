@@ -560,7 +560,6 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     __shared__ float scores[G][kAttnMaxChunkLen];
     __shared__ __align__(16) float vred[8][G][D];
     __shared__ double dred[W][NH];
-    __shared__ float fred[8];
     __shared__ float cw[G][kAttnMaxChunks];
     __shared__ bool last;
 
@@ -980,7 +979,11 @@ hipError_t launch_resid(const InputStage& in, uint32_t width, float* y, hipStrea
     return hipGetLastError();
 }
 
-__global__ void advance_kernel(uint32_t* state) { state[ST_POS] += 1u; }
+// Not after a step-kernel launch of this step timed out (ST_BAD 2): ST_POS then stays at the step's
+// position, which the per-operation kernels run again.
+__global__ void advance_kernel(uint32_t* state) {
+    if (state[ST_BAD] != 2u) state[ST_POS] += 1u;
+}
 
 // Clears n words with vector stores (a kernel rather than a memset, so that a caller may capture
 // it in a graph).

@@ -485,6 +485,7 @@ struct Stage {
     const float *res, *w_a, *w_n;
     const uint32_t* xt;   // S_RESID: the input as (value, tag) word pairs (poll_tagged); S_TDIGITS: the
                           // tagged digit image (poll_image)
+    const float* xf;      // S_RESID instead of xt: the input as plain floats, written before the launch
     uint32_t tag;         // the tag of the input's current values
     float eps_a, eps_n, scale;
     const int8_t* dig;    // S_DIGITS
@@ -573,7 +574,10 @@ __device__ __forceinline__ bool stage_inputs(int kind, const Stage& in, const In
     } else if (kind == S_TDIGITS) {
         ok = poll_image(in.xt, nst * kStepImg, in.tag, img, img + nst * kStepImg, wave, lane);  // step_xs_offset
     } else if (kind == S_RESID) {
-        ok = poll_tagged(in.xt, K, in.tag, xs, wave * 64 + lane);  // the residual is in xs + K
+        if (in.xf)
+            dma_all(in.xf, K * 4, reinterpret_cast<uint8_t*>(xs), wave, lane);
+        else
+            ok = poll_tagged(in.xt, K, in.tag, xs, wave * 64 + lane);  // the residual is in xs + K
     } else {
         embed_row(emb, xs, wave * 64 + lane, kThreads);
     }
@@ -1166,12 +1170,19 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
         d.yt = a.QKVT;
         d.ytag = tag0 + l;
         d.rows = L.qkv.rows;
-        if (l == 0) {
+        if (l == 0 && !a.prev_post_ffn) {
             d.in_kind = S_EMBED;
             d.emb.table = a.table;
             d.emb.ids = a.ids;
             d.emb.state = a.state;
             d.emb.emb_scale = a.emb_scale;
+        } else if (l == 0) {
+            d.in_kind = S_RESID;
+            d.in.xf = a.D;
+            d.in.res = a.H;
+            d.in.w_a = a.prev_post_ffn;
+            d.in.eps_a = a.prev_post_ffn_eps;
+            d.in.scale = a.prev_scale;
         } else {
             CLayer& P = layer_at(a, l - 1);
             d.in_kind = S_RESID;
@@ -1333,7 +1344,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     if (a.state[ST_STOP]) return;  // uniform: written only before the launch
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     const uint32_t pos = a.state[ST_POS];
-    const uint32_t tag0 = a.state[ST_EPOCH] * a.n_layers + 1u;  // never 0, the tag of a cleared pair
+    const uint32_t tag0 = a.state[ST_EPOCH] * a.tag_stride + 1u + a.tag_base;  // never 0, a cleared pair's tag
     Grid g{a.bar, 0u, 0u, &ok_flag, a.clock};
     stamp(g, M_START);
     bool failed = false;
@@ -1345,7 +1356,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
     Ring r;
     if (wave != 0) {
         const uint32_t w = blockIdx.x * kStreamWaves + (wave - 1);
-        const uint64_t o0 = a.stream_off[w], o1 = a.stream_off[w + 1];
+        const uint64_t o0 = a.stream_off[2 * w], o1 = a.stream_off[2 * w + 1];
         const uint64_t base = reinterpret_cast<uint64_t>(a.stream) + o0;
         r.base_lo = (uint32_t)base;
         r.base_hi = (uint32_t)(base >> 32);

@@ -18,16 +18,23 @@ pytestmark = pytest.mark.gpu
 THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
-def model_16q():
-    """Six layers: five local (16 query / 8 KV heads of 256, window 16), one global (16 query heads, one
-    KV head of 512, K weights reused as V, Gemma 4's RoPE factors), at hidden 1024."""
-    return synth.gemma4_model(name="gemma4-test", layers=6, hidden=1024, intermediate=2048, local_q=(16, 8, 256),
-                              global_q=(16, 1, 512), vocabulary=2048, window=16)
+def model_16q(layers=6, global_every=6):
+    """Local layers of 16 query / 8 KV heads of 256 (window 16) and every `global_every`-th layer global
+    (16 query heads, one KV head of 512, K weights reused as V, Gemma 4's RoPE factors), at hidden
+    1024: by default five local layers and a global one."""
+    return synth.gemma4_model(name="gemma4-test", layers=layers, hidden=1024, intermediate=2048, local_q=(16, 8, 256),
+                              global_q=(16, 1, 512), vocabulary=2048, window=16, global_every=global_every)
 
 
-def test_gemma4_layers_teacher_forced_and_greedy_ids():
-    model = model_16q()
-    g = model.layers[5]
+# The step kernel takes the local layers in runs between the global ones, which the per-operation
+# kernels take: runs [0, 5) then layer 5; or runs [0, 2), [3, 5), [6, 7) around layers 2 and 5 (runs
+# that start after a per-operation layer and one that ends the model).
+@pytest.mark.parametrize("layers,global_every", [(6, 6), (7, 3)])
+def test_gemma4_layers_teacher_forced_and_greedy_ids(layers, global_every):
+    model = model_16q(layers, global_every)
+    glob = [i for i in range(layers) if i % global_every == global_every - 1]
+    runs = sum(1 for i in range(layers) if i not in glob and (i == 0 or i - 1 in glob))
+    g = model.layers[glob[0]]
     assert g.v is None and g.head_width == 512 and g.kv_heads == 1 and (g.rope_factors == 1e30).sum() == 192
     n = 80  # past the local window (16) and several 32-token attention chunks
     ids = [int(i) for i in synth.prompt_ids(n, model.vocabulary, name="gemma4-test.ids")]
@@ -47,6 +54,10 @@ def test_gemma4_layers_teacher_forced_and_greedy_ids():
         s.reset()
         prompt = ids[:12]
         got = s.generate(prompt, [model.vocabulary - 1], 6)
+        # each decode step: one step-kernel launch per run, the per-operation kernels per global layer
+        s.reset()
+        _, t = s.profile(prompt, 2)
+        assert t["layers"][0] == 2 * runs and t["qkv"][0] == 2 * len(glob), t
     ref = oracle.Model(model, capacity=32, threads=THREADS)
     want, _, _ = ref.generate(prompt, [model.vocabulary - 1], 6)
     ref.close()
