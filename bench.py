@@ -457,6 +457,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the configs 0-3 operator legs")
     ap.add_argument("--configs-only", action="store_true", help="only the configs 0-3 GPU legs (profiling)")
     ap.add_argument("--no-extras", action="store_true", help="skip the prefill and speculative-decoding legs")
+    ap.add_argument("--legs", default="prefill,long,speculative,gemma4",
+                    help="the extra legs to run (comma-separated subset of prefill, long, speculative, gemma4)")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
@@ -464,6 +466,9 @@ def main():
         sys.exit(2)
     if a.steps < 1 or a.warmup < 1:
         sys.exit("--steps and --warmup must be >= 1")
+    legs = set() if a.no_extras else {x for x in a.legs.split(",") if x}
+    if legs - {"prefill", "long", "speculative", "gemma4"}:
+        sys.exit(f"--legs: unknown leg(s) {sorted(legs - {'prefill', 'long', 'speculative', 'gemma4'})}")
 
     from adaforge_amd import synth
     from adaforge_amd.backend import HipDiagnostics
@@ -537,10 +542,13 @@ def main():
         configs = gpu_configs()
 
     prefill = spec = gemma4 = longctx = None
-    if not a.no_extras:
+    if "prefill" in legs:
         prefill = prefill_leg(model, stop)
+    if "long" in legs:
         longctx = long_context_leg(model, stop)
+    if "speculative" in legs:
         spec = speculative_leg()
+    if "gemma4" in legs:
         gemma4 = gemma4_leg()
 
     cpu = None
