@@ -66,13 +66,13 @@ enum InputKind : int {
     IN_DIGITS = 4, // the input's digit image (below), written by the producing kernel
 };
 
-// Exact int8 digit form of an fp32 vector for the matrix-core GEMV: block b of 32 elements
-// is s_b (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21).  The image of a vector of nst super-tiles
-// (128 elements each) is nst * 640 bytes: dig[b * 4 + t][32] int8 holds digit t of block b
-// (nst * 512 bytes), then tab[b * 4 + t] = {s_b 2^-7t, t == 0 ? 8 sum_j x_j : 0}.
-struct DigitTab {
-    float scale;
-    float bias;
+// Int8 digit form of an fp32 vector for the matrix-core GEMV: block b of 32 elements is
+// s_b (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21), s_b = 2^(ilogb(max |x|) - 5).  The image of a vector
+// of nst super-tiles (128 elements each) is nst * kStepImg (576) bytes: dig[b * 4 + t][32] int8
+// holds digit t of block b (nst * 512 bytes), then one BlockTab per block: s_b 2^-14, s_b 2^-21
+// and -8 sum_j x_j.
+struct alignas(16) BlockTab {
+    float s14, s21, nbias, pad;
 };
 
 struct InputStage {
@@ -368,7 +368,7 @@ constexpr size_t kStepBarBytes = 32 * 10 * 4;
 // Q4View layout followed by its 128 scale bytes.
 constexpr uint32_t kStepStreamWaves = 7;
 constexpr uint32_t kStepRecord = 1152;
-constexpr uint32_t kStepImg = 576;  // digit image bytes per super-tile: 512 digits + 4 block entries
+constexpr uint32_t kStepImg = 576;  // digit image bytes per super-tile: 512 digits + 4 BlockTab entries
 constexpr uint32_t kStepStreamPad = 64 * kStepRecord;  // readable bytes after the last run (ring over-read)
 
 __host__ __device__ inline uint32_t step_units(uint32_t units, uint32_t b, uint32_t grid) {

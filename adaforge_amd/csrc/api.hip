@@ -697,7 +697,7 @@ int af_ffn_create(const af_ffn_weights* w, af_ffn** out) {
     if ((rc = dev_upload(f->pre, w->pre.weights, (size_t)hidden * 4, "FFN norm"))) return rc;
     if (has_post && (rc = dev_upload(f->post, w->post.weights, (size_t)hidden * 4, "FFN norm"))) return rc;
     if ((rc = dev_alloc(f->act, (size_t)inter * 4, "FFN activations"))) return rc;
-    const size_t img = (size_t)(inter + 127) / 128 * 640;  // blocks past the activations stay zero
+    const size_t img = (size_t)(inter + 127) / 128 * kStepImg;  // blocks past the activations stay zero
     if ((rc = dev_alloc(f->act_img, img, "FFN activation digits"))) return rc;
     HIP_OK(hipMemset(f->act_img.p, 0, img), "FFN activation digits clear");
     if ((rc = dev_alloc(f->mid, (size_t)hidden * 4, "FFN down output"))) return rc;
@@ -1780,7 +1780,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         {&s->ATT, (size_t)max_q * 4, true},
         {&s->PROJ, (size_t)hidden * 4, true},
         {&s->ACT, (size_t)inter * 4, true},
-        {&s->ACTIMG, (size_t)(inter + 127) / 128 * 640, true},  // the down GEMV's input digit image
+        {&s->ACTIMG, (size_t)(inter + 127) / 128 * kStepImg, true},  // the down GEMV's input digit image
         {&s->D, (size_t)hidden * 4, true},
         {&s->QKVT, (size_t)s->max_qkv * 8, true},  // (value, tag) pairs: tag 0 is never current
         {&s->PROJT, (size_t)hidden * 8, true},

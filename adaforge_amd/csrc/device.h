@@ -431,14 +431,10 @@ __device__ __forceinline__ void quad_stats(const float (&v)[8], float& m, float&
 }
 
 // Table entries of a block (max |x| m, element sum `sum`): plane scales s 2^-7t and the bias.
-__device__ __forceinline__ DigitTab digit_entry(float m, float sum, int t) {
+// The table entry of a block of max |x| m and element sum `sum` (BlockTab).
+__device__ __forceinline__ BlockTab block_tab(float m, float sum) {
     const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
-    return DigitTab{ldexpf(s, -7 * t), t == 0 ? 8.0f * sum : 0.0f};
-}
-
-__device__ __forceinline__ void digit_tab(DigitTab* tab, uint32_t b, float m, float sum) {
-#pragma unroll
-    for (int t = 0; t < 4; ++t) tab[b * 4 + t] = digit_entry(m, sum, t);
+    return BlockTab{ldexpf(s, -14), ldexpf(s, -21), -8.0f * sum, 0.0f};
 }
 
 // ---- GEMV prologue: the input's digit image in LDS ----------------------------------------------
@@ -472,7 +468,7 @@ __device__ __forceinline__ void input_load(const InputStage& in, uint32_t K, uin
     const uint32_t tid = threadIdx.x;
     if constexpr (IN == IN_DIGITS) {
         const uint4* src = reinterpret_cast<const uint4*>(in.dig);
-        const uint32_t n16 = nst * 40;
+        const uint32_t n16 = nst * (kStepImg / 16);
 #pragma unroll
         for (int j = 0; j < 3 * Q; ++j) {
             const uint32_t i = tid + j * blockDim.x;
@@ -498,14 +494,14 @@ __device__ __forceinline__ void input_load(const InputStage& in, uint32_t K, uin
 // (normalised) input.  xs (K floats of LDS) is used by IN_EMBED only.  The caller syncs.
 template <int IN, int Q>
 __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t nst, InputRegs<IN, Q>& g, float* xs,
-                             int8_t* dig, DigitTab* tab, double* red) {
+                             int8_t* dig, BlockTab* tab, double* red) {
     const uint32_t tid = threadIdx.x, n8 = K / 8;
     if constexpr (IN == IN_DIGITS) {
         uint4* dst = reinterpret_cast<uint4*>(dig);  // digits and table are contiguous
 #pragma unroll
         for (int j = 0; j < 3 * Q; ++j) {
             const uint32_t i = tid + j * blockDim.x;
-            if (i < nst * 40) dst[i] = g.d[j];
+            if (i < nst * (kStepImg / 16)) dst[i] = g.d[j];
         }
         return;
     } else {
@@ -583,62 +579,38 @@ __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t n
             quad_stats(v[j], m, sum);  // every lane of the quad takes part, in range or not
             if (b < nst * 4) {
                 digits8(v[j], m, dig, b, p);
-                if (p == 0) digit_tab(tab, b, m, sum);
+                if (p == 0) tab[b] = block_tab(m, sum);
             }
         }
     }
 }
 
-constexpr int kQ4Ahead = 16;  // super-tiles loaded ahead per wave
-
 struct Q4Tile {
-    uint4 code;   // lane 16 g + r: the 16 code bytes of block g of row r of the super-tile
-    uint2 scale;  // lane (q, n): the fp16 scales of rows 4q..4q+3 for block n / 4
+    uint4 code;      // lane 16 g + r: the 16 code bytes of block g of row r of the super-tile
+    uint32_t scale;  // lane 16 g + r: the fp16 scale of block g of row r (low half)
 };
 
-// Loads lane's share of super-tile st of 16-row tile `tile` (tiled layout: codes
-// [tile][st][4 blocks][16 rows][16 bytes], scales [tile][st][4 blocks][16 rows]).  The code
-// load is lane-linear: each 64-byte line is requested by four consecutive lanes.
-__device__ __forceinline__ void q4_tile_load(const uint4* codes, const uint2* scales, size_t tile, uint32_t nst,
-                                             uint32_t st, uint32_t lane, Q4Tile& t) {
-    const size_t base = tile * nst + st;
-    t.code = ld_stream(codes + base * 64 + lane);
-    t.scale = ld_stream(scales + base * 16 + ((lane & 15) >> 2) * 4 + (lane >> 4));
-}
-
-// acc[i] += row (4q + i) of the tile times the input, summed over the lane's column n: two
-// int8 MFMAs (low then high nibbles) against the digit planes of super-tile st in LDS, folded
-// with the block scales.  Lane l = 16 q + n; column n is (block n / 4, digit plane n % 4).
-__device__ __forceinline__ void q4_mfma_tile(const Q4Tile& w, uint32_t st, const int8_t* dig, const DigitTab* tab,
-                                             uint32_t lane, float (&acc)[4]) {
-    const uint32_t q = lane >> 4, n = lane & 15, blk = n >> 2, t = n & 3;
-    const uint4 cw = w.code;
-    const uint2 sw = w.scale;
-    const v4i a1 = {(int)(cw.x & 0x0F0F0F0Fu), (int)(cw.y & 0x0F0F0F0Fu), (int)(cw.z & 0x0F0F0F0Fu),
-                    (int)(cw.w & 0x0F0F0F0Fu)};
-    const v4i a2 = {(int)((cw.x >> 4) & 0x0F0F0F0Fu), (int)((cw.y >> 4) & 0x0F0F0F0Fu),
-                    (int)((cw.z >> 4) & 0x0F0F0F0Fu), (int)((cw.w >> 4) & 0x0F0F0F0Fu)};
+// acc += row r's part of one record (super-tile st of a 16-row tile) times the input, for lane
+// 16 q + r: two int8 MFMAs with A = the digit planes (row m = 4 g + t: digit t of block g, non-zero
+// in k-group g only; a0 / a1 the lane's plane or the zero block, chosen by the caller's address)
+// and B = the codes (low nibbles against elements 0..15, high nibbles against 16..31), so the lane
+// receives D[4 q + t][r], the digit sums of block q and row r, and adds
+// d(r, q) ((2^14 D0 + 2^7 D1 + D2) s 2^-14 + D3 s 2^-21 - 8 sum_j x_j).  2^14 D0 + 2^7 D1 + D2 is
+// exact in int32 (|D_t| <= 32 * 15 * 64).
+__device__ __forceinline__ void q4_mfma_tile(const Q4Tile& w, const v4i& a0, const v4i& a1, const BlockTab& tb,
+                                             float& acc) {
+    constexpr uint32_t M = 0x0F0F0F0Fu;
+    const uint4 c = w.code;
+    const v4i bl = {(int)(c.x & M), (int)(c.y & M), (int)(c.z & M), (int)(c.w & M)};
+    const v4i bh = {(int)((c.x >> 4) & M), (int)((c.y >> 4) & M), (int)((c.z >> 4) & M), (int)((c.w >> 4) & M)};
     const v4i zero = {0, 0, 0, 0};
-    v4i b1 = zero, b2 = zero;
-    if (blk == q) {  // B lane (k-group q, column n) is non-zero for block q only
-        const uint4* dp = reinterpret_cast<const uint4*>(dig + ((size_t)(st * 4 + q) * 4 + t) * 32);
-        const uint4 lo = dp[0], hi = dp[1];
-        b1 = v4i{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w};
-        b2 = v4i{(int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-    }
-    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, b1, zero, 0, 0, 0);
-    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, b2, d, 0, 0, 0);
-    const DigitTab tb = tab[(st * 4 + blk) * 4 + t];
-    const uint16_t dh[4] = {(uint16_t)(sw.x & 0xFFFFu), (uint16_t)(sw.x >> 16), (uint16_t)(sw.y & 0xFFFFu),
-                            (uint16_t)(sw.y >> 16)};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = fmaf(h2f(dh[i]), fmaf((float)d[i], tb.scale, -tb.bias), acc[i]);
+    v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, bl, zero, 0, 0, 0);
+    d = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, bh, d, 0, 0, 0);
+    const int I = (d[0] << 14) + (d[1] << 7) + d[2];
+    float in = fmaf((float)I, tb.s14, tb.nbias);
+    in = fmaf((float)d[3], tb.s21, in);
+    acc = fmaf(h2f((uint16_t)w.scale), in, acc);
 }
 
-// Sum of acc over the 16 columns of each row (lanes of a 16-lane group hold one row quad).
-__device__ __forceinline__ void q4_row_sums(float (&acc)[4]) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = row_sum(acc[i]);
-}
 
 }  // namespace af

@@ -77,9 +77,9 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
         }
     }
     GemvCursor cs = ld;
-    const uint32_t code_off = lane * 16, scale_off = ((((lane & 15) >> 2) * 4) + (lane >> 4)) * 8;
+    const uint32_t code_off = lane * 16, scale_off = lane * 2;
     v4u rc[kGemvRing];
-    v2u rsc[kGemvRing];
+    uint32_t rsc[kGemvRing];
     auto request = [&](int u, const GemvCursor& c, bool ok) {
         const bool second = T == 2 && c.k == 1;
         const uint8_t* codes = second ? a.w2.codes : a.w.codes;
@@ -90,7 +90,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
         const __amdgpu_buffer_rsrc_t rscale =
             __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(scales) + rec * 64, 0, ok ? 128 : 0, 0x00020000);
         rc[u] = __builtin_amdgcn_raw_buffer_load_b128(rcode, code_off, 0, 2);
-        rsc[u] = __builtin_amdgcn_raw_buffer_load_b64(rscale, scale_off, 0, 2);
+        rsc[u] = __builtin_amdgcn_raw_buffer_load_b16(rscale, scale_off, 0, 2);
     };
 
     InputRegs<IN, Q> g;
@@ -105,23 +105,26 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
 
     const size_t xs_bytes = IN == IN_EMBED ? (size_t)K * 4 : 0;
     int8_t* dig = reinterpret_cast<int8_t*>(smem + xs_bytes);
-    DigitTab* tab = reinterpret_cast<DigitTab*>(smem + xs_bytes + (size_t)nst * 512);
+    BlockTab* tab = reinterpret_cast<BlockTab*>(smem + xs_bytes + (size_t)nst * 512);
+    uint4* zero_blk = reinterpret_cast<uint4*>(smem + xs_bytes + (size_t)nst * kStepImg);  // 32 bytes
     input_digits<IN, Q>(a.in, K, nst, g, reinterpret_cast<float*>(smem), dig, tab, red);
+    if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);
     float* pflat = &part[0][0][0];
     for (uint32_t i = tid; i < kGemvWaves * kGemvMaxUnits * T * 16; i += blockDim.x) pflat[i] = 0.0f;
     __syncthreads();
 
-    const uint32_t q = lane >> 4, n = lane & 15;  // D tile: rows 4q..4q+3, column n
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    // lane 16 q + r: A row r (digit plane r of the super-tile) in k-group q, which is non-zero when
+    // r / 4 == q (the plane at a_base + st * a_step, else the zero block with a_step 0); D column r
+    const uint32_t r = lane & 15, q = lane >> 4;
+    const bool aon = (r >> 2) == q;
+    const int8_t* a_base = aon ? dig + r * 32 : reinterpret_cast<const int8_t*>(zero_blk);
+    const uint32_t a_step = aon ? 512u : 0u;
+    float acc = 0.0f;
     uint32_t cur = cs.j * T + cs.k;
     auto flush = [&]() {
-        q4_row_sums(acc);
-        if (n == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) part[wave][cur][4 * q + i] = acc[i];
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = 0.f;
+        acc = row_total(acc);  // row r over the 4 blocks (k-groups)
+        if (q == 0) part[wave][cur][r] = acc;
+        acc = 0.0f;
     };
     for (uint32_t i0 = 0; i0 < n_w; i0 += kGemvRing) {
 #pragma unroll
@@ -133,8 +136,9 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
                     flush();
                     cur = sl;
                 }
-                const Q4Tile w{make_uint4(rc[u].x, rc[u].y, rc[u].z, rc[u].w), make_uint2(rsc[u].x, rsc[u].y)};
-                q4_mfma_tile(w, cs.st, dig, tab, lane, acc);
+                const Q4Tile w{make_uint4(rc[u].x, rc[u].y, rc[u].z, rc[u].w), rsc[u]};
+                const v4i* ap = reinterpret_cast<const v4i*>(a_base + cs.st * a_step);
+                q4_mfma_tile(w, ap[0], ap[1], tab[cs.st * 4 + q], acc);
                 gemv_advance(cs, nst, T);
             }
             request(u, ld, i + kGemvRing < n_w);
@@ -160,7 +164,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
             }
             __syncthreads();
             int8_t* img = a.dig_out;
-            DigitTab* otab = reinterpret_cast<DigitTab*>(img + (size_t)(out_rows / 128 + (out_rows % 128 != 0)) * 512);
+            BlockTab* otab = reinterpret_cast<BlockTab*>(img + (size_t)(out_rows / 128 + (out_rows % 128 != 0)) * 512);
             for (uint32_t i = tid; i < nu / 2 * 4; i += blockDim.x) {  // quads: 8 rows each of a group's 32
                 const uint32_t jg = i >> 2, p = i & 3, blk = b + jg * G;
                 float v[8];
@@ -169,7 +173,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
                 float m, sum;
                 quad_stats(v, m, sum);
                 digits8(v, m, img, blk, p);
-                if (p == 0) digit_tab(otab, blk, m, sum);
+                if (p == 0) otab[blk] = block_tab(m, sum);
             }
             return;
         }
@@ -206,7 +210,7 @@ static hipError_t q4_launch3(Q4Args a, uint32_t out_rows, hipStream_t st) {
     const uint32_t units = (out_rows + 15) / 16;
     if (units == 0) return hipSuccess;
     a.slices = kGemvWaves;
-    const size_t lds = (IN == IN_EMBED ? (size_t)a.w.blocks * 32 * 4 : 0) + (size_t)a.w.nst * (512 + 128);
+    const size_t lds = (IN == IN_EMBED ? (size_t)a.w.blocks * 32 * 4 : 0) + (size_t)a.w.nst * kStepImg + 32;
     if constexpr (OUT == OUT_GELU) {
         if (a.dig_out) {  // a digit image of the output needs whole 32-row blocks per workgroup
             if (out_rows % 32) return hipErrorInvalidValue;

@@ -236,17 +236,6 @@ __device__ __forceinline__ float part_sum(const float* part, uint32_t k, uint32_
 }
 
 
-// Digit image of a GEMV input, nst * kStepImg bytes: the digit planes dig[b * 4 + t][32] of
-// block b (nst * 512 bytes), then one entry per block: for x_j = s (q0 + q1 2^-7 + q2 2^-14 +
-// q3 2^-21), s = 2^(ilogb(max |x|) - 5), the scales s 2^-14 and s 2^-21 and -8 sum_j x_j.
-struct alignas(16) BlockTab {
-    float s14, s21, nbias, pad;
-};
-
-__device__ __forceinline__ BlockTab block_tab(float m, float sum) {
-    const float s = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
-    return BlockTab{ldexpf(s, -14), ldexpf(s, -21), -8.0f * sum, 0.0f};
-}
 
 
 // A streaming wave's weight records: a ring of kRing in registers, refilled from the wave's run
