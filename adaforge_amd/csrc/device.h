@@ -490,8 +490,12 @@ __device__ __forceinline__ void input_load(const InputStage& in, uint32_t K, uin
     }
 }
 
-// Finishes the prologue from the registers input_load filled: the LDS digit image of the
-// (normalised) input.  xs (K floats of LDS) is used by IN_EMBED only.  The caller syncs.
+// Finishes the prologue from the registers input_load filled: the LDS digit image of the input.
+// xs (K floats of LDS) is used by IN_EMBED only.  The caller syncs.  An input with an RMSNorm
+// (IN_NORM, IN_RESID, IN_EMBED), f32(t rn w_n) with rn = rms(t)^-1, is imaged as u = f32(t w_n),
+// and the kernel scales its row sums by rn (gemv_row_factor), so the image does not wait for the
+// block sum of squares of t; its wave sums are left in red[8, 16).  (The difference is the f32
+// rounding of each input element, about 2^-24 of it.)  red: 16 slots.
 template <int IN, int Q>
 __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t nst, InputRegs<IN, Q>& g, float* xs,
                              int8_t* dig, BlockTab* tab, double* red) {
@@ -535,7 +539,7 @@ __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t n
                     double sa = 0.0;
 #pragma unroll
                     for (int j = 0; j < Q; ++j) sa += sq4(g.x[j][0]) + sq4(g.x[j][1]);
-                    ra = inv_rms(block_sum_d(sa, red), K, in.eps_a);
+                    ra = inv_rms_fast(block_sum_once(sa, red), K, in.eps_a);
                 }
 #pragma unroll
                 for (int j = 0; j < Q; ++j) {
@@ -563,13 +567,14 @@ __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t n
                     }
                 }
             }
-            const double rn = inv_rms(block_sum_d(ss, red), K, in.eps_n);
+            ss = wave_sum(ss);
+            if ((tid & 63) == 0) red[8 + (tid >> 6)] = ss;
 #pragma unroll
             for (int j = 0; j < Q; ++j) {
                 float w[8];
                 oct_f(g.wn[j], w);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) v[j][k] = norm_apply(t[j][k], rn, w[k]);
+                for (int k = 0; k < 8; ++k) v[j][k] = __fmul_rn(t[j][k], w[k]);
             }
         }
 #pragma unroll
@@ -582,6 +587,18 @@ __device__ inline void input_digits(const InputStage& in, uint32_t K, uint32_t n
                 if (p == 0) tab[b] = block_tab(m, sum);
             }
         }
+    }
+}
+
+// The RMSNorm row factor rn of a GEMV whose input_digits left the wave sums of squares in
+// red[8, 16) (1 for an input without a norm); after a barrier that follows input_digits.
+template <int IN>
+__device__ __forceinline__ double gemv_row_factor(const double* red, uint32_t K, float eps) {
+    if constexpr (IN == IN_NORM || IN == IN_RESID || IN == IN_EMBED) {
+        const double ss = ((red[8] + red[9]) + (red[10] + red[11])) + ((red[12] + red[13]) + (red[14] + red[15]));
+        return inv_rms_fast(ss, K, eps);
+    } else {
+        return 1.0;
     }
 }
 

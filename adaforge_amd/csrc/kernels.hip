@@ -54,7 +54,7 @@ template <int T, int IN, int OUT, int Q, int UGS>
 __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_rows, uint32_t units) {
     constexpr uint32_t ugs = UGS;
     extern __shared__ __align__(16) uint8_t smem[];
-    __shared__ double red[8];
+    __shared__ double red[16];
     __shared__ float part[kGemvWaves][kGemvMaxUnits * T][16];
 
     if (a.state && a.state[ST_STOP]) return;
@@ -147,6 +147,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
     }
     if (n_w > 0) flush();
     __syncthreads();
+    const double rn = gemv_row_factor<IN>(red, K, a.in.eps_n);  // the input's deferred RMSNorm factor
 
     if constexpr (OUT == OUT_GELU) {
         if constexpr (UGS == 1) {  // the rows' GELU products, one per thread, then a digit block per 32-row group
@@ -158,7 +159,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
                     gs += part[w][j * T][r];
                     us += part[w][j * T + 1][r];
                 }
-                const float v = gelu_mul(gs, us);
+                const float v = gelu_mul((float)(rn * (double)gs), (float)(rn * (double)us));
                 act_l[i] = v;
                 a.y[unit_of(j) * 16 + r] = v;
             }
@@ -186,7 +187,7 @@ __global__ __launch_bounds__(512) void q4_gemv_kernel(Q4Args a, uint32_t out_row
         for (int k = 0; k < T; ++k) {
             float s = part[0][j * T + k][r];
             for (uint32_t w = 1; w < kGemvWaves; ++w) s += part[w][j * T + k][r];
-            v[k] = s;
+            v[k] = (float)(rn * (double)s);
         }
         if constexpr (OUT == OUT_GELU) a.y[row] = gelu_mul(v[0], v[T - 1]);
         else if constexpr (OUT == OUT_ADD) a.y[row] = __fadd_rn(v[0], a.add[row]);
