@@ -220,7 +220,7 @@ struct BatchIn {
 
 struct BatchGemm {
     Q4View w, w2;           // w2: the up matrix of a gate/up pair
-    const int8_t* img;      // digit image of T vectors of w.blocks blocks
+    const int8_t* img;      // input image of T vectors of w.blocks blocks (fp16 halves and scales)
     uint32_t T;
     float* y;               // y[t * y_stride + r], r < w.rows (gate/up: f32(gelu(gate)) * up)
     size_t y_stride;
@@ -252,7 +252,7 @@ constexpr uint32_t kBatchAttnChunks = 32;  // chunk partials per (token, head) a
 size_t batch_image_bytes(uint32_t blocks, uint32_t tokens);
 hipError_t launch_batch_attention(BatchAttn a, uint32_t head_width, hipStream_t s);
 size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bool gelu_pair);
-hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s);
+hipError_t launch_batch_input(const BatchIn& in, hipStream_t s);
 // Returns through parts the splits whose partials were left in a.part (0: y written).
 hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s, uint32_t* parts = nullptr);
 

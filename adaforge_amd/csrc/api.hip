@@ -480,7 +480,7 @@ int af_q4_gemm(const af_q4* m, const float* x, uint32_t tokens, float* y, void* 
     in.stride = in.K;
     in.x = x;
     in.img = g_scratch.batch_image.as<int8_t>();
-    HIP_OK(launch_batch_digits(in, s), "batched GEMV input digits");
+    HIP_OK(launch_batch_input(in, s), "batched GEMV input digits");
     BatchGemm g{};
     g.w = w;
     g.img = in.img;
@@ -1375,7 +1375,7 @@ struct af_session {
                     in.snap_stride = nl * H;
                 }
             }
-            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = launch_batch_input(in, stream)) != hipSuccess) return e;
             if ((e = batch_gemm(L.qkv, nullptr, T, QKVB.as<float>(), L.qkv.rows)) != hipSuccess) return e;
 
             AttnArgs aa{};
@@ -1425,7 +1425,7 @@ struct af_session {
             if ((e = launch_batch_attention(ba, L.width, stream)) != hipSuccess) return e;
 
             in = batch_in(BI_PLAIN, T, L.qn, ATTB.as<float>(), L.qn);
-            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = launch_batch_input(in, stream)) != hipSuccess) return e;
             uint32_t o_parts = 0;
             if ((e = batch_gemm(L.o, nullptr, T, PROJB.as<float>(), H, &o_parts)) != hipSuccess) return e;
 
@@ -1436,7 +1436,7 @@ struct af_session {
             in.w_n = L.ffn_norm.as<float>();
             in.eps_n = L.ffn_eps;
             in.x_out = HB.as<float>();
-            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = launch_batch_input(in, stream)) != hipSuccess) return e;
             uint32_t ff_parts = 0;
             if ((e = batch_gemm(L.gate, &L.up, T, ACTB.as<float>(), intermediate, &ff_parts)) != hipSuccess) return e;
 
@@ -1446,7 +1446,7 @@ struct af_session {
                 in.parts = ff_parts;
                 in.part_row = (size_t)(intermediate + 15) / 16 * 16;
             }
-            if ((e = launch_batch_digits(in, stream)) != hipSuccess) return e;
+            if ((e = launch_batch_input(in, stream)) != hipSuccess) return e;
             // the last layer's down output stays in DB for the caller
             if ((e = batch_gemm(L.down, nullptr, T, DB.as<float>(), H, l + 1 < nl ? &down_parts : nullptr)) !=
                 hipSuccess)
@@ -1463,7 +1463,7 @@ struct af_session {
         in.x_out = XB.as<float>();
         in.snap = snap + (nl - 1) * H;
         in.snap_stride = nl * H;
-        return launch_batch_digits(in, stream);
+        return launch_batch_input(in, stream);
     }
 
     // Positions [from, to) through the batched layers (K/V appended), in batches of `batch`.

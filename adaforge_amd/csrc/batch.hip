@@ -1,7 +1,7 @@
 // Batched prefill kernels for gfx950: up to kBatchMax prompt tokens through a layer with every
 // weight read once for the whole batch (crates/cuda-backend/src/batch.rs, kernels/ada/q4_batch.cu
-// in the reference).  A layer's batch is a chain of launches: the digit image of every token's GEMV
-// input (batch_digits_kernel, with the residual and RMSNorm prologues), the Q4_0 GEMM over all tokens
+// in the reference).  A layer's batch is a chain of launches: the input image of every token's GEMV
+// input (batch_input_kernel, with the residual and RMSNorm prologues), the Q4_0 GEMM over all tokens
 // (batch_gemm_kernel, then batch_reduce_kernel when the GEMM splits K across workgroups), and the
 // attention of all tokens (attention_kernel with one grid z-slice per token, after a pass that
 // appends every token's K and V).
@@ -34,7 +34,7 @@ uint32_t padded_tokens(uint32_t T) { return (T + 15) / 16 * 16; }
 struct GemmPlan {
     uint32_t R, S;
 };
-// The digit image is read by every workgroup of a K range, R row tiles at a time, so R sets its
+// The input image is read by every workgroup of a K range, R row tiles at a time, so R sets its
 // reuse: up to 8 tiles (4 of each matrix of a gate/up pair) while at least 32 row groups remain.
 GemmPlan gemm_plan(uint32_t rows, uint32_t blocks, bool pair) {
     const uint32_t tiles = (rows + 15) / 16, r_max = pair ? 4 : 8;
@@ -88,7 +88,7 @@ __device__ __forceinline__ void block_halves(const float (&v)[8], uint32_t b, ui
 // for memory once.
 // PS: x comes from in.parts split-K partial planes (NO == 1 only).
 template <int NO, bool PS>
-__global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
+__global__ __launch_bounds__(512) void batch_input_kernel(BatchIn in) {
     extern __shared__ __align__(16) float xs[];  // [K], BI_EMBED only
     __shared__ double red[8];
     const uint32_t t = blockIdx.x, tid = threadIdx.x, K = in.K, nb = K / 32, no = K / 8, Tp = gridDim.x;
@@ -229,7 +229,7 @@ __global__ __launch_bounds__(512) void batch_digits_kernel(BatchIn in) {
 // BI_PLAIN inputs without a norm: one thread per 8-element octet, grid (Tp, octets / 256).  PS: the
 // input is gelu(gate) * up from a gate/up pair's deferred split-K partials.
 template <bool PS>
-__global__ __launch_bounds__(256) void batch_plain_digits_kernel(BatchIn in) {
+__global__ __launch_bounds__(256) void batch_plain_input_kernel(BatchIn in) {
     const uint32_t t = blockIdx.x, o = blockIdx.y * 256 + threadIdx.x, nb = in.K / 32, Tp = gridDim.x;
     if (o >= nb * 4) return;  // whole quads: nb * 4 is a multiple of 4
     _Float16* hi = reinterpret_cast<_Float16*>(in.img);
@@ -702,7 +702,7 @@ size_t batch_gemm_part_bytes(uint32_t rows, uint32_t blocks, uint32_t tokens, bo
     return (size_t)p.S * (gelu_pair ? 2 : 1) * padded_tokens(tokens) * ((rows + 15) / 16 * 16) * 4;
 }
 
-hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
+hipError_t launch_batch_input(const BatchIn& in, hipStream_t s) {
     if (in.T == 0 || in.T > kBatchMax || in.K == 0 || in.K > 16384 || in.K % 32) return hipErrorInvalidValue;
     if (in.mode == BI_PLAIN && !in.w_n) {
         if (in.stride % 4 || reinterpret_cast<uintptr_t>(in.x) % 16) return hipErrorInvalidValue;
@@ -712,9 +712,9 @@ hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
             if (in.parts > kDeferPairParts || reinterpret_cast<uintptr_t>(in.part) % 16 || in.part_row % 4 ||
                 in.part_row < in.K)
                 return hipErrorInvalidValue;
-            hipLaunchKernelGGL(batch_plain_digits_kernel<true>, g, dim3(256), 0, s, in);
+            hipLaunchKernelGGL(batch_plain_input_kernel<true>, g, dim3(256), 0, s, in);
         } else {
-            hipLaunchKernelGGL(batch_plain_digits_kernel<false>, g, dim3(256), 0, s, in);
+            hipLaunchKernelGGL(batch_plain_input_kernel<false>, g, dim3(256), 0, s, in);
         }
     } else {
         // float4 access to x, res, x_out and the norm weights
@@ -728,13 +728,13 @@ hipError_t launch_batch_digits(const BatchIn& in, hipStream_t s) {
             if (in.mode != BI_RESID || octets > 512 || in.parts > kDeferParts || !a16(in.part) || in.part_row % 4 ||
                 in.part_row < in.K)
                 return hipErrorInvalidValue;
-            hipLaunchKernelGGL((batch_digits_kernel<1, true>), g, dim3(512), 0, s, in);
+            hipLaunchKernelGGL((batch_input_kernel<1, true>), g, dim3(512), 0, s, in);
         } else if (octets <= 512) {
-            hipLaunchKernelGGL((batch_digits_kernel<1, false>), g, dim3(512), lds, s, in);
+            hipLaunchKernelGGL((batch_input_kernel<1, false>), g, dim3(512), lds, s, in);
         } else if (octets <= 1024) {
-            hipLaunchKernelGGL((batch_digits_kernel<2, false>), g, dim3(512), lds, s, in);
+            hipLaunchKernelGGL((batch_input_kernel<2, false>), g, dim3(512), lds, s, in);
         } else {
-            hipLaunchKernelGGL((batch_digits_kernel<4, false>), g, dim3(512), lds, s, in);
+            hipLaunchKernelGGL((batch_input_kernel<4, false>), g, dim3(512), lds, s, in);
         }
     }
     return hipGetLastError();
