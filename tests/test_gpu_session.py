@@ -192,19 +192,27 @@ def test_multi_layer_model_teacher_forced_and_greedy_ids(v_norm, layer_scale, q_
     oracle.compare(head_reference(model, hidden), logits)
 
 
-def test_step_kernel_time_out_falls_back_to_per_operation_kernels():
+@pytest.mark.parametrize("segmented", [False, True])
+def test_step_kernel_time_out_falls_back_to_per_operation_kernels(segmented):
     """A step-kernel launch whose grid barrier times out (forced from the host: the barrier opening
     layer 1's down projection waits for one arrival more than the grid makes) does not poison the
     session: the failed step and the rest of the generation run again on the per-operation
     kernels, and ids, layer outputs and logits match the oracle.  Covers a failure during prefill
-    (the first launch is a prefill step) and the session's later calls."""
-    model = synth.tiny_model(layers=4, vocabulary=2048, window=3, name="fallback")
+    (the first launch is a prefill step) and the session's later calls.  segmented: a Gemma-4-shaped
+    model whose global layers 2 and 5 run on the per-operation kernels between step-kernel runs
+    [0, 2), [3, 5), [6, 7); the first run times out, and the later launches of the step return at
+    once."""
+    if segmented:
+        model = synth.gemma4_model(name="fallback-g4", layers=7, hidden=1024, intermediate=2048, local_q=(4, 2, 256),
+                                   global_q=(4, 1, 512), vocabulary=2048, window=3, global_every=3)
+    else:
+        model = synth.tiny_model(layers=4, vocabulary=2048, window=3, name="fallback")
     prompt = [int(i) for i in synth.prompt_ids(7, model.vocabulary, name="fallback.prompt")]
     stop = [model.vocabulary - 1]
     ref = oracle.Model(model, capacity=40)
     want, _, margins = ref.generate(prompt, stop, 10)
     ref.close()
-    kv_rows = model.layers[0].kv_heads * model.layers[0].head_width
+    kv_rows = max(L.kv_heads * L.head_width for L in model.layers)
     with open_with_env(model, 40, AF_STEP_FAIL_PHASE=9) as s:
         got = s.generate(prompt, stop, 10)
         assert got.ids == want, (got.ids, want, margins)
@@ -225,6 +233,11 @@ def test_step_kernel_time_out_falls_back_to_per_operation_kernels():
         want1, _, _ = ref.generate(prompt[:1], stop, 10)
         ref.close()
         assert got.ids == want1, (got.ids, want1)
+    # prefill one step per position: the first prefill step fails, its position is not advanced
+    # (the step ends in the position's advance, not in the head), and the prefill runs again there
+    with open_with_env(model, 40, AF_STEP_FAIL_PHASE=9, AF_PREFILL_BATCH=0) as s:
+        got = s.generate(prompt, stop, 10)
+        assert got.ids == want, (got.ids, want)
 
 
 def test_continuation_and_streaming_equal_one_generation():
