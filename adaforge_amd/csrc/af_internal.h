@@ -167,6 +167,11 @@ struct AttnArgs {
     size_t in_stride;        // batch: floats between the tokens' q / k / v rows
     size_t out_stride;       // batch: floats between the tokens' outputs
     float* q_out;            // ATT_APPEND: the normalised, rotated queries [tokens][q_heads][head_width]
+    // raw_parts > 0: the q / k / v rows are the split-K partials a batched GEMM left (its reduce
+    // deferred): element i of token z's rows (i counted from q_raw; k_raw and v_raw point into the
+    // same rows) is the sum, in split order, of raw_part[(k raw_tp + z) raw_prow + i], k < raw_parts
+    const float* raw_part;
+    uint32_t raw_parts, raw_prow, raw_tp;
 };
 
 enum AttnMode : int {

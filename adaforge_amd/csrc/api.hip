@@ -1376,7 +1376,8 @@ struct af_session {
                 }
             }
             if ((e = launch_batch_input(in, stream)) != hipSuccess) return e;
-            if ((e = batch_gemm(L.qkv, nullptr, T, QKVB.as<float>(), L.qkv.rows)) != hipSuccess) return e;
+            uint32_t qkv_parts = 0;  // the append pass sums qkv's partials when its reduce is deferred
+            if ((e = batch_gemm(L.qkv, nullptr, T, QKVB.as<float>(), L.qkv.rows, &qkv_parts)) != hipSuccess) return e;
 
             AttnArgs aa{};
             const float* qkv = QKVB.as<float>();
@@ -1407,6 +1408,12 @@ struct af_session {
             aa.group = L.q_heads / L.kv_heads;
             aa.mode = ATT_APPEND;
             aa.q_out = QB.as<float>();
+            if (qkv_parts) {
+                aa.raw_part = BGEMM.as<float>();
+                aa.raw_parts = qkv_parts;
+                aa.raw_prow = (L.qkv.rows + 15) / 16 * 16;
+                aa.raw_tp = (T + 15) / 16 * 16;
+            }
             if ((e = launch_attention(aa, aa.group, L.width, stream, T)) != hipSuccess) return e;
             BatchAttn ba{};
             ba.q = QB.as<float>();

@@ -551,7 +551,9 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
 // token), chunk softmax, and p-weighted values; chunk partials (acc, max, sum)
 // are merged by the last block of the KV head.
 
-template <int D, int G>
+// RP: the q / k / v rows come from split-K partials (AttnArgs::raw_parts), a separate instance so
+// that the decode path's code is unchanged by it.
+template <int D, int G, bool RP = false>
 __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     static_assert(D == 256 || D == 512, "one thread per channel");
     constexpr int NH = G + 2;     // this block's query heads, then the new key and value
@@ -599,10 +601,36 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     // UK tokens per lane group, rows past the chunk clamped to its last one (the new token's row is
     // read from LDS instead; its cache slot may be written meanwhile).
     float raw[NH];
+    if constexpr (RP) {
+        // the partial planes, eight at a time, each round's loads issued before its sums
+        size_t ro[NH];
 #pragma unroll
-    for (int h = 0; h < G; ++h) raw[h] = q_raw[(size_t)(qh0 + h) * D + tid];
-    raw[G] = has_new ? k_raw[(size_t)kvh * D + tid] : 0.0f;
-    raw[G + 1] = has_new ? v_raw[(size_t)kvh * D + tid] : 0.0f;
+        for (int h = 0; h < G; ++h) ro[h] = (size_t)(qh0 + h) * D + tid;
+        ro[G] = (size_t)(a.k_raw - a.q_raw) + (size_t)kvh * D + tid;
+        ro[G + 1] = (size_t)(a.v_raw - a.q_raw) + (size_t)kvh * D + tid;
+        const float* p = a.raw_part + (size_t)z * a.raw_prow;
+        const size_t plane = (size_t)a.raw_tp * a.raw_prow;
+#pragma unroll
+        for (int h = 0; h < NH; ++h) raw[h] = 0.0f;
+        for (uint32_t k0 = 0; k0 < a.raw_parts; k0 += 8) {
+            float pv[8][NH];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int h = 0; h < NH; ++h)
+                    pv[k][h] = k0 + k < a.raw_parts && h < nh ? p[(k0 + k) * plane + ro[h]] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+#pragma unroll
+                for (int h = 0; h < NH; ++h)
+                    if (k0 + k < a.raw_parts) raw[h] = k0 + k == 0 ? pv[k][h] : raw[h] + pv[k][h];
+        }
+    } else {
+#pragma unroll
+        for (int h = 0; h < G; ++h) raw[h] = q_raw[(size_t)(qh0 + h) * D + tid];
+        raw[G] = has_new ? k_raw[(size_t)kvh * D + tid] : 0.0f;
+        raw[G + 1] = has_new ? v_raw[(size_t)kvh * D + tid] : 0.0f;
+    }
     const float qnw = a.q_norm[tid], knw = has_new ? a.k_norm[tid] : 0.0f;
     const double ifreq = tid < D / 2 ? a.inv_freq[tid] : 0.0;
     __builtin_amdgcn_sched_barrier(0);
@@ -925,17 +953,34 @@ hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_wid
     const uint32_t G = attention_block_heads(group, head_width);
     if (a.group != group || group % G || tokens == 0) return hipErrorInvalidValue;
     const dim3 grid(a.mode == ATT_APPEND ? 1 : a.cmax, a.kv_heads * (group / G), tokens);
+    if (a.raw_parts && (a.mode != ATT_APPEND || !a.raw_part)) return hipErrorInvalidValue;
+    const bool rp = a.raw_parts != 0;
     if (head_width == 256) {
         switch (G) {
-            case 1: hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a); break;
-            case 2: hipLaunchKernelGGL((attention_kernel<256, 2>), grid, dim3(256), 0, s, a); break;
-            case 4: hipLaunchKernelGGL((attention_kernel<256, 4>), grid, dim3(256), 0, s, a); break;
+            case 1:
+                if (rp) hipLaunchKernelGGL((attention_kernel<256, 1, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a);
+                break;
+            case 2:
+                if (rp) hipLaunchKernelGGL((attention_kernel<256, 2, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((attention_kernel<256, 2>), grid, dim3(256), 0, s, a);
+                break;
+            case 4:
+                if (rp) hipLaunchKernelGGL((attention_kernel<256, 4, true>), grid, dim3(256), 0, s, a);
+                else hipLaunchKernelGGL((attention_kernel<256, 4>), grid, dim3(256), 0, s, a);
+                break;
             default: return hipErrorInvalidValue;
         }
     } else if (head_width == 512) {
         switch (G) {
-            case 1: hipLaunchKernelGGL((attention_kernel<512, 1>), grid, dim3(512), 0, s, a); break;
-            case 2: hipLaunchKernelGGL((attention_kernel<512, 2>), grid, dim3(512), 0, s, a); break;
+            case 1:
+                if (rp) hipLaunchKernelGGL((attention_kernel<512, 1, true>), grid, dim3(512), 0, s, a);
+                else hipLaunchKernelGGL((attention_kernel<512, 1>), grid, dim3(512), 0, s, a);
+                break;
+            case 2:
+                if (rp) hipLaunchKernelGGL((attention_kernel<512, 2, true>), grid, dim3(512), 0, s, a);
+                else hipLaunchKernelGGL((attention_kernel<512, 2>), grid, dim3(512), 0, s, a);
+                break;
             default: return hipErrorInvalidValue;
         }
     } else {
