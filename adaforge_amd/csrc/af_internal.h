@@ -315,6 +315,10 @@ struct StepArgs {
                                     // what the merge can hold in LDS: step_merge_chunks)
     uint32_t advance;               // 1: move ST_POS on at the end (a step without the head)
     uint32_t xs_off;                // LDS byte offset of the residual prologue's staging (step_xs_offset)
+    // LDS of an attention item (step_attn_layout): its "pre" part (RoPE frequencies, q/k norm
+    // weights and the chunk's cached K/V rows, copied while the qkv phase runs) at attn_pre_off, clear
+    // of the qkv phase's LDS; chunks of at most stage_clen tokens are staged there.
+    uint32_t attn_pre_off, stage_clen;
     float* snap;                    // optional: layer outputs [n_layers][hidden] (the last by the head)
     uint64_t* clock;                // optional: [phases][kStepMarks][grid] timestamps (100 MHz), one
                                     // phase per barrier interval (see StepMark)
@@ -395,6 +399,9 @@ __host__ __device__ inline uint32_t step_wave_records(uint32_t units, uint32_t T
 __host__ __device__ constexpr uint32_t step_part_stride(uint32_t group) { return (group * (256u + 2u) + 3u) & ~3u; }
 
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group);
+// Where an attention item's "pre" LDS part goes and how many tokens a chunk stages there.
+void step_attn_layout(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group, uint32_t* pre_off,
+                      uint32_t* stage_clen);
 uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim);
 uint32_t step_merge_chunks(uint32_t group, size_t lds);  // chunk partials one merge holds in LDS
 hipError_t step_max_grid(uint32_t group, size_t lds, uint32_t* grid);

@@ -911,6 +911,7 @@ struct af_session {
     uint32_t fail_phase = ~0u;  // AF_STEP_FAIL_PHASE: a step-kernel barrier that times out (tests)
     bool xcd_local = false;     // the step kernel's XCD-local layout (setup_step)
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
+    uint32_t step_attn_pre = 0, step_stage_clen = 0;  // an attention item's LDS (step_attn_layout)
     size_t step_lds = 0;
     // The step kernel takes runs of consecutive layers, one launch per run: a single run of every
     // layer, or, when some layers are outside its limits (Gemma 4's 512-wide global layers), the
@@ -1136,6 +1137,8 @@ struct af_session {
         a.stream_off = STREAM_RUNS.as<uint64_t>() + (size_t)k * step_grid * kStepStreamWaves * 2;
         a.cmax = step_cmax;
         a.xs_off = step_xs_offset(hidden, intermediate, step_q);
+        a.attn_pre_off = step_attn_pre;
+        a.stage_clen = step_stage_clen;
         a.advance = advance ? 1u : 0u;
         a.snap = snap;
         a.fail_phase = k == 0 ? fail_phase : ~0u;
@@ -1555,6 +1558,7 @@ int setup_step(af_session& s) {
     }
     s.step_grid = grid;
     s.step_cmax = cm;
+    step_attn_layout(s.hidden, s.intermediate, step_q, group, &s.step_attn_pre, &s.step_stage_clen);
     s.group = group;
     s.step_lds = lds;
     s.step_q = step_q;

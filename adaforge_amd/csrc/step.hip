@@ -265,18 +265,23 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ring_rsrc(const Ring& r) {
 }
 
 // Records a streaming wave of a workgroup without an attention item pulls through the caches during
-// the attention phase: those after its ring, i.e. the rest of o-proj and most of gate/up.  The
-// copies land in a 1 KB LDS slot that nothing reads (a DMA needs an LDS destination and no
-// registers); what matters is that the bytes then sit in L2 and the Infinity Cache, so the wave's
-// own ring loads of them later return at cache latency while HBM would otherwise idle.
+// the attention phase: those after its ring, i.e. the rest of o-proj, gate/up and the first of down.
+// One 4-byte DMA per 128-byte line into a dword of an LDS slot that nothing reads (a DMA needs an
+// LDS destination and no registers): the miss fetches the whole line into L2 and the Infinity
+// Cache, so the wave's own ring loads of it later return at cache latency, while HBM would
+// otherwise idle; moving every byte to the CU instead (1 KB per instruction) cost 32 times the
+// cache-to-CU traffic and 8 times the instructions for the same gain.
 constexpr uint32_t kPrefetchRecords = 32;
+constexpr uint32_t kPrefetchLine = 128;
 static_assert((kRing + kPrefetchRecords) * kStepRecord <= kStepStreamPad, "stream padding below the prefetch");
 
 __device__ __forceinline__ void prefetch_records(const Ring& r, uint8_t* sink, uint32_t lane) {
     const uint64_t base = ((uint64_t)r.base_hi << 32) | r.base_lo;
     const uint8_t* src = reinterpret_cast<const uint8_t*>(base) + r.soff;
-    for (uint32_t i = 0; i < kPrefetchRecords * kStepRecord; i += 1024)
-        __builtin_amdgcn_global_load_lds(src + i + lane * 16, (lds_ptr)sink, 16, 0, 0);
+    constexpr uint32_t kBytes = kPrefetchRecords * kStepRecord;
+    for (uint32_t i = 0; i < kBytes; i += 64 * kPrefetchLine)
+        if (i + lane * kPrefetchLine < kBytes)  // inside the window the padding covers
+            __builtin_amdgcn_global_load_lds(src + i + lane * kPrefetchLine, (lds_ptr)sink, 4, 0, 0);
 }
 
 __device__ __forceinline__ void ring_fill(Ring& r, const __amdgpu_buffer_rsrc_t& rs, int u, uint32_t lane) {
@@ -385,7 +390,7 @@ __device__ __forceinline__ void consume_one(Ring& r, const __amdgpu_buffer_rsrc_
     const uint32_t s1 = c.st + c.dst, s2 = s1 - c.nst;
     const bool wrap = s1 >= c.nst;
     const bool last = wrap || c.end0;  // the run's last record (the phase's last: see consume_phase)
-    const uint32_t pa = la.a0 + c.st * la.am;
+    const uint32_t pa = la.a0 + __umul24(c.st, la.am);  // full-rate 24-bit multiply (st < 2^24, am <= 512)
     const v4i a0 = lds_at<v4i>(pa), a1 = lds_at<v4i>(pa + 16);
     const v4f tb = lds_at<v4f>(la.t0 + c.st * 64);  // BlockTab: s14, s21, nbias
     const v4i zero4 = {0, 0, 0, 0};
@@ -708,17 +713,19 @@ __device__ __forceinline__ void quad_digits_store_tagged(const float (&v)[8], ui
 
 // Work item (KV head h, chunk c) of the visible range runs with all 512 threads; the last chunk
 // of a head to finish merges the head's partials and writes the digit image of its query heads'
-// outputs for the o-proj GEMV.  Chunks of at most stage_clen tokens have their cached K and V
-// rows staged in LDS before the attention phase opens.
+// outputs for the o-proj GEMV.  Chunks of at most StepArgs::stage_clen tokens have their cached K
+// and V rows staged in LDS before the attention phase opens.
 template <int GQ>
-constexpr uint32_t stage_clen() {
+constexpr uint32_t stage_clen_max() {
     return GQ == 4 ? 32u : 64u;
 }
 
 // LDS of an attention item.  The "pre" part (RoPE angles, q/k norm weights, staged K/V rows) is
-// written by wave 0 while the qkv phase streams its weights, so it lies above that phase's
-// digit image; the "transient" part is written after the phase opens.  The merge reuses the space
-// from offset 0: the head's chunk partials, then the merged outputs.
+// written by the streaming waves once they have consumed their qkv records, while wave 0 finishes
+// the qkv phase, so it lies clear of everything the qkv phase touches (step_attn_layout: above its
+// digit image and clear of the residual it still reads); the "transient" part is written after the
+// phase opens, from offset 0.  The merge reuses the space from offset 0: the head's chunk partials,
+// then the merged outputs.
 template <int GQ>
 struct AttnLds {
     static constexpr int D = 256, NH = GQ + 2;
@@ -741,9 +748,8 @@ struct AttnLds {
     static constexpr size_t transient_bytes() {
         return 4 * (NH * D + GQ * D + GQ * kStepMaxClen + 16 * GQ * D) + 8 * 8 * NH + 4 * 8 + 2 * 2 * D;
     }
-    static constexpr size_t pre_offset() { return (transient_bytes() + 255) / 256 * 256; }
-    static constexpr size_t bytes() { return pre_offset() + 8 * 384 + 4 * 2 * D + 2 * 2 * stage_clen<GQ>() * D; }
-    __device__ explicit AttnLds(uint8_t* lds) {
+    static constexpr size_t pre_bytes(uint32_t sclen) { return 8 * 384 + 4 * 2 * D + 2 * 2 * (size_t)sclen * D; }
+    __device__ AttnLds(uint8_t* lds, uint32_t pre_off, uint32_t sclen) {
         nrm = reinterpret_cast<float*>(lds);
         qs = nrm + NH * D;
         scores = qs + GQ * D;
@@ -752,29 +758,33 @@ struct AttnLds {
         fred = reinterpret_cast<float*>(dred + 8 * NH);
         knew = reinterpret_cast<uint16_t*>(fred + 8);
         vnew = knew + D;
-        rope = reinterpret_cast<double*>(lds + pre_offset());
+        rope = reinterpret_cast<double*>(lds + pre_off);
         ifreq = rope + 256;
         qnw = reinterpret_cast<float*>(ifreq + 128);
         knw = qnw + D;
         kst = reinterpret_cast<uint16_t*>(knw + D);
-        vst = kst + stage_clen<GQ>() * D;
+        vst = kst + (size_t)sclen * D;
     }
 };
 
-// Wave 0, while the qkv phase streams (nothing here depends on this step's q, k, v): the RoPE
-// inverse frequencies, the q/k norm weights and the chunk's cached K and V rows, copied into
-// the "pre" LDS part.  The copies are waited for with wave 0's next wait (in its qkv epilogue).
+// Streaming wave i of n, once it has consumed its qkv records (nothing here depends on this step's
+// q, k, v): its share of the RoPE inverse frequencies, the q/k norm weights and the chunk's cached
+// K and V rows (two rows per copy instruction, pairs i, i + n, ..), copied into the "pre" LDS
+// part.  Issued here rather than by wave 0 during the qkv phase: the copies queue behind the weight
+// ring's loads, and wave 0 would wait for them before storing the qkv outputs the attention items
+// need.  The caller waits for the copies before the attention phase.
 template <int GQ>
-__device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t h, uint32_t c, uint32_t clen,
-                                              uint32_t start, uint8_t* lds, uint32_t lane) {
-    AttnLds<GQ> m(lds);
+__device__ __forceinline__ void attention_pre(CLayer& L, const StepArgs& a, uint32_t pos, uint32_t h, uint32_t c,
+                                              uint32_t clen, uint32_t start, uint8_t* lds, uint32_t i, uint32_t n,
+                                              uint32_t lane) {
+    AttnLds<GQ> m(lds, a.attn_pre_off, a.stage_clen);
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
-    dma(L.inv_freq, 8 * 128, reinterpret_cast<uint8_t*>(m.ifreq), lane);
-    dma(L.q_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.qnw), lane);
-    dma(L.k_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.knw), lane);
-    if (clen <= stage_clen<GQ>()) {
+    if (i == 0) dma(L.inv_freq, 8 * 128, reinterpret_cast<uint8_t*>(m.ifreq), lane);
+    if (i == 1 % n) dma(L.q_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.qnw), lane);
+    if (i == 2 % n) dma(L.k_norm, 4 * 256, reinterpret_cast<uint8_t*>(m.knw), lane);
+    if (clen <= a.stage_clen) {
         const uint32_t old_end = min(t1, pos);  // the new token's row is computed in the phase
-        for (uint32_t t = t0; t < old_end; t += 2) {  // two 512-byte rows per wave instruction
+        for (uint32_t t = t0 + 2 * i; t < old_end; t += 2 * n) {  // two 512-byte rows per wave instruction
             const uint32_t row = t + (lane >> 5);
             if (row < old_end) {
                 const size_t src = ((size_t)h * L.ring + row % L.ring) * 256 + (lane & 31) * 8;
@@ -782,6 +792,22 @@ __device__ __forceinline__ void attention_pre(CLayer& L, uint32_t pos, uint32_t 
                 __builtin_amdgcn_global_load_lds(L.vcache + src, (lds_ptr)(m.vst + (t - t0) * 256), 16, 0, 0);
             }
         }
+    }
+}
+
+// Streaming wave 1 (the one that copied the RoPE inverse frequencies in attention_pre), after its
+// copies are waited for: the RoPE angles of this position into the pre part.  The item reads them
+// after its first barrier, which the streaming waves reach only after this.
+template <int GQ>
+__device__ __forceinline__ void attention_rope(const StepArgs& a, uint32_t pos, uint8_t* lds, uint32_t lane) {
+    AttnLds<GQ> m(lds, a.attn_pre_off, a.stage_clen);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const uint32_t f = lane + 64 * i;
+        double sn, cs;
+        sincos((double)pos * m.ifreq[f], &sn, &cs);
+        m.rope[f] = cs;
+        m.rope[128 + f] = sn;
     }
 }
 
@@ -800,7 +826,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     constexpr int kPol = XL ? kNT : kSC1;
     constexpr int kSt = XL ? kSC0 : kSC1;  // stores: into the XCD's L2, or through to the memory side
     constexpr int kScope = XL ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
-    AttnLds<GQ> sh(lds);
+    AttnLds<GQ> sh(lds, a.attn_pre_off, a.stage_clen);
     float* nrm = sh.nrm;
     float* qs = sh.qs;
     float* scores = sh.scores;
@@ -812,7 +838,7 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen), n = t1 - t0;
     const uint32_t ring = L.ring;
     const bool append = t1 == pos + 1;
-    const bool staged = clen <= stage_clen<GQ>();
+    const bool staged = clen <= a.stage_clen;
     const int nh = append ? NH : GQ;  // heads normalised here: the queries, and k, v of the new token
 
     // This token's query heads (and k, v when the chunk ends at it), computed by the qkv phase and
@@ -838,17 +864,6 @@ __device__ __forceinline__ void attention_item(CLayer& L, const StepArgs& a, uin
             for (int j = 0; j < J; ++j)
                 if (need >> j & 1)
                     __builtin_amdgcn_global_load_lds(src(j), (lds_ptr)(stg + j * 1024), 16, 0, kPol);
-            if (spins == 0) {
-                // the RoPE angles of this position, while the first copies are in flight
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    const uint32_t f = lane + 64 * i;
-                    double sn, cs;
-                    sincos((double)pos * sh.ifreq[f], &sn, &cs);
-                    sh.rope[f] = cs;
-                    sh.rope[128 + f] = sn;
-                }
-            }
             wait_vm();
 #pragma unroll
             for (int j = 0; j < J; ++j) {
@@ -1263,32 +1278,37 @@ __device__ __forceinline__ bool attn_item(const AttnGeo& ag, uint32_t& h, uint32
 
 }  // namespace
 
-// Wave 0: copies for phase ph that do not depend on the phase before it (norm weights of a
-// residual prologue, or the attention item's RoPE frequencies, norm weights and cached K/V
-// rows).  Issued only: the caller waits (wave 0 waits for everything at the end of its epilogue).
+// Wave 0: copies for phase ph that do not depend on the phase before it (the norm weights of a
+// residual prologue; an attention item's copies are the streaming waves', norms_pre_part).  Issued
+// only: the caller waits (wave 0 waits for everything at the end of its epilogue).
 template <int GQ, bool XL>
 __device__ __forceinline__ void phase_pre(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t pos, uint8_t* lds,
                                           uint32_t lane) {
     if (ph >= n_phases) return;
     const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
-    if (kind == P_ATTN) {
-        CLayer& L = layer_at(a, l);
-        const AttnGeo ag = attn_geo(L, pos, a.cmax);
-        uint32_t h, c;
-        if (attn_item<XL>(ag, h, c)) attention_pre<GQ>(L, pos, h, c, ag.clen, ag.start, lds, lane);
-    } else if (kind == P_QKV || kind == P_GATEUP) {
+    if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
         preload_norms(d.in_kind, d.in, d.K, a.xs_off, lds, lane);
     }
 }
 
-// The residual and norm weights of GEMV phase ph (qkv, gate/up), copied by the streaming waves once
-// their records are consumed: waves 1-7 each take every 7th KB.  Returns false for other phases (left to
-// phase_pre on wave 0).
-__device__ __forceinline__ bool norms_pre_part(const StepArgs& a, int32_t ph, int32_t n_phases, uint8_t* lds,
-                                               uint32_t wave, uint32_t lane) {
+// The copies for phase ph by the streaming waves once their records are consumed: the residual and
+// norm weights of a GEMV phase (qkv, gate/up; waves 1-7 each take every 7th KB), or the attention
+// item's pre part (attention_pre; the attention phase's pre part always lies clear of the qkv
+// phase's LDS, step_attn_layout).  Returns false for other phases (left to phase_pre on wave 0).
+template <int GQ, bool XL>
+__device__ __forceinline__ bool norms_pre_part(const StepArgs& a, int32_t ph, int32_t n_phases, uint32_t pos,
+                                               uint8_t* lds, uint32_t wave, uint32_t lane) {
     if (ph >= n_phases) return false;
     const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
+    if (kind == P_ATTN) {
+        CLayer& L = layer_at(a, l);
+        const AttnGeo ag = attn_geo(L, pos, a.cmax);
+        uint32_t h, c;
+        if (attn_item<XL>(ag, h, c))
+            attention_pre<GQ>(L, a, pos, h, c, ag.clen, ag.start, lds, wave - 1, kStreamWaves, lane);
+        return true;
+    }
     if (kind != P_QKV && kind != P_GATEUP) return false;
     const Gemv d = describe(a, l, kind);
     float* xs = reinterpret_cast<float*>(lds + a.xs_off);
@@ -1304,7 +1324,7 @@ template <int GQ>
 __device__ __forceinline__ size_t phase_pre_low(const StepArgs& a, int32_t ph, int32_t n_phases) {
     if (ph >= n_phases) return ~(size_t)0;
     const uint32_t l = (uint32_t)ph / kPhases, kind = (uint32_t)ph % kPhases;
-    if (kind == P_ATTN) return AttnLds<GQ>::pre_offset();
+    if (kind == P_ATTN) return a.attn_pre_off;
     if (kind == P_QKV || kind == P_GATEUP) {
         const Gemv d = describe(a, l, kind);
         return (size_t)a.xs_off + (size_t)4 * d.K;  // from the residual's slot
@@ -1417,8 +1437,14 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 // waited for here, so that no LDS copy is pending at the loop's back edge: the
                 // compiler would otherwise wait for every load in flight (this wave's weight ring
                 // included) before the next phase's first LDS read
-                if (pre_now) norms_pre_part(a, ph + 1, n_phases, lds, wave, lane);
+                if (pre_now || kind == P_QKV) norms_pre_part<GQ, XL>(a, ph + 1, n_phases, pos, lds, wave, lane);
                 wait_vm();
+                if (wave == 1 && kind == P_QKV && ph + 1 < n_phases) {  // next: this layer's attention
+                    CLayer& L = layer_at(a, l);
+                    const AttnGeo ag = attn_geo(L, pos, a.cmax);
+                    uint32_t h, c;
+                    if (attn_item<XL>(ag, h, c)) attention_rope<GQ>(a, pos, lds, lane);
+                }
                 if (wave == 1) stamp_at(g, g.p, M_CONSUMED);
             } else {
                 // waited for before the outputs are stored: a phase that reads the residual may be
@@ -1427,8 +1453,6 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                     store_residual(d.in, lds, d.K, a.xs_off, lane);
                     wait_vm();
                 }
-                if (pre_now && (ph + 1 >= n_phases || (uint32_t)(ph + 1) % kPhases == P_ATTN))
-                    phase_pre<GQ, XL>(a, ph + 1, n_phases, pos, lds, lane);
                 stamp(g, M_PRE);
                 // the streaming waves with records (wave - 1 < fe) have left their partials in part
                 const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
@@ -1553,11 +1577,41 @@ uint32_t step_xs_offset(uint32_t hidden, uint32_t inter, uint32_t q_dim) {
     return (std::max(nst * kStepImg, o_img + o_stage) + 15) / 16 * 16;  // the largest digit image of any GEMV phase
 }
 
+// An attention item's LDS.  Its transient part lies at offset 0 (fixed: with a run-time offset the
+// compiler cannot keep its addresses apart from the pre part's, and the item ran 0.6 us slower).
+// Its pre part is copied while the qkv phase still reads its digit image [0, img) and (workgroup
+// 0, store_residual) the residual at [xs, xs + 4 hidden): it goes above the transient part and clear
+// of the residual, with as many staged tokens (up to stage_clen_max) as the LDS budget leaves.
+// Config 4: pre part at 84480 (above the residual), 64 tokens, 155136 bytes.  Returns the dynamic
+// LDS bytes the launch needs.
+constexpr size_t kStepLdsBudget = 160 * 1024 - 8 * 1024;  // the CU's LDS less the kernel's static LDS
+
+template <int GQ>
+static size_t attn_layout(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t* pre_off, uint32_t* sclen) {
+    const size_t xs = step_xs_offset(hidden, inter, q_dim);
+    const size_t xs_end = xs + (size_t)4 * hidden * 4;  // x, res, two norm weight vectors
+    const size_t res_end = xs + (size_t)4 * hidden;
+    const size_t fixed = AttnLds<GQ>::pre_bytes(0), row = AttnLds<GQ>::pre_bytes(1) - fixed;
+    size_t p = (AttnLds<GQ>::transient_bytes() + 255) / 256 * 256;
+    if (p < res_end && p + AttnLds<GQ>::pre_bytes(stage_clen_max<GQ>()) > xs) p = (res_end + 255) / 256 * 256;
+    const size_t fit = kStepLdsBudget > p + fixed ? (kStepLdsBudget - p - fixed) / row : 0;
+    *pre_off = (uint32_t)p;
+    *sclen = (uint32_t)std::min<size_t>(stage_clen_max<GQ>(), fit);
+    return std::max(xs_end, p + AttnLds<GQ>::pre_bytes(*sclen));
+}
+
+void step_attn_layout(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group, uint32_t* pre_off,
+                      uint32_t* stage_clen) {
+    if (group == 1) (void)attn_layout<1>(hidden, inter, q_dim, pre_off, stage_clen);
+    else if (group == 2) (void)attn_layout<2>(hidden, inter, q_dim, pre_off, stage_clen);
+    else (void)attn_layout<4>(hidden, inter, q_dim, pre_off, stage_clen);
+}
+
 size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t group) {
-    // images, then the staging of a residual prologue (x, res, two norm weight vectors)
-    const size_t g = step_xs_offset(hidden, inter, q_dim) + (size_t)4 * hidden * 4;
-    const size_t att = group == 1 ? AttnLds<1>::bytes() : group == 2 ? AttnLds<2>::bytes() : AttnLds<4>::bytes();
-    return std::max(g, att);
+    uint32_t pre_off = 0, sclen = 0;
+    return group == 1   ? attn_layout<1>(hidden, inter, q_dim, &pre_off, &sclen)
+           : group == 2 ? attn_layout<2>(hidden, inter, q_dim, &pre_off, &sclen)
+                        : attn_layout<4>(hidden, inter, q_dim, &pre_off, &sclen);
 }
 
 // A plain launch: the grid is the occupancy API's co-resident maximum (step_max_grid, one
