@@ -131,6 +131,31 @@ def test_batched_trace_gemma4_width_512_shared_v():
     print(f"gemma4 batched: layer ratio {ratio:.3f}, K/V ratio {ulps:.3f}, {differ} fp16 values differ", flush=True)
 
 
+@pytest.mark.parametrize("width", [256, 512])
+def test_batched_trace_long_chunks_teacher_forced(width):
+    """The batched attention's chunks that span several key blocks (more than 2,048 keys at width 256,
+    1,024 at width 512: batch_attention_kernel's multi-block branch, which every prompt longer than
+    that takes in a batched prefill), traced 32 positions at a time through a global layer and checked
+    teacher-forced past those lengths."""
+    if width == 256:
+        model = synth.model(name="batch-long", layers=2, hidden=1024, intermediate=2048, q_heads=16, kv_heads=8,
+                            head_width=256, vocabulary=2048, window=0, global_every=1)
+        n, positions = 2200, [0, 1023, 1024, 2047, 2048, 2049, 2079, 2080, 2199]
+    else:
+        model = synth.gemma4_model(name="batch-long512", layers=2, hidden=1024, intermediate=2048,
+                                   local_q=(16, 8, 256), global_q=(16, 1, 512), vocabulary=2048, window=16,
+                                   global_every=2)
+        n, positions = 1100, [0, 511, 512, 1023, 1024, 1025, 1055, 1056, 1099]
+    ids = [int(i) for i in synth.prompt_ids(n, model.vocabulary, name=f"batch-long{width}.ids")]
+    kv_rows = max(L.kv_heads * L.head_width for L in model.layers)
+    with open_with_env(model, n + 8, AF_TRACE_BATCH=32) as s:
+        outputs, kv, _, _ = s.trace(ids, kv_rows=kv_rows, logits=False, hidden=False)
+    ratio, ulps, differ = oracle.check_layer_stack(model, ids, outputs, kv, threads=THREADS, positions=positions)
+    print(f"batched long trace width {width} n={n}: layer ratio {ratio:.3f}, K/V ratio {ulps:.3f}, "
+          f"{differ} fp16 values differ", flush=True)
+    assert np.isfinite(outputs).all()
+
+
 def test_batched_prefill_generation_matches_oracle_and_resumes():
     """Generation with the default batched prefill: greedy ids equal the oracle's for a 75-token prompt
     (three batches, the local ring wrapping), then a follow-up turn on the cached prefix (its pending

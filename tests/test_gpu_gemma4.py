@@ -138,7 +138,9 @@ def test_softcap_matches_reference_and_rejects_invalid_cap():
 def test_session_from_gguf_file_equals_session_from_memory(tmp_path):
     """The same Gemma 4 model stored as a GGUF file (tests/gguf_writer.py) and opened with
     af_gguf_session_open (the reference's layer assembly from file metadata) decodes exactly like the
-    session built from the weights in memory: identical greedy ids and identical raw logits."""
+    session built from the weights in memory (identical greedy ids and raw logits), and is checked
+    against the CPU oracle on its own: every layer output teacher-forced, the logits of its final
+    hidden state, and its greedy ids equal to the oracle's."""
     from adaforge_amd.gguf import GgufInspector
     from tests import gguf_writer
 
@@ -147,6 +149,7 @@ def test_session_from_gguf_file_equals_session_from_memory(tmp_path):
     path.write_bytes(gguf_writer.gemma4_gguf(model))
     prompt = [int(i) for i in synth.prompt_ids(20, model.vocabulary, name="gemma4-gguf.prompt")]
     stop = [model.vocabulary - 1]
+    kv_rows = max(L.kv_heads * L.head_width for L in model.layers)
     with HipDiagnostics().open_session(model, 64) as mem:
         want = mem.generate(prompt, stop, 8)
         mem.reset()
@@ -154,6 +157,14 @@ def test_session_from_gguf_file_equals_session_from_memory(tmp_path):
     with GgufInspector().open_session(str(path), 64) as s:
         got = s.generate(prompt, stop, 8)
         s.reset()
-        _, _, got_logits, _ = s.trace(prompt, layer_outputs=False)
+        outputs, kv, got_logits, hidden = s.trace(prompt, kv_rows=kv_rows)
     assert got.ids == want.ids
     assert np.array_equal(got_logits, want_logits)
+    ratio, ulps, differ = oracle.check_layer_stack(model, prompt, outputs, kv, threads=THREADS)
+    print(f"gguf session: layer max ratio {ratio:.3f}, K/V ratio {ulps:.3f}, {differ} fp16 values differ", flush=True)
+    nrm = oracle.rmsnorm(model.final_norm, model.final_eps, hidden).astype(np.float32)
+    oracle.compare(oracle.q6_matvec(model.table, model.hidden, model.vocabulary, nrm, threads=THREADS), got_logits)
+    ref = oracle.Model(model, capacity=64, threads=THREADS)
+    ref_ids, _, _ = ref.generate(prompt, stop, 8)
+    ref.close()
+    assert got.ids == ref_ids, (got.ids, ref_ids)

@@ -76,6 +76,25 @@ def test_step_kernel_long_trace_teacher_forced(q_heads, kv_heads, window, n):
     trace_and_check(model, n, name=f"step-{q_heads}x{kv_heads}")
 
 
+def test_step_kernel_trace_past_8192_positions_teacher_forced():
+    """The BASELINE attention geometry traced through the step kernel over 8,300 positions: the global
+    layer's 32 unstaged chunks of up to 260 tokens (and their merges) at contexts past 8,192, and the
+    local layer's ring after eight wraps, checked teacher-forced at positions there (the bench decodes
+    at contexts up to 7,628; the kernel accepts capacities up to 32,768)."""
+    model = long_model(16, 8, 1024, name="long8k")
+    n = 8300
+    ids = [int(i) for i in synth.prompt_ids(n, model.vocabulary, name="long8k.ids")]
+    kv_rows = model.layers[0].kv_heads * model.layers[0].head_width
+    with HipDiagnostics().open_session(model, n + 8) as s:
+        outputs, kv, _, _ = s.trace(ids, kv_rows=kv_rows, logits=False, hidden=False)
+        _, timings = s.profile(ids, 2)
+        assert timings["layers"][0] > 0, timings["layers"]  # the step kernel ran
+    positions = [0, 4095, 4096, 8191, 8192, 8193, 8223, 8224, 8299]
+    ratio, ulps, differ = oracle.check_layer_stack(model, ids, outputs, kv, threads=THREADS, positions=positions)
+    print(f"step-8k: layer max ratio {ratio:.3f}, K/V ratio {ulps:.3f}, {differ} fp16 values differ", flush=True)
+    assert np.isfinite(outputs).all()
+
+
 def test_per_operation_kernels_long_trace_teacher_forced():
     """The per-operation kernels (the fall-back path; split attention over up to 64 chunks of at
     least 32 tokens merged by the last block) on the BASELINE geometry past the window's wrap."""

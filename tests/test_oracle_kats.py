@@ -130,6 +130,21 @@ def test_q6_known_constant_row_and_softcap_q6_rs_203():
         oracle.softcap(float("nan"), 30.0)
 
 
+def test_softcap_mid_range_closed_form_q6_rs_66():
+    """softcap(x, cap) = tanh(x / cap) cap in f32 (crates/domain/src/q6.rs:66-71), away from 0 and from
+    saturation, where the reference's own KATs do not reach: against the closed form in double to a
+    few f32 ulps.  tanh(x) cap (30 tanh 30 = 30) and tanh(x cap) cap (30 tanh 900 = 30) both fail the
+    first case; a missing factor cap fails every one."""
+    for x, cap in [(30.0, 30.0), (-15.0, 30.0), (7.5, 50.0), (-29.0, 15.0), (0.25, 30.0)]:
+        want = cap * math.tanh(x / cap)
+        got = oracle.softcap(x, cap)
+        assert abs(got - want) <= 4 * float(np.spacing(np.float32(abs(want)))), (x, cap, got, want)
+    assert abs(oracle.softcap(30.0, 30.0) - 22.8478247) < 1e-5  # 30 tanh 1
+    assert abs(oracle.softcap(-15.0, 30.0) + 13.8635147) < 1e-5  # -30 tanh 0.5
+    assert oracle.softcap(-12.0, 30.0) == -oracle.softcap(12.0, 30.0)  # odd
+    assert oracle.softcap(1e-4, 30.0) == pytest.approx(1e-4, rel=1e-7)  # the identity near 0
+
+
 def _known_q6_block():
     """crates/domain/src/embedding.rs:261-277: code i % 64 packed, sub-scales i - 8, d = 0.5."""
     b = np.zeros(210, np.uint8)
