@@ -1952,7 +1952,7 @@ int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint
     };
     // A verification pass costs a few decode steps, so after a pass that accepts nothing the next
     // `skip` tokens are decoded without drafting (doubling on each further miss, reset by a hit);
-    // the ids are the same either way.
+    // the ids are the same either way, up to the rounding of the batched layers' predictions.
     uint32_t skip = 0, backoff = 0;
     while (ids.size() < max_new) {
         if (is_stop(next)) {

@@ -249,7 +249,10 @@ int af_session_open(const af_layer_weights* layers, uint32_t n_layers, const af_
  * pass, default 32; 0 or 1: one decode step per position, as ADAFORGE_BATCH_PREFILL=0,
  * stack.rs:982-987); AF_SPECULATIVE=1 with AF_SPEC_DEPTH (default 11, at most 15): greedy
  * speculative decoding with prompt-lookup drafts verified in one batched pass (ADAFORGE_SPECULATIVE,
- * ADAFORGE_SPEC_DEPTH, stack.rs:1252-1338, 1485-1511); the ids are the greedy ids either way. */
+ * ADAFORGE_SPEC_DEPTH, stack.rs:1252-1338, 1485-1511).  A verification pass predicts each position
+ * from the batched layers, which sum in another order than the decode step (the reference's batched
+ * path is bit-identical to its own sequential one, stack.rs:1063-1064): the ids equal plain greedy
+ * decoding's up to rounding, so they can differ where the top two logits of a step nearly tie. */
 int af_session_generate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop,
                         size_t n_stop, uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out,
                         size_t* n_out, int32_t* stopped, af_generation_stats* stats);

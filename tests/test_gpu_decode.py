@@ -76,6 +76,37 @@ def test_config4_greedy_ids_match_oracle_golden(golden, model, session):
     assert got[:n] == want[:n], next(i for i in range(n) if got[i] != want[i])
 
 
+def test_config4_speculative_ids_match_golden(golden, model):
+    """Greedy speculative decoding (AF_SPECULATIVE=1, stack.rs:1252-1338) on config 4's golden prompt:
+    each verification pass runs the token and its prompt-lookup draft through the batched layers, whose
+    sums run in another order than the step kernel's, so its ids equal plain greedy decoding's up to
+    rounding, not bit for bit; at this model's top-2 margins (the golden run's smallest over the compared
+    steps is printed) they are the golden ids.  The golden tail repeats itself, so drafts are found and
+    accepted."""
+    prompt, want = golden["prompt"], golden["tokens"]
+    stop = [unused_id(want, model.vocabulary)]
+    saved = os.environ.get("AF_SPECULATIVE")
+    os.environ["AF_SPECULATIVE"] = "1"
+    try:
+        s = HipDiagnostics().open_session(model, W.C4_PROMPT + W.C4_DECODE + 8)
+    finally:
+        if saved is None:
+            del os.environ["AF_SPECULATIVE"]
+        else:
+            os.environ["AF_SPECULATIVE"] = saved
+    with s:
+        first = s.generate(prompt, stop, 128)
+        second = s.generate(prompt + first.ids, stop, 128)
+        passes, drafted, accepted = s.speculation()
+    got = first.ids + second.ids
+    n = comparable(golden)
+    print(f"config4 speculative: {passes} verification passes, {accepted} of {drafted} drafted ids accepted; "
+          f"ids compared over {n} steps, smallest golden top-2 margin there {min(golden['margins'][:n]):.2e}",
+          flush=True)
+    assert got[:n] == want[:n], next(i for i in range(n) if got[i] != want[i])
+    assert passes > 0 and accepted > 0
+
+
 def test_config4_teacher_forced_argmax_and_top8_logits(golden, model, session):
     """Each golden id fed in turn (af_session_trace): the logits after it are the next step's."""
     session.reset()
