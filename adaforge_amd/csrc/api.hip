@@ -2033,6 +2033,9 @@ int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint
 
 // GenerationSession::generate (crates/cuda-backend/src/stack.rs:1171-1386).  With a timer the
 // decode steps are launched directly with an event pair around every kernel (no stop ids).
+// Decode steps queued on the stream ahead of the one whose id is being read back.
+constexpr uint32_t kDecodeAhead = 8;
+
 int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop, size_t n_stop,
                   uint32_t max_new, af_token_fn on_token, void* user, uint32_t* ids_out, size_t* n_out,
                   int32_t* stopped_out, af_generation_stats* stats, KernelTimer* timer) {
@@ -2089,9 +2092,14 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
     HIP_OK(hipEventRecord(s->ev_start, st), "event");
     // Enqueue the decode steps from k0 on; each step's head writes its id and flags to mapped host
     // memory, and a stop id makes the remaining steps return at once.
-    auto enqueue_from = [&](uint32_t k0) -> int {
+    // Steps k0 .. k1 - 1 onto the stream.  At most kDecodeAhead steps are queued ahead of the one
+    // being read back: the GPU never waits for the host (a step takes milliseconds, a launch
+    // microseconds), and a call of many steps does not put thousands of kernel dispatches in flight
+    // at once (a 128-step call of a model whose decode graph holds 49 kernels would queue 6,272).
+    uint32_t queued = 0;
+    auto enqueue_range = [&](uint32_t k0, uint32_t k1) -> int {
         s->timer = timer;
-        for (uint32_t k = k0; k < max_new; ++k) {
+        for (uint32_t k = k0; k < k1; ++k) {
             s->host_pos = P - 1 + k;
             hipError_t e;
             if (k == 0 && pend == 0)
@@ -2107,14 +2115,16 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
             }
         }
         s->timer = nullptr;
+        queued = std::max(queued, k1);
         return AF_OK;
     };
-    if ((rc = enqueue_from(0))) return rc;
+    if ((rc = enqueue_range(0, std::min(max_new, kDecodeAhead)))) return rc;
     std::vector<uint32_t> ids;
     bool stopped = false, bad = false;
     double first_ms = 0, last_ms = 0;
     for (uint32_t k = 0; k < max_new; ++k) {
         HIP_OK(hipEventSynchronize(s->events[k]), "decode step");
+        if (queued < max_new && (rc = enqueue_range(queued, queued + 1))) return rc;
         const volatile StepRecord* vr = s->records + P + k;
         StepRecord r;
         r.id = vr->id;
@@ -2128,7 +2138,9 @@ int generate_core(af_session* s, const uint32_t* prompt, size_t n_prompt, const 
             bool timed_out = false;
             if ((rc = s->step_timed_out(timed_out, nullptr))) return rc;
             if (timed_out) {
-                if ((rc = s->fall_back()) || (rc = s->set_state(P - 1 + k, (uint32_t)n_stop)) || (rc = enqueue_from(k)))
+                queued = k;
+                if ((rc = s->fall_back()) || (rc = s->set_state(P - 1 + k, (uint32_t)n_stop)) ||
+                    (rc = enqueue_range(k, std::min(max_new, k + kDecodeAhead))))
                     return rc;
                 --k;
                 continue;
