@@ -299,15 +299,65 @@ def cpu_decode(model, prompt, tokens, threads):
 
 # ---- the headline: config 4 -------------------------------------------------------------------------
 
+TRAFFIC_JSON = os.path.join(ROOT, "profiles", "traffic_config4.json")
+# the sources whose code the counted kernels run (a counter figure describes only the build it came from)
+TRAFFIC_SOURCES = ["adaforge_amd/csrc/step.hip", "adaforge_amd/csrc/kernels.hip", "adaforge_amd/csrc/device.h",
+                   "adaforge_amd/csrc/af_internal.h"]
+
+
+def source_hashes():
+    import hashlib
+    out = {}
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            out[rel] = hashlib.sha256(f.read()).hexdigest()[:16]
+    return out
+
+
 def measured_traffic(kernel="void af::decode_step_kernel<2, true>(af::StepArgs)"):
     """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE passes
-    (profiles/traffic_config4.json, calibrated against a copy of known size), or None."""
-    path = os.path.join(ROOT, "profiles", "traffic_config4.json")
+    (profiles/traffic_config4.json, calibrated against a copy of known size), or None when the file
+    is missing or was measured on other kernel sources than these (their hashes are stored in it)."""
     try:
-        with open(path) as f:
-            return json.load(f)["kernels"][kernel]["hbm_bytes"]
+        with open(TRAFFIC_JSON) as f:
+            t = json.load(f)
+        if t.get("sources") != source_hashes():
+            return None
+        return t["kernels"][kernel]["hbm_bytes"]
     except (OSError, KeyError, ValueError):
         return None
+
+
+def write_traffic(fetch_csv, write_csv, cal_fetch_csv, cal_write_csv, copy_bytes=1 << 28):
+    """profiles/traffic_config4.json from rocprofv3 --pmc runs (one counter per run): per kernel the mean
+    FETCH_SIZE and WRITE_SIZE per dispatch (KiB), each scaled by what the same counter reads for one
+    device-to-device copy of copy_bytes (the largest copy dispatch of the calibration runs), and the
+    hashes of the kernel sources measured."""
+    import csv
+
+    def per_kernel(path):
+        acc = {}
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                acc.setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+        return acc
+
+    cal_f = max(max(v) for k, v in per_kernel(cal_fetch_csv).items() if "copy" in k.lower())
+    cal_w = max(max(v) for k, v in per_kernel(cal_write_csv).items() if "copy" in k.lower())
+    ff, wf = copy_bytes / 1024.0 / cal_f, copy_bytes / 1024.0 / cal_w
+    fetch, write = per_kernel(fetch_csv), per_kernel(write_csv)
+    kernels = {}
+    for name in ("void af::decode_step_kernel<2, true>(af::StepArgs)", "void af::q6_head_kernel<2>(af::HeadArgs)"):
+        if name in fetch and name in write:
+            fk, wk = statistics.mean(fetch[name]), statistics.mean(write[name])
+            kernels[name] = {"dispatches": len(fetch[name]), "fetch_kib": round(fk, 1), "write_kib": round(wk, 1),
+                             "hbm_bytes": int(round((fk * ff + wk * wf) * 1024))}
+    out = {"calibration": {"copy_bytes": copy_bytes, "fetch_kib": round(cal_f, 1), "write_kib": round(cal_w, 1),
+                           "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+           "sources": source_hashes(), "kernels": kernels}
+    with open(TRAFFIC_JSON, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out, indent=1))
 
 
 def kv_read_bytes(model, tokens):
@@ -457,9 +507,14 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the configs 0-3 operator legs")
     ap.add_argument("--configs-only", action="store_true", help="only the configs 0-3 GPU legs (profiling)")
     ap.add_argument("--no-extras", action="store_true", help="skip the prefill and speculative-decoding legs")
+    ap.add_argument("--traffic", nargs=4, metavar=("FETCH_CSV", "WRITE_CSV", "CAL_FETCH_CSV", "CAL_WRITE_CSV"),
+                    help="write profiles/traffic_config4.json from rocprofv3 --pmc counter CSVs and exit")
     ap.add_argument("--legs", default="prefill,long,speculative,gemma4",
                     help="the extra legs to run (comma-separated subset of prefill, long, speculative, gemma4)")
     a = ap.parse_args()
+    if a.traffic:
+        write_traffic(*a.traffic)
+        return
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
               f"(--gpus {a.gpus} is not supported; DESIGN.md describes how the path would shard)", file=sys.stderr)
@@ -603,7 +658,8 @@ def main():
             "frac": round(achieved / PEAK_GBS, 4),
             "traffic": measured_traffic(),
             "traffic_source": "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per launch, calibrated on a 256 MiB copy "
-                              "(profiles/decode_step_kernel_config4.md)",
+                              "(profiles/decode_step_kernel_config4.md); null when the committed figures were "
+                              "measured on other kernel sources than this build's",
             "avg_us": round(1000.0 * avg_ms, 2),
             "bytes_per_launch": round(step_bytes),
             "launches": n,
