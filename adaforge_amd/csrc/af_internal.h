@@ -172,6 +172,10 @@ struct AttnArgs {
     // same rows) is the sum, in split order, of raw_part[(k raw_tp + z) raw_prow + i], k < raw_parts
     const float* raw_part;
     uint32_t raw_parts, raw_prow, raw_tp;
+    uint32_t tokens;         // set by launch_attention
+    // the blocks of a slot share an XCD's L2 (workgroups b and b + 8 of a launch run on one XCD,
+    // checked on this device by a probe launch): partials and tickets stay in that L2
+    uint32_t xcd_local;
 };
 
 enum AttnMode : int {
@@ -276,6 +280,7 @@ hipError_t launch_zero_words(uint32_t* p, uint32_t n, hipStream_t s);
 uint32_t head_grid(uint32_t rows);
 
 constexpr uint32_t kAttnMinChunk = 32;
+constexpr uint32_t kAttnShortChunks = 16;  // attention_kernel's short form: at most 16 chunks of 32
 // A query head's chunk partial in attention_kernel's split-K scratch: D sums, the chunk's max and
 // sum, padded so that every row starts on a 16-byte boundary.
 __host__ __device__ constexpr uint32_t attn_part_row(uint32_t D) { return D + 4; }
@@ -326,7 +331,7 @@ struct StepArgs {
                                     // many, so that it ends in the barrier's own time-out (a host-set
                                     // test of the fall-back path); ~0u: none
     uint32_t xcd_local;             // 1: head group h's qkv rows, attention items and chunk partials all
-                                    // live on XCD h (workgroups b with b % 8 == h) and are exchanged
+                                    // live on one XCD (workgroups b with b % 8 == h) and are exchanged
                                     // through that XCD's L2 (step_qkv_tile, step_attn_chunk)
     // Values handed over by launch layer l carry the tag epoch * tag_stride + 1 + tag_base + l (epoch:
     // state word ST_EPOCH, one more per launch; tag_base + n_layers <= tag_stride), so that no tag
@@ -339,7 +344,8 @@ struct StepArgs {
 };
 
 // XCD-local layout (StepArgs::xcd_local): eight KV heads of two query heads each, a 256-workgroup
-// grid whose workgroup b runs on XCD b % 8 (verified at session open by step_xcd_map).  Head group
+// grid whose workgroups b and b + 8 share an XCD (workgroup b on XCD (x0 + b) % 8, x0 varying from
+// launch to launch; verified at session open by step_xcd_map).  Head group
 // h = b % 8 owns 64 qkv tiles (its two query heads' 32, its K head's 16, its V head's 16), two per
 // workgroup of rank r = b / 8; its attention chunk c runs on workgroup 8 (31 - c) + h.
 constexpr uint32_t kXcds = 8;

@@ -115,6 +115,40 @@ int dev_upload(DevMem& m, const void* src, size_t bytes, const char* what) {
     return AF_OK;
 }
 
+// Whether this device dispatches the workgroups of a launch to its 8 XCDs in turn, so that
+// workgroups b and b + 8 share an XCD: the XCC_ID each workgroup of a 4096-workgroup probe launch
+// reads is (XCC_ID of workgroup 0 + b) % 8.  The turn does not restart at XCD 0 with each launch (it
+// continues from the previous launch's last workgroup), so only this relative order is checked and
+// relied on.  Probed once per process; attention launches rely on it for their XCD-local merge
+// (AttnArgs::xcd_local) unless AF_ATTN_XCD_LOCAL=0.
+std::once_flag g_xcd_once;
+bool g_xcd_rr = false;
+
+bool attn_xcd_local() {
+    std::call_once(g_xcd_once, [] {
+        constexpr uint32_t kProbe = 4096;
+        DevMem map;
+        if (dev_alloc(map, (size_t)kProbe * 4, "XCD map") != AF_OK) return;
+        std::vector<uint32_t> xcc(kProbe);
+        if (step_xcd_map(kProbe, map.as<uint32_t>(), nullptr) != hipSuccess ||
+            hipMemcpy(xcc.data(), map.p, (size_t)kProbe * 4, hipMemcpyDeviceToHost) != hipSuccess)
+            return;
+        bool rr = true;
+        for (uint32_t b = 0; b < kProbe; ++b) rr = rr && xcc[b] == (xcc[0] + b) % kXcds;
+        g_xcd_rr = rr;
+    });
+    const char* env = std::getenv("AF_ATTN_XCD_LOCAL");
+    return g_xcd_rr && !(env && std::strcmp(env, "0") == 0);
+}
+
+// The chunk count attention_kernel derives for `nvis` visible positions (at most cmax chunks of at
+// least min_chunk positions, equal lengths but the last).
+uint32_t attn_chunks(uint32_t nvis, uint32_t cmax, uint32_t min_chunk) {
+    uint32_t chunks = std::min(cmax, (nvis + min_chunk - 1) / min_chunk);
+    const uint32_t clen = (nvis + chunks - 1) / chunks;
+    return (nvis + clen - 1) / clen;
+}
+
 unsigned host_threads() {
     unsigned n = std::thread::hardware_concurrency();
     return std::max(1u, std::min(16u, n ? n : 1u));
@@ -757,12 +791,15 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     if (p->position >= p->rope.context) return fail(AF_ERR_INVALID, "position outside the RoPE context");
     const uint32_t nvis = p->config.window ? std::min(p->position + 1, p->config.window) : p->position + 1;
     if (p->ring < nvis || p->ring == 0) return fail(AF_ERR_INVALID, "KV ring smaller than the visible range");
+    if ((uint64_t)p->ring * p->config.width * 2 > 0x7FFF0000ull)  // addressed with 32-bit byte offsets
+        return fail(AF_ERR_INVALID, "KV ring above 2 GiB per KV head");
     for (float e : {p->q_eps, p->k_eps, p->v_eps})
         if (!std::isfinite(e) || e <= 0.0f) return fail(AF_ERR_INVALID, "epsilon must be finite and positive");
     if ((rc = ensure_device())) return rc;
     const uint32_t group = p->config.q_heads / p->config.kv_heads, D = p->config.width;
     if (nvis > kAttnMaxChunks * kAttnMaxChunkLen) return fail(AF_ERR_INVALID, "visible range above 131072 tokens");
     const uint32_t cmax = kAttnMaxChunks;
+    const bool xl = attn_xcd_local();
     std::lock_guard<std::mutex> lock(g_scratch.mu);
     if ((rc = grow(g_scratch.attn_part, (size_t)p->config.kv_heads * cmax * group * attn_part_row(D) * 4, false, "attention scratch")))
         return rc;
@@ -799,10 +836,11 @@ int af_attention_decode(const af_attention_args* p, void* stream) {
     a.out = p->out;
     a.part = g_scratch.attn_part.as<float>();
     a.counters = g_scratch.attn_counters.as<uint32_t>();
-    a.cmax = cmax;
+    a.cmax = attn_chunks(nvis, cmax, kAttnMinChunk);  // the position is known: a block per chunk
     a.min_chunk = kAttnMinChunk;
     a.kv_heads = p->config.kv_heads;
     a.group = group;
+    a.xcd_local = xl ? 1u : 0u;
     HIP_OK(launch_attention(a, group, D, (hipStream_t)stream), "attention launch");
     return AF_OK;
 }
@@ -910,6 +948,7 @@ struct af_session {
     bool use_step = true;     // all layers of a step in one persistent launch
     uint32_t fail_phase = ~0u;  // AF_STEP_FAIL_PHASE: a step-kernel barrier that times out (tests)
     bool xcd_local = false;     // the step kernel's XCD-local layout (setup_step)
+    bool attn_xl = false;       // attention launches' XCD-local merge (attn_xcd_local)
     uint32_t step_grid = 0, step_cmax = 0, group = 0;
     uint32_t step_attn_pre = 0, step_stage_clen = 0;  // an attention item's LDS (step_attn_layout)
     size_t step_lds = 0;
@@ -1040,6 +1079,7 @@ struct af_session {
         aa.min_chunk = kAttnMinChunk;
         aa.kv_heads = L.kv_heads;
         aa.group = L.q_heads / L.kv_heads;
+        aa.xcd_local = attn_xl ? 1u : 0u;
         const double nvis = L.window ? std::min<double>(host_pos + 1, L.window) : host_pos + 1.0;
         const double attn_bytes = nvis * 2.0 * L.kn * 2.0 + 4.0 * (2.0 * L.qn + 2.0 * L.kn) + 4.0 * L.kn;
         if ((e = timed(K_ATTN, attn_bytes, [&] { return launch_attention(aa, L.q_heads / L.kv_heads, L.width, stream); })) !=
@@ -1565,8 +1605,9 @@ int setup_step(af_session& s) {
     s.step_count = count;
     int rc;
     // XCD-local layout (StepArgs::xcd_local): BASELINE's attention geometry (8 KV heads of two query
-    // heads, width 256, separate V) on a 256-workgroup grid whose workgroup b runs on XCD b % 8,
-    // which a probe launch checks on this device; AF_STEP_XCD_LOCAL=0 turns it off.
+    // heads, width 256, separate V) on a 256-workgroup grid whose workgroups b and b + 8 share an XCD
+    // (workgroup b on XCD (x0 + b) % 8, where x0 varies from launch to launch), which a probe launch
+    // checks on this device; AF_STEP_XCD_LOCAL=0 turns it off.
     bool xl = grid == 256 && group == 2 && !(std::getenv("AF_STEP_XCD_LOCAL") &&
                                               std::strcmp(std::getenv("AF_STEP_XCD_LOCAL"), "0") == 0);
     for (uint32_t i = 0; i < nl; ++i) {
@@ -1580,7 +1621,7 @@ int setup_step(af_session& s) {
         HIP_OK(step_xcd_map(grid, map.as<uint32_t>(), nullptr), "XCD map");
         std::vector<uint32_t> xcc(grid);
         HIP_OK(hipMemcpy(xcc.data(), map.p, (size_t)grid * 4, hipMemcpyDeviceToHost), "XCD map");
-        for (uint32_t b = 0; b < grid; ++b) xl = xl && xcc[b] == b % kXcds;
+        for (uint32_t b = 0; b < grid; ++b) xl = xl && xcc[b] == (xcc[0] + b) % kXcds;
     }
     s.xcd_local = xl;
     std::vector<StepLayer> table;
@@ -1818,6 +1859,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     s->events.resize(AF_MAX_NEW_TOKENS);
     for (auto& e : s->events) HIP_OK(hipEventCreate(&e), "event");
     HIP_OK(hipEventCreate(&s->ev_start), "event");
+    s->attn_xl = attn_xcd_local();
     if ((rc = setup_step(*s))) return rc;
     HIP_OK(hipDeviceSynchronize(), "session upload");
     if (s->use_graphs) {

@@ -13,6 +13,8 @@ namespace af {
 // and the last workgroup reads them from the memory side: no device-scope fence, which would write
 // back and invalidate the L2.
 constexpr int kPartSC1 = 16;       // buffer access policy sc1: through to (or from) the memory side
+constexpr int kPartSC0 = 1;        // stores: workgroup scope, into the XCD's L2
+constexpr int kPartNT = 2;         // loads: non-temporal, miss the CU's L1 and hit the XCD's L2
 constexpr int kWaitVm0 = 0x0F70;   // s_waitcnt vmcnt(0), expcnt and lgkmcnt unconstrained
 
 // ---- Q4_0 GEMV: persistent, one workgroup per CU ----------------------------------------------
@@ -539,8 +541,11 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
 
 // ---- GQA decode attention ---------------------------------------------------------------------
 //
-// Grid (cmax, kv_heads * query groups, tokens), D threads; grid z indexes the tokens of a batch
-// (positions position + z, rows z * in_stride of q/k/v and z * out_stride of out).  Modes: ATT_DECODE
+// A flat grid of D-thread blocks over (slot, chunk), slot = token * kv_heads * query groups + KV
+// head * query groups + query group: block b takes chunk (b / 8) % C of slot ((b / 8) / C) * 8 + b % 8
+// (C = cmax, or 1 in ATT_APPEND), so the blocks of one slot are a multiple of 8 apart and, with
+// workgroups dispatched to the 8 XCDs in turn, share an XCD.  The token of a slot indexes the batch (positions position + z,
+// rows z * in_stride of q/k/v and z * out_stride of out).  Modes: ATT_DECODE
 // appends the new K/V and attends; ATT_APPEND only normalises, rotates and appends K/V (grid x 1);
 // ATT_ATTEND attends with every position's K/V already in the cache.  Each block takes one chunk of the
 // visible range [max(0, pos + 1 - window), pos] for one KV head and its GQ
@@ -549,30 +554,69 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
 // normalises and rotates the new key, optionally normalises the value, rounds
 // both to fp16 and appends them at slot pos % ring.  Then scores (16 lanes per
 // token), chunk softmax, and p-weighted values; chunk partials (acc, max, sum)
-// are merged by the last block of the KV head.
+// are merged by the last block of the slot.  XL: the slots' blocks share an XCD (the launch checked the
+// dispatch order), so the partials and the ticket stay in that XCD's L2; otherwise they go through the
+// memory side, where every XCD's accesses meet.
 
 // RP: the q / k / v rows come from split-K partials (AttnArgs::raw_parts), a separate instance so
 // that the decode path's code is unchanged by it.
-template <int D, int G, bool RP = false>
+__device__ __forceinline__ uint4 as_u4(v4u v) { return make_uint4(v.x, v.y, v.z, v.w); }
+
+// Maximum and sum over the positions of one attention score step, whose LK lanes each hold one
+// position's value: the 32-lane halves (and, at 16 lanes per position, the rows) swapped in registers.
+template <int LK>
+__device__ __forceinline__ float positions_max(float v) {
+    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(h[0]), __uint_as_float(h[1]));
+    if constexpr (LK == 16) {
+        const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+    }
+    return v;
+}
+template <int LK>
+__device__ __forceinline__ float positions_sum(float v) {
+    if constexpr (LK == 16) {
+        return row_total(v);
+    } else {
+        const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(h[0]) + __uint_as_float(h[1]);
+    }
+}
+
+template <int D, int G, bool RP = false, bool XL = false, bool SH = false>
 __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     static_assert(D == 256 || D == 512, "one thread per channel");
     constexpr int NH = G + 2;     // this block's query heads, then the new key and value
     constexpr int W = D / 64;     // waves
     constexpr int LK = D / 16;    // lanes per token in the score loop (16 channels each)
-    constexpr int TG = D / LK;    // token groups in the score loop (16)
-    constexpr int UK = 8;         // cached K rows in flight per score-loop lane group
-    constexpr int UV = 8;         // cached V rows in flight per value-loop lane group
-    __shared__ float nrm[NH][D];
+    constexpr int KPW = 64 / LK;  // tokens per wave in one score-loop step
+    constexpr int LV = D / 8;     // lanes per token in the value loop (8 channels each)
+    constexpr int VPW = 64 / LV;  // tokens per wave in one value-loop step
+    // SH: at most kAttnShortChunks chunks of at most kAttnMinChunk positions (every row returned to
+    // the registers costs the CU's load-return bandwidth, so the first batches fit such a chunk)
+    constexpr int UK = SH ? kAttnMinChunk / W / KPW : 8;  // cached K rows in flight per score-loop lane group
+    constexpr int UV = SH ? kAttnMinChunk / W / VPW : 8;  // cached V rows in flight per value-loop lane group
+    constexpr uint32_t kWaveTokens = kAttnMaxChunkLen / W;  // a wave's share of a chunk, at most
+    __shared__ float rawl[NH][D];
     __shared__ float qs[G][D];
-    __shared__ float scores[G][kAttnMaxChunkLen];
-    __shared__ __align__(16) float vred[8][G][D];
+    __shared__ float sc[SH ? 1 : W][G][SH ? 1 : kWaveTokens];  // each wave's scores, then probabilities
+    __shared__ __align__(16) float wacc[W][G][D];     // each wave's p-weighted value sums
+    __shared__ float wml[W][G][2];                    // each wave's maximum and sum
     __shared__ double dred[W][NH];
-    __shared__ float cw[G][kAttnMaxChunks];
+    __shared__ __align__(16) float cw[G][kAttnMaxChunks];
+    __shared__ __align__(16) float sl[G][kAttnMaxChunks];
     __shared__ bool last;
+    constexpr int kStPol = XL ? kPartSC0 : kPartSC1, kLdPol = XL ? kPartNT : kPartSC1;
+    constexpr int kScope = XL ? __HIP_MEMORY_SCOPE_WORKGROUP : __HIP_MEMORY_SCOPE_AGENT;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
     if (a.state && a.state[ST_STOP]) return;
-    const uint32_t z = blockIdx.z;
+    const uint32_t qgroups = a.group / G, per_token = a.kv_heads * qgroups;
+    const uint32_t cgrid = a.mode == ATT_APPEND ? 1u : a.cmax;
+    const uint32_t slot = (blockIdx.x / 8 / cgrid) * 8 + blockIdx.x % 8, c = blockIdx.x / 8 % cgrid;
+    if (slot >= a.tokens * per_token) return;
+    const uint32_t z = slot / per_token;
     const uint32_t pos = (a.state ? a.state[ST_POS] : a.position) + z;
     const float* q_raw = a.q_raw + (size_t)z * a.in_stride;
     const float* k_raw = a.k_raw + (size_t)z * a.in_stride;
@@ -583,9 +627,8 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     uint32_t chunks = min(a.cmax, (nvis + a.min_chunk - 1) / a.min_chunk);
     const uint32_t clen = (nvis + chunks - 1) / chunks;
     chunks = (nvis + clen - 1) / clen;
-    // block (c, kvh * qgroups + qg): chunk c of query heads kvh * group + qg * G + [0, G)
-    const uint32_t qgroups = a.group / G;
-    const uint32_t c = blockIdx.x, kvh = blockIdx.y / qgroups, qg = blockIdx.y % qgroups;
+    // chunk c of query heads kvh * group + qg * G + [0, G)
+    const uint32_t kvh = slot % per_token / qgroups, qg = slot % qgroups;
     const uint32_t qh0 = kvh * a.group + qg * G;
     if (a.mode == ATT_APPEND ? qg != 0 && !a.q_out : c >= chunks) return;
     const uint32_t t0 = start + c * clen, t1 = min(pos + 1, t0 + clen);
@@ -595,11 +638,14 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
     const bool has_new = a.mode == ATT_APPEND || (a.mode == ATT_DECODE && t1 == pos + 1);
     const bool append = has_new && qg == 0;  // and this block stores them in the cache
     const int nh = has_new ? NH : G;
+    // Wave w takes the chunk's positions t0 + W k + w, k < nk: scores, softmax and p-weighted values
+    // of its own positions, with no block barrier in between; the waves' partials are then combined.
+    const uint32_t nk = n > wave ? (n - wave + W - 1) / W : 0u;
 
     // The prologue's inputs are requested first (vector loads return in issue order), then the
-    // score loop's first batch of cached K rows, which the prologue's arithmetic does not wait for:
-    // UK tokens per lane group, rows past the chunk clamped to its last one (the new token's row is
-    // read from LDS instead; its cache slot may be written meanwhile).
+    // first batches of cached K and V rows, which the prologue's arithmetic does not wait for: rows
+    // past the wave's positions clamped to the chunk's last one (the new token's row is read from
+    // LDS instead; its cache slot may be written meanwhile).
     float raw[NH];
     if constexpr (RP) {
         // the partial planes, eight at a time, each round's loads issued before its sums
@@ -626,60 +672,96 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
                     if (k0 + k < a.raw_parts) raw[h] = k0 + k == 0 ? pv[k][h] : raw[h] + pv[k][h];
         }
     } else {
+        // every load unconditional (a load under a branch is waited for at the branch's end)
 #pragma unroll
         for (int h = 0; h < G; ++h) raw[h] = q_raw[(size_t)(qh0 + h) * D + tid];
-        raw[G] = has_new ? k_raw[(size_t)kvh * D + tid] : 0.0f;
-        raw[G + 1] = has_new ? v_raw[(size_t)kvh * D + tid] : 0.0f;
+        const float kr = k_raw[(size_t)kvh * D + tid], vr = v_raw[(size_t)kvh * D + tid];
+        raw[G] = has_new ? kr : 0.0f;
+        raw[G + 1] = has_new ? vr : 0.0f;
     }
-    const float qnw = a.q_norm[tid], knw = has_new ? a.k_norm[tid] : 0.0f;
-    const double ifreq = tid < D / 2 ? a.inv_freq[tid] : 0.0;
+    // thread j < D / 2 normalises and rotates the channel pair (j, j + D / 2)
+    const bool pair = tid < D / 2;
+    const uint32_t jh = tid % (D / 2);
+    const float qw0 = a.q_norm[jh], qw1 = a.q_norm[jh + D / 2];
+    const float kw0 = a.k_norm[jh], kw1 = a.k_norm[jh + D / 2];
+    const double ifreq = a.inv_freq[jh];
     __builtin_amdgcn_sched_barrier(0);
-    const uint32_t grp = tid / LK, j = tid % LK;
+    // The KV head's cache rows through buffer resources: with no bytes in ATT_APPEND, where the
+    // loads below return zeros without a memory access (loads under a branch would be waited for
+    // at its end, before the prologue).
+    const uint32_t head_bytes = a.mode == ATT_APPEND ? 0u : ring * (uint32_t)D * 2u;
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(a.kcache + (size_t)kvh * ring * D, 0, head_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(a.vcache + (size_t)kvh * ring * D, 0, head_bytes, 0x00020000);
+    const uint32_t g = lane / LK, j = lane % LK;  // score loop: token slot, 16-channel slice
     uint4 kb[UK][2];
-    auto load_k = [&](uint32_t tb) {
+    auto load_k = [&](uint32_t k0) {
 #pragma unroll
         for (int u = 0; u < UK; ++u) {
-            const uint32_t tt = min(tb + TG * u, t1 - 1);
-            const uint4* kp = reinterpret_cast<const uint4*>(a.kcache + ((size_t)kvh * ring + tt % ring) * D + 16 * j);
-            kb[u][0] = kp[0];
-            kb[u][1] = kp[1];
+            const uint32_t k = k0 + KPW * u + g;
+            const uint32_t off = ((t0 + min(W * k + wave, n - 1)) % ring * D + 16 * j) * 2;
+            kb[u][0] = as_u4(__builtin_amdgcn_raw_buffer_load_b128(krs, off, 0, 0));
+            kb[u][1] = as_u4(__builtin_amdgcn_raw_buffer_load_b128(krs, off + 16, 0, 0));
         }
     };
-    if (a.mode != ATT_APPEND) load_k(t0 + grp);
+    const uint32_t hv = lane / LV, dl = lane % LV;  // value loop: token slot, 8-channel slice
+    uint4 vb[SH ? 1 : UV];
+    auto load_v = [&](uint32_t k0) {
+#pragma unroll
+        for (int u = 0; u < UV; ++u) {
+            const uint32_t k = k0 + VPW * u + hv;
+            vb[u] = as_u4(__builtin_amdgcn_raw_buffer_load_b128(vrs, ((t0 + min(W * k + wave, n - 1)) % ring * D + 8 * dl) * 2, 0, 0));
+        }
+    };
+    // SH: one of the wave's positions per value row (VC channels per lane), every position of the
+    // wave at once; rows past the wave's positions read as zeros (their probabilities are zero)
+    constexpr int VC = D / 64, NT = kAttnMinChunk / W;
+    using VRow = std::conditional_t<VC == 4, uint2, uint4>;
+    VRow vs[SH ? NT : 1];
+    load_k(0);
+    if constexpr (SH) {
+#pragma unroll
+        for (int k = 0; k < NT; ++k) {
+            const uint32_t off = (uint32_t)k < nk ? (((t0 + W * k + wave) % ring) * D + VC * lane) * 2 : 0x80000000u;
+            if constexpr (VC == 4) {
+                const v2u w = __builtin_amdgcn_raw_buffer_load_b64(vrs, off, 0, 0);
+                vs[k] = make_uint2(w.x, w.y);
+            } else {
+                vs[k] = as_u4(__builtin_amdgcn_raw_buffer_load_b128(vrs, off, 0, 0));
+            }
+        }
+    } else {
+        load_v(0);
+    }
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- prologue: RMSNorm of the query heads (and new K, V) with one block reduction, then RoPE
+    // ---- prologue: RMSNorm of the query heads (and the new K, V), then RoPE; two barriers
     double sn = 0.0, cs = 1.0;
-    if (tid < D / 2) sincos((double)pos * ifreq, &sn, &cs);
+    if (pair) sincos((double)pos * ifreq, &sn, &cs);
 #pragma unroll
     for (int h = 0; h < NH; ++h) {
         const double v = wave_sum((double)raw[h] * (double)raw[h]);
         if (lane == 0) dred[wave][h] = v;
+        rawl[h][tid] = raw[h];
     }
     __syncthreads();
-#pragma unroll
-    for (int h = 0; h < NH; ++h) {
-        if (h >= nh) break;
-        double ss = 0.0;  // waves summed pairwise in index order
+    auto block_ss = [&](int h) {  // waves summed pairwise in index order
         if constexpr (W == 4) {
-            ss = (dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h]);
+            return (dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h]);
         } else {
-            ss = ((dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h])) +
-                 ((dred[4][h] + dred[5][h]) + (dred[6][h] + dred[7][h]));
+            return ((dred[0][h] + dred[1][h]) + (dred[2][h] + dred[3][h])) +
+                   ((dred[4][h] + dred[5][h]) + (dred[6][h] + dred[7][h]));
         }
-        if (h < G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.q_eps), qnw);
-        else if (h == G) nrm[h][tid] = norm_apply(raw[h], inv_rms(ss, D, a.k_eps), knw);
-        else nrm[h][tid] = a.v_norm ? (float)__dmul_rn((double)raw[h], inv_rms(ss, D, a.v_eps)) : raw[h];
-    }
-    __syncthreads();
+    };
     // the new token's K (rotated) and V, fp16, for this block's reads: in the cache when this block
     // appends them, otherwise in LDS (another block of the KV head appends the same values)
     __shared__ uint16_t knew[D], vnew[D];
-    if (tid < D / 2) {
+    if (pair) {
 #pragma unroll
         for (int h = 0; h < G + 1; ++h) {
             if (h == G && !has_new) break;
-            const double x = (double)nrm[h][tid], y = (double)nrm[h][tid + D / 2];
+            const double r = inv_rms(block_ss(h), D, h < G ? a.q_eps : a.k_eps);
+            const double x = (double)norm_apply(raw[h], r, h < G ? qw0 : kw0);
+            const double y = (double)norm_apply(rawl[h][tid + D / 2], r, h < G ? qw1 : kw1);
             const float r0 = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
             const float r1 = (float)__dadd_rn(__dmul_rn(x, sn), __dmul_rn(y, cs));
             if (h < G) {
@@ -691,12 +773,13 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
             }
         }
     }
-    if (has_new) vnew[tid] = f2h(nrm[G + 1][tid]);
+    if (has_new)
+        vnew[tid] = f2h(a.v_norm ? (float)__dmul_rn((double)raw[G + 1], inv_rms(block_ss(G + 1), D, a.v_eps)) : raw[G + 1]);
     __syncthreads();
     if (append) {
-        const size_t slot = ((size_t)kvh * ring + pos % ring) * D;
-        a.kcache[slot + tid] = knew[tid];
-        a.vcache[slot + tid] = vnew[tid];
+        const size_t slot_off = ((size_t)kvh * ring + pos % ring) * D;
+        a.kcache[slot_off + tid] = knew[tid];
+        a.vcache[slot_off + tid] = vnew[tid];
     }
     if (a.mode == ATT_APPEND) {
         if (a.q_out) {
@@ -707,25 +790,129 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         return;
     }
 
-    // ---- scores: LK lanes per token (16 channels each), TG token groups, UK tokens per group in flight
+    float mw[G], lw[G];
+    if constexpr (SH) {
+        // ---- scores of this wave's positions k = KPW u + g, u < UK (all of them), in registers:
+        // the LK lanes of a position all hold its score (-inf past the wave's positions)
+        float sd[UK][G];
+        float qr[G][16];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) qr[gi][e] = qs[gi][16 * j + e];
+#pragma unroll
+        for (int u = 0; u < UK; ++u) {
+            const uint32_t k = KPW * u + g, t = t0 + W * k + wave;
+            uint4 k0v = kb[u][0], k1v = kb[u][1];
+            if (has_new && t == pos) {
+                k0v = *reinterpret_cast<const uint4*>(knew + 16 * j);
+                k1v = *reinterpret_cast<const uint4*>(knew + 16 * j + 8);
+            }
+            const uint32_t kw[8] = {k0v.x, k0v.y, k0v.z, k0v.w, k1v.x, k1v.y, k1v.z, k1v.w};
+            float kf[16];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                kf[2 * e] = h2f((uint16_t)(kw[e] & 0xFFFFu));
+                kf[2 * e + 1] = h2f((uint16_t)(kw[e] >> 16));
+            }
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
+                d = row_sum(d);
+                if constexpr (LK == 32) d += __shfl_xor(d, 16);  // the position's second row of 16 lanes
+                sd[u][gi] = k < nk ? d * a.scale : -INFINITY;
+            }
+        }
+        // ---- softmax over the wave's positions: across the KPW positions of a step with lane swaps
+        float pr[UK][G];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi) {
+            float mx = sd[0][gi];
+#pragma unroll
+            for (int u = 1; u < UK; ++u) mx = fmaxf(mx, sd[u][gi]);
+            mx = positions_max<LK>(mx);
+            float sum = 0.0f;
+#pragma unroll
+            for (int u = 0; u < UK; ++u) {
+                pr[u][gi] = sd[u][gi] > -INFINITY ? expf(sd[u][gi] - mx) : 0.0f;
+                sum += pr[u][gi];
+            }
+            mw[gi] = mx;
+            lw[gi] = positions_sum<LK>(sum);
+        }
+        // ---- p-weighted values: position k's probability from lane (k % KPW) LK of its step
+        float acc[G][VC];
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int e = 0; e < VC; ++e) acc[gi][e] = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NT; ++k) {
+            if ((uint32_t)k >= nk) break;
+            const uint32_t t = t0 + W * k + wave;
+            VRow v = vs[k];  // (a conditional assignment, as for the K rows)
+            if (has_new && t == pos) v = *reinterpret_cast<const VRow*>(vnew + VC * lane);
+            uint32_t vw[VC / 2];
+            if constexpr (VC == 4) {
+                vw[0] = v.x;
+                vw[1] = v.y;
+            } else {
+                vw[0] = v.x;
+                vw[1] = v.y;
+                vw[2] = v.z;
+                vw[3] = v.w;
+            }
+            float vf[VC];
+#pragma unroll
+            for (int e = 0; e < VC / 2; ++e) {
+                vf[2 * e] = h2f((uint16_t)(vw[e] & 0xFFFFu));
+                vf[2 * e + 1] = h2f((uint16_t)(vw[e] >> 16));
+            }
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                const float pk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[k / KPW][gi]), (k % KPW) * LK));
+#pragma unroll
+                for (int e = 0; e < VC; ++e) acc[gi][e] = fmaf(pk, vf[e], acc[gi][e]);
+            }
+        }
+#pragma unroll
+        for (int gi = 0; gi < G; ++gi)
+#pragma unroll
+            for (int e = 0; e < VC; e += 4)
+                *reinterpret_cast<float4*>(&wacc[wave][gi][VC * lane + e]) =
+                    make_float4(acc[gi][e], acc[gi][e + 1], acc[gi][e + 2], acc[gi][e + 3]);
+        if (lane == 0) {
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                wml[wave][gi][0] = mw[gi];
+                wml[wave][gi][1] = lw[gi];
+            }
+        }
+    } else {
+    // ---- scores of this wave's positions: LK lanes per position (16 channels each), KPW positions
+    // per step, UK steps in flight
+    float* const ws = &sc[wave][0][0];  // [G][kWaveTokens]
     {
         float qr[G][16];
 #pragma unroll
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 16; ++e) qr[gi][e] = qs[gi][16 * j + e];
-        for (uint32_t tb = t0 + grp; tb < t1; tb += UK * TG) {
-            if (tb != t0 + grp) load_k(tb);
+        for (uint32_t k0 = 0; k0 < nk; k0 += UK * KPW) {
+            if (k0) load_k(k0);
 #pragma unroll
             for (int u = 0; u < UK; ++u) {
-                const uint32_t t = tb + TG * u;
-                if (t >= t1) break;
-                uint4 k0 = kb[u][0], k1 = kb[u][1];
+                const uint32_t k = k0 + KPW * u + g;
+                if (k >= nk) break;
+                const uint32_t t = t0 + W * k + wave;
+                uint4 k0v = kb[u][0], k1v = kb[u][1];
                 if (has_new && t == pos) {
-                    k0 = *reinterpret_cast<const uint4*>(knew + 16 * j);
-                    k1 = *reinterpret_cast<const uint4*>(knew + 16 * j + 8);
+                    k0v = *reinterpret_cast<const uint4*>(knew + 16 * j);
+                    k1v = *reinterpret_cast<const uint4*>(knew + 16 * j + 8);
                 }
-                const uint32_t kw[8] = {k0.x, k0.y, k0.z, k0.w, k1.x, k1.y, k1.z, k1.w};
+                const uint32_t kw[8] = {k0v.x, k0v.y, k0v.z, k0v.w, k1v.x, k1v.y, k1v.z, k1v.w};
                 float kf[16];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
@@ -738,75 +925,53 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
 #pragma unroll
                     for (int e = 0; e < 16; ++e) d = fmaf(qr[gi][e], kf[e], d);
                     d = row_sum(d);
-                    if constexpr (LK == 32) d += __shfl_xor(d, 16);  // the token's second row of 16 lanes
-                    if (j == 0) scores[gi][t - t0] = d * a.scale;
+                    if constexpr (LK == 32) d += __shfl_xor(d, 16);  // the position's second row of 16 lanes
+                    if (j == 0) ws[gi * kWaveTokens + k] = d * a.scale;
                 }
             }
         }
     }
-    __syncthreads();
+    // the wave reads what its own lanes wrote to LDS: in order, no block barrier
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 
-    // the value loop's first batch of cached V rows, in flight during the softmax
-    constexpr uint32_t LV = D / 8;
-    const uint32_t tg = tid / LV, dl = tid % LV;
-    uint4 vb[UV];
-    auto load_v = [&](uint32_t tb) {
-#pragma unroll
-        for (int u = 0; u < UV; ++u) {
-            const uint32_t tt = min(tb + 8 * u, t1 - 1);
-            vb[u] = *reinterpret_cast<const uint4*>(a.vcache + ((size_t)kvh * ring + tt % ring) * D + 8 * dl);
-        }
-    };
-    load_v(t0 + tg);
-
-    // softmax over the chunk: wave maxima of every query head, one barrier, then the exponentials
-    // and wave sums, one barrier; waves combined in index order
-    __shared__ float smx[G][W], ssum[G][W];
-    float m[G], l[G];
+    // ---- this wave's softmax: maximum, exponentials, sum
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
         float mx = -INFINITY;
-        for (uint32_t i = tid; i < n; i += blockDim.x) mx = fmaxf(mx, scores[gi][i]);
+        for (uint32_t k = lane; k < nk; k += 64) mx = fmaxf(mx, ws[gi * kWaveTokens + k]);
         mx = wave_max(mx);
-        if (lane == 0) smx[gi][wave] = mx;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        float mx = smx[gi][0];
-        for (int w = 1; w < W; ++w) mx = fmaxf(mx, smx[gi][w]);
-        m[gi] = mx;
         float sum = 0.0f;
-        for (uint32_t i = tid; i < n; i += blockDim.x) {
-            const float p = expf(scores[gi][i] - mx);
-            scores[gi][i] = p;
+        for (uint32_t k = lane; k < nk; k += 64) {
+            const float p = expf(ws[gi * kWaveTokens + k] - mx);
+            ws[gi * kWaveTokens + k] = p;
             sum += p;
         }
-        sum = wave_sum(sum);
-        if (lane == 0) ssum[gi][wave] = sum;
+        mw[gi] = mx;
+        lw[gi] = wave_sum(sum);
     }
-    __syncthreads();
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        float t = 0.0f;
-        for (int w = 0; w < W; ++w) t += ssum[gi][w];
-        l[gi] = t;
-    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 
-    // ---- values: D / 8 lanes per token row (8 channels each), 8 token groups, UV rows per group in flight
+    // ---- this wave's p-weighted values: LV lanes per position (8 channels each), VPW positions per
+    // step, UV steps in flight; the VPW slots of a lane's channels added at the end
     {
         float acc[G][8];
 #pragma unroll
         for (int gi = 0; gi < G; ++gi)
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[gi][e] = 0.0f;
-        for (uint32_t tb = t0 + tg; tb < t1; tb += 8 * UV) {
-            if (tb != t0 + tg) load_v(tb);
+        for (uint32_t k0 = 0; k0 < nk; k0 += UV * VPW) {
+            if (k0) load_v(k0);
 #pragma unroll
             for (int u = 0; u < UV; ++u) {
-                const uint32_t t = tb + 8 * u;
-                if (t >= t1) break;
-                const uint4 v = has_new && t == pos ? *reinterpret_cast<const uint4*>(vnew + 8 * dl) : vb[u];
+                const uint32_t k = k0 + VPW * u + hv;
+                if (k >= nk) break;
+                const uint32_t t = t0 + W * k + wave;
+                // (a conditional assignment: a select between the two loads would become a load
+                // from a selected address, which keeps vb in memory)
+                uint4 v = vb[u];
+                if (has_new && t == pos) v = *reinterpret_cast<const uint4*>(vnew + 8 * dl);
                 const uint32_t vw[4] = {v.x, v.y, v.z, v.w};
                 float vf[8];
 #pragma unroll
@@ -816,25 +981,58 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
                 }
 #pragma unroll
                 for (int gi = 0; gi < G; ++gi) {
-                    const float p = scores[gi][t - t0];
+                    const float p = ws[gi * kWaveTokens + k];
 #pragma unroll
                     for (int e = 0; e < 8; ++e) acc[gi][e] = fmaf(p, vf[e], acc[gi][e]);
                 }
             }
         }
+        if constexpr (VPW == 2) {  // lanes l and l + 32 hold the same channels: one total in both
 #pragma unroll
-        for (int gi = 0; gi < G; ++gi)
+            for (int gi = 0; gi < G; ++gi)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) vred[tg][gi][8 * dl + e] = acc[gi][e];
+                for (int e = 0; e < 8; ++e) {
+                    const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(acc[gi][e]),
+                                                                    __float_as_uint(acc[gi][e]), false, false);
+                    acc[gi][e] = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+                }
+        }
+        if (hv == 0) {  // written whatever nk (zeros for a wave with no positions)
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                *reinterpret_cast<float4*>(&wacc[wave][gi][8 * dl]) = make_float4(acc[gi][0], acc[gi][1], acc[gi][2], acc[gi][3]);
+                *reinterpret_cast<float4*>(&wacc[wave][gi][8 * dl + 4]) = make_float4(acc[gi][4], acc[gi][5], acc[gi][6], acc[gi][7]);
+            }
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int gi = 0; gi < G; ++gi) {
+                wml[wave][gi][0] = mw[gi];
+                wml[wave][gi][1] = lw[gi];
+            }
+        }
     }
+    }  // SH
     __syncthreads();
-    float o[G];
+
+    // ---- the chunk's partial (channel tid): waves weighted by exp(m_w - M), in wave order (a wave
+    // with no positions has m_w = -inf, weight 0; wave 0 always has one)
+    float o[G], m[G], l[G];
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-        float t = 0.0f;
+        float M = wml[0][gi][0];
 #pragma unroll
-        for (int g = 0; g < 8; ++g) t += vred[g][gi][tid];
-        o[gi] = t;
+        for (int w = 1; w < W; ++w) M = fmaxf(M, wml[w][gi][0]);
+        float ot = 0.0f, lt = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+            const float e = expf(wml[w][gi][0] - M);
+            ot = fmaf(e, wacc[w][gi][tid], ot);
+            lt = fmaf(e, wml[w][gi][1], lt);
+        }
+        o[gi] = ot;
+        m[gi] = M;
+        l[gi] = lt;
     }
     if (chunks == 1) {
 #pragma unroll
@@ -842,71 +1040,76 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         return;
     }
 
-    // ---- split-K merge: the last block of this (KV head, query group) combines the chunk partials
+    // ---- split-K merge: the last block of the slot combines the chunk partials
     // (a query head's partial row: D sums, max, sum, padding to whole 16-byte pieces)
     constexpr uint32_t R = attn_part_row(D);
     const size_t stride = (size_t)G * R;
-    const uint32_t slot = blockIdx.z * gridDim.y + blockIdx.y;  // (token, KV head, query group)
-    // The blocks of a KV head may run on different XCDs, whose L2s are not coherent with each
-    // other: the partials are stored through to the memory side (sc1) and waited for, the ticket is
-    // an agent-scope atomic, and the last block reads the partials from the memory side, so no
-    // L2 write-back or invalidation (a device-scope fence) is needed.
+    // Without XL the blocks of a slot may run on different XCDs, whose L2s are not coherent with
+    // each other: the partials are stored through to the memory side (sc1) and waited for, the
+    // ticket is an agent-scope atomic, and the last block reads the partials from the memory side,
+    // so no L2 write-back or invalidation (a device-scope fence) is needed.  With XL they share one
+    // XCD's L2: stores into it, a ticket in it, loads that miss the CU's L1 and hit it.
     const __amdgpu_buffer_rsrc_t prs =
         __builtin_amdgcn_make_buffer_rsrc(a.part + (size_t)slot * a.cmax * stride, 0, 0x7FFFFFFF, 0x00020000);
     const uint32_t mine = c * (uint32_t)stride * 4;  // this chunk's byte offset
 #pragma unroll
     for (int gi = 0; gi < G; ++gi) {
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[gi]), prs, mine + (gi * R + tid) * 4, 0, kPartSC1);
-        if (tid == 0) {
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m[gi]), prs, mine + (gi * R + D) * 4, 0, kPartSC1);
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(l[gi]), prs, mine + (gi * R + D + 1) * 4, 0, kPartSC1);
-        }
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(o[gi]), prs, mine + (gi * R + tid) * 4, 0, kStPol);
+        if (tid == 0)
+            __builtin_amdgcn_raw_buffer_store_b64(v2u{__float_as_uint(m[gi]), __float_as_uint(l[gi])}, prs,
+                                                  mine + (gi * R + D) * 4, 0, kStPol);
     }
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
     if (tid == 0) {
-        const uint32_t ticket = __hip_atomic_fetch_add(a.counters + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t ticket = __hip_atomic_fetch_add(a.counters + slot, 1u, __ATOMIC_RELAXED, kScope);
         last = ticket == chunks - 1;
     }
     __syncthreads();
     if (!last) return;
-    // chunk maxima and sums into LDS (one load per thread), then the weights exp(m_c - M)
-    for (uint32_t i = tid; i < chunks * G; i += blockDim.x) {
-        const uint32_t k = i / G, gi = i % G, off = (k * (uint32_t)stride + gi * R + D) * 4;
-        cw[gi][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, off, 0, kPartSC1));
-        vred[0][gi][k] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(prs, off + 4, 0, kPartSC1));
-    }
-    __syncthreads();
-    float M[G], L[G];
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        M[gi] = -INFINITY;
-        for (uint32_t k = 0; k < chunks; ++k) M[gi] = fmaxf(M[gi], cw[gi][k]);
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < chunks * G; i += blockDim.x) {
-        const uint32_t k = i / G, gi = i % G;
-        cw[gi][k] = expf(cw[gi][k] - M[gi]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int gi = 0; gi < G; ++gi) {
-        L[gi] = 0.0f;
-        for (uint32_t k = 0; k < chunks; ++k) L[gi] = fmaf(cw[gi][k], vred[0][gi][k], L[gi]);
-    }
-    // weighted sums: thread tid takes 16-byte piece f of the G query heads' sums in every P-th chunk
-    // (chunks ph, ph + P, ..., MU of them in flight), then the P phases are added in order
-    constexpr uint32_t NF = G * D / 4, P = D / NF, MU = 16;
+    // One round of loads: chunk (tid / G)'s maximum and sum of query head tid % G, and the first MU
+    // of this thread's weighted-sum pieces: 16-byte piece f of the G query heads' sums in every P-th
+    // chunk (chunks ph, ph + P, ...).  The maxima and sums go through LDS (one barrier); every
+    // thread then takes the maximum M of its head and the weights exp(m_c - M) of its own chunks,
+    // and the P phases' sums are added in order (a second barrier).
+    constexpr uint32_t NF = G * D / 4, P = D / NF, MU = SH ? kAttnShortChunks / P : 16;
+    static_assert(G * kAttnMaxChunks <= D, "one thread per (query head, chunk) maximum");
     const uint32_t f = tid % NF, ph = tid / NF, fg = f / (D / 4), f4 = f % (D / 4);
-    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (uint32_t k0 = ph; k0 < chunks; k0 += MU * P) {
-        float4 pv[MU];
+    const uint32_t c4 = (chunks + 3) & ~3u;  // chunks rounded up to whole float4 reads
+    const bool has_ml = tid < chunks * G;
+    v2u ml{0u, 0u};
+    if (has_ml)
+        ml = __builtin_amdgcn_raw_buffer_load_b64(prs, ((tid / G) * (uint32_t)stride + (tid % G) * R + D) * 4, 0, kLdPol);
+    float4 pv[MU];
+    auto load_pieces = [&](uint32_t k0) {
 #pragma unroll
         for (uint32_t u = 0; u < MU; ++u) {
             const uint32_t k = min(k0 + u * P, chunks - 1);
-            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(prs, (k * (uint32_t)stride + fg * R + 4 * f4) * 4, 0, kPartSC1);
+            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(prs, (k * (uint32_t)stride + fg * R + 4 * f4) * 4, 0, kLdPol);
             pv[u] = make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
         }
+    };
+    load_pieces(ph);
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    if (tid < c4 * G) {  // past the last chunk: maximum -inf, sum 0
+        cw[tid % G][tid / G] = has_ml ? __uint_as_float(ml.x) : -INFINITY;
+        sl[tid % G][tid / G] = has_ml ? __uint_as_float(ml.y) : 0.0f;
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    if (has_ml) {
+        const float4* m4 = reinterpret_cast<const float4*>(cw[tid % G]);
+        for (uint32_t q = 0; q < c4 / 4; ++q) {
+            const float4 v = m4[q];
+            M = fmaxf(M, fmaxf(fmaxf(v.x, v.y), fmaxf(v.z, v.w)));
+        }
+    }
+    __syncthreads();
+    if (tid < c4 * G) cw[tid % G][tid / G] = has_ml ? expf(__uint_as_float(ml.x) - M) : 0.0f;
+    __syncthreads();
+    float4 acc4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float lp = 0.0f;  // sum over this thread's chunks of w_c l_c
+    for (uint32_t k0 = ph;;) {
 #pragma unroll
         for (uint32_t u = 0; u < MU; ++u) {
             const uint32_t k = k0 + u * P;
@@ -916,23 +1119,30 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
                 acc4.y = fmaf(w, pv[u].y, acc4.y);
                 acc4.z = fmaf(w, pv[u].z, acc4.z);
                 acc4.w = fmaf(w, pv[u].w, acc4.w);
+                lp = fmaf(w, sl[fg][k], lp);
             }
         }
+        k0 += MU * P;
+        if (k0 >= chunks) break;
+        load_pieces(k0);
     }
-    float4* red4 = reinterpret_cast<float4*>(&vred[0][0][0]);  // [P][NF], after L is read
-    __syncthreads();
+    static_assert(P * NF * 16 <= sizeof(wacc) && P * G == 4, "merge reduction layout");
+    float4* red4 = reinterpret_cast<float4*>(&wacc[0][0][0]);  // [P][NF]
+    __shared__ float redl[4];                                   // [P][G]: the sums of w_c l_c
     red4[ph * NF + f] = acc4;
+    if (f4 == 0) redl[ph * G + fg] = lp;
     __syncthreads();
     if (tid < NF) {
         float4 t = red4[f];
+        float il = redl[fg];
         for (uint32_t q = 1; q < P; ++q) {
             const float4 r = red4[q * NF + f];
             t.x += r.x;
             t.y += r.y;
             t.z += r.z;
             t.w += r.w;
+            il += redl[q * G + fg];
         }
-        const float il = L[fg];
         float4 y;
         y.x = t.x / il;
         y.y = t.y / il;
@@ -940,7 +1150,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         y.w = t.w / il;
         *reinterpret_cast<float4*>(out + (size_t)(qh0 + fg) * D + 4 * f4) = y;
     }
-    if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(a.counters + slot, 0u, __ATOMIC_RELAXED, kScope);
 }
 
 // Query heads per attention block: all of a KV head's at width 256 (1, 2 or 4), two at width 512
@@ -949,38 +1159,44 @@ uint32_t attention_block_heads(uint32_t group, uint32_t head_width) {
     return head_width == 256 ? group : std::min<uint32_t>(group, 2u);
 }
 
-hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s, uint32_t tokens) {
+namespace {
+template <int D, int G>
+void launch_attention_dg(const AttnArgs& a, dim3 grid, hipStream_t s) {
+    // the split-partial input only feeds the append pass (no merge); XL only changes the merge; SH
+    // when the launch's position (known on the host) leaves at most kAttnShortChunks short chunks
+    const bool sh = !a.state && a.mode != ATT_APPEND && a.cmax <= kAttnShortChunks && a.min_chunk == kAttnMinChunk &&
+                    (a.window ? std::min(a.position + a.tokens, a.window) : a.position + a.tokens) <=
+                        kAttnShortChunks * kAttnMinChunk;
+    if (a.raw_parts) hipLaunchKernelGGL((attention_kernel<D, G, true>), grid, dim3(D), 0, s, a);
+    else if (a.xcd_local && sh) hipLaunchKernelGGL((attention_kernel<D, G, false, true, true>), grid, dim3(D), 0, s, a);
+    else if (a.xcd_local) hipLaunchKernelGGL((attention_kernel<D, G, false, true>), grid, dim3(D), 0, s, a);
+    else if (sh) hipLaunchKernelGGL((attention_kernel<D, G, false, false, true>), grid, dim3(D), 0, s, a);
+    else hipLaunchKernelGGL((attention_kernel<D, G>), grid, dim3(D), 0, s, a);
+}
+}  // namespace
+
+hipError_t launch_attention(const AttnArgs& args, uint32_t group, uint32_t head_width, hipStream_t s, uint32_t tokens) {
     const uint32_t G = attention_block_heads(group, head_width);
-    if (a.group != group || group % G || tokens == 0) return hipErrorInvalidValue;
-    const dim3 grid(a.mode == ATT_APPEND ? 1 : a.cmax, a.kv_heads * (group / G), tokens);
-    if (a.raw_parts && (a.mode != ATT_APPEND || !a.raw_part)) return hipErrorInvalidValue;
-    const bool rp = a.raw_parts != 0;
+    if (args.group != group || group % G || tokens == 0 || args.kv_heads == 0) return hipErrorInvalidValue;
+    if (args.raw_parts && (args.mode != ATT_APPEND || !args.raw_part)) return hipErrorInvalidValue;
+    AttnArgs a = args;
+    a.tokens = tokens;
+    // (slot, chunk) blocks, slots rounded up to whole groups of 8 (one per XCD)
+    const uint64_t slots = (uint64_t)tokens * a.kv_heads * (group / G);
+    const uint64_t blocks = (slots + 7) / 8 * 8 * (a.mode == ATT_APPEND ? 1u : a.cmax);
+    if (blocks == 0 || blocks > 0x7FFFFFFFull) return hipErrorInvalidValue;
+    const dim3 grid((uint32_t)blocks);
     if (head_width == 256) {
         switch (G) {
-            case 1:
-                if (rp) hipLaunchKernelGGL((attention_kernel<256, 1, true>), grid, dim3(256), 0, s, a);
-                else hipLaunchKernelGGL((attention_kernel<256, 1>), grid, dim3(256), 0, s, a);
-                break;
-            case 2:
-                if (rp) hipLaunchKernelGGL((attention_kernel<256, 2, true>), grid, dim3(256), 0, s, a);
-                else hipLaunchKernelGGL((attention_kernel<256, 2>), grid, dim3(256), 0, s, a);
-                break;
-            case 4:
-                if (rp) hipLaunchKernelGGL((attention_kernel<256, 4, true>), grid, dim3(256), 0, s, a);
-                else hipLaunchKernelGGL((attention_kernel<256, 4>), grid, dim3(256), 0, s, a);
-                break;
+            case 1: launch_attention_dg<256, 1>(a, grid, s); break;
+            case 2: launch_attention_dg<256, 2>(a, grid, s); break;
+            case 4: launch_attention_dg<256, 4>(a, grid, s); break;
             default: return hipErrorInvalidValue;
         }
     } else if (head_width == 512) {
         switch (G) {
-            case 1:
-                if (rp) hipLaunchKernelGGL((attention_kernel<512, 1, true>), grid, dim3(512), 0, s, a);
-                else hipLaunchKernelGGL((attention_kernel<512, 1>), grid, dim3(512), 0, s, a);
-                break;
-            case 2:
-                if (rp) hipLaunchKernelGGL((attention_kernel<512, 2, true>), grid, dim3(512), 0, s, a);
-                else hipLaunchKernelGGL((attention_kernel<512, 2>), grid, dim3(512), 0, s, a);
-                break;
+            case 1: launch_attention_dg<512, 1>(a, grid, s); break;
+            case 2: launch_attention_dg<512, 2>(a, grid, s); break;
             default: return hipErrorInvalidValue;
         }
     } else {

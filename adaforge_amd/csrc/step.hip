@@ -1260,7 +1260,7 @@ __device__ __forceinline__ AttnGeo attn_geo(CLayer& L, uint32_t pos, uint32_t cm
 
 // The attention item (KV head h, chunk c) of this workgroup, if it has one: item i = h chunks + c
 // runs on workgroup grid - 1 - i, or in the XCD-local layout chunk c of head h on workgroup
-// 8 (grid / 8 - 1 - c) + h (every chunk of a head on XCD h).
+// 8 (grid / 8 - 1 - c) + h (every chunk of a head on one XCD).
 template <bool XL>
 __device__ __forceinline__ bool attn_item(const AttnGeo& ag, uint32_t& h, uint32_t& c) {
     if constexpr (XL) {
