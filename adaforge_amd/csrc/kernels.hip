@@ -759,7 +759,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
 #pragma unroll
         for (int h = 0; h < G + 1; ++h) {
             if (h == G && !has_new) break;
-            const double r = inv_rms(block_ss(h), D, h < G ? a.q_eps : a.k_eps);
+            const double r = inv_rms_fast(block_ss(h), D, h < G ? a.q_eps : a.k_eps);
             const double x = (double)norm_apply(raw[h], r, h < G ? qw0 : kw0);
             const double y = (double)norm_apply(rawl[h][tid + D / 2], r, h < G ? qw1 : kw1);
             const float r0 = (float)__dsub_rn(__dmul_rn(x, cs), __dmul_rn(y, sn));
@@ -774,7 +774,7 @@ __global__ __launch_bounds__(D) void attention_kernel(AttnArgs a) {
         }
     }
     if (has_new)
-        vnew[tid] = f2h(a.v_norm ? (float)__dmul_rn((double)raw[G + 1], inv_rms(block_ss(G + 1), D, a.v_eps)) : raw[G + 1]);
+        vnew[tid] = f2h(a.v_norm ? (float)__dmul_rn((double)raw[G + 1], inv_rms_fast(block_ss(G + 1), D, a.v_eps)) : raw[G + 1]);
     __syncthreads();
     if (append) {
         const size_t slot_off = ((size_t)kvh * ring + pos % ring) * D;
