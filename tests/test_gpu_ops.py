@@ -183,6 +183,20 @@ def test_config3_gqa_attention(ctx, kind):
     assert oracle.f16_ulps(k, kr).max() <= 1 and oracle.f16_ulps(v, vr).max() == 0
 
 
+@pytest.mark.parametrize("ctx", W.C3_CONTEXTS[:2])
+def test_config3_attention_memory_side_merge_matches_xcd_local(ctx, monkeypatch):
+    """The chunk partials and merge ticket through the memory side (AF_ATTN_XCD_LOCAL=0, read at
+    every call) give the oracle's result too, bit for bit the XCD-local merge's output: both merge
+    the same partials in the same order, only their cache policies differ."""
+    case = W.config3(ctx, "global")
+    xl, k1, v1 = attention_case(case)
+    monkeypatch.setenv("AF_ATTN_XCD_LOCAL", "0")
+    mem, k2, v2 = attention_case(case)
+    oracle.compare(W.config3_reference(case), mem)
+    assert np.array_equal(xl.view(np.uint32), mem.view(np.uint32))
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
+
+
 def small_case(ctx, window=None, q_heads=4, kv_heads=2, qscale=1.0, v_norm=False, tag="sc"):
     Wd = W.C3_WIDTH
     hist = ctx - 1
