@@ -1861,6 +1861,11 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
     HIP_OK(hipEventCreate(&s->ev_start), "event");
     s->attn_xl = attn_xcd_local();
     if ((rc = setup_step(*s))) return rc;
+    // A model whose step mixes step-kernel runs with per-operation layers is launched directly:
+    // replays of its captured step faulted on the host inside hipGraphLaunch under a rocprofv3
+    // kernel trace (cause not established), and without a profiler it decodes at the same rate
+    // either way (at most kDecodeAhead steps are queued ahead, so launch costs are hidden).
+    if (s->use_step && s->segmented()) s->use_graphs = false;
     HIP_OK(hipDeviceSynchronize(), "session upload");
     if (s->use_graphs) {
         // the step kernel and the head (decode), or the step kernel alone (prefill); on the

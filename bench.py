@@ -465,7 +465,7 @@ def gemma4_leg(new_tokens=256):
     head of width 512, K reused as V, proportional RoPE; attention scale 1, V-norm, softcap 30).  Its
     512-wide global layers are outside the persistent step kernel's limits: the step kernel takes the
     five-layer runs of local layers between them (one launch per run) and the per-operation kernels
-    the global layers, all in one hipGraph per token.  Batched prefill of 128 ids, then greedy decode
+    the global layers, launched directly (no graph: the same rate).  Batched prefill of 128 ids, then greedy decode
     in 128-token turns; decode tok/s over the turns."""
     from adaforge_amd import synth
     model = synth.gemma4_model(name="gemma4-bench", layers=48, hidden=HIDDEN, intermediate=INTER,
@@ -488,7 +488,7 @@ def gemma4_leg(new_tokens=256):
                        "sixth layer global: 16 q / 1 kv x 512, K as V, proportional RoPE; scale 1, V-norm, "
                        "softcap 30), Q4_0 projections, tied Q6_K table (vocab 262144); the step kernel "
                        "over each run of local layers, the per-operation kernels on the global layers, "
-                       "one hipGraph per token",
+                       "launched directly (no graph)",
            "prompt_tokens": PROMPT, "prefill_ms": round(prefill_ms, 2),
            "prefill_tok_s": round((PROMPT - 1) / prefill_ms * 1000.0, 1),
            "decode_tokens": produced, "decode_tok_s": round(produced / dt, 1)}
