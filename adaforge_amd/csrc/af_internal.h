@@ -268,6 +268,11 @@ hipError_t launch_batch_gemm(const BatchGemm& a, bool gelu_pair, hipStream_t s, 
 // ---- launchers (kernels.hip) -----------------------------------------------------------------
 hipError_t launch_q4_gemv(const Q4Args& a, int in_kind, int out_kind, uint32_t out_rows, hipStream_t s);
 hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_t s);
+// The head (IN_RESID) over nv <= kHeadBatchMax hidden states at once, vector v's x and res at
+// v vstride floats from a.in's; vector v's (id, bad) into a.result[2 v, 2 v + 1]; a.partial holds nv
+// entries per workgroup.
+constexpr uint32_t kHeadBatchMax = 4;
+hipError_t launch_head_batch(const HeadArgs& a, uint32_t nv, uint32_t vstride, uint32_t grid, hipStream_t s);
 hipError_t launch_attention(const AttnArgs& a, uint32_t group, uint32_t head_width, hipStream_t s,
                             uint32_t tokens = 1);
 uint32_t attention_block_heads(uint32_t group, uint32_t head_width);

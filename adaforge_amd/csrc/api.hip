@@ -985,7 +985,7 @@ struct af_session {
     uint32_t prefill_batch = kBatchMax, trace_batch = 0;
     // Greedy speculative decoding with prompt-lookup drafts (AF_SPECULATIVE=1; AF_SPEC_DEPTH draft
     // tokens at most, default 11, at most kVerifyMax - 1): the draft and the pending token run through
-    // the batched layers in one pass and the head checks each position.
+    // the batched layers in one pass and the head checks the positions, up to four per launch.
     bool speculative = false;
     uint32_t spec_depth = 11;
     uint64_t spec_passes = 0, spec_drafted = 0, spec_accepted = 0;  // since open (af_session_speculation)
@@ -1840,7 +1840,7 @@ int open_session(const af_layer_weights* layers, uint32_t n_layers, const af_out
         {&s->LOGITS, (size_t)hm.rows * 4, false},
         {&s->PART, (size_t)s->cmax * std::max<uint32_t>(max_qh_part, max_kv * step_part_stride(max_group)) * 4, false},
         {&s->COUNTERS, (size_t)std::max<uint32_t>(max_qh, 64) * 4, true},
-        {&s->HPART, (size_t)s->head_blocks * 16, false},
+        {&s->HPART, (size_t)s->head_blocks * 16 * kHeadBatchMax, false},  // (the verification head's per vector)
         {&s->HCOUNT, 256, true},
         {&s->STATE, ST_WORDS * 4, true},
         {&s->IDS, ((size_t)capacity + 2) * 4, true},
@@ -1928,8 +1928,9 @@ std::vector<uint32_t> draft_lookup(const std::vector<uint32_t>& h, size_t limit)
 // The decode loop of GenerationSession::generate with speculation (stack.rs:1252-1338), after the
 // prefill has left position P - 1 (or, with nothing pending, the last consumed position's head input)
 // to run.  Each round emits the pending greedy token; with a draft, the token and its draft go through
-// the batched layers at once, the head runs on each position until the first prediction that
-// differs from the draft, the matching draft tokens are emitted, and the caches keep only their
+// the batched layers at once, the head runs over the positions (up to kHeadBatchMax per launch, the
+// table read once per launch) until the first prediction that differs from the draft, the
+// matching draft tokens are emitted, and the caches keep only their
 // positions (the rest are overwritten later: a local ring holds window + kBatchMax slots).  The
 // emitted ids are the greedy ids of plain decoding, up to the arithmetic of the batched layers.
 int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint32_t* stop, size_t n_stop,
@@ -2025,13 +2026,31 @@ int speculate(af_session* s, const uint32_t* prompt, size_t n_prompt, const uint
         HIP_OK(hipMemcpyAsync(s->IDS.as<uint32_t>() + base, batch.data(), (size_t)T * 4, hipMemcpyHostToDevice, st),
                "draft upload");
         HIP_OK(s->enqueue_batch(base, T, nullptr), "verification pass");
-        // position i's prediction, until the first that differs from draft[i]
+        // position i's prediction, until the first that differs from draft[i]: the head over up to
+        // kHeadBatchMax positions per launch (the table read once per launch), launches stopping
+        // at the first batch that holds a difference
         size_t keep = 0;
         uint32_t predicted = 0;
-        for (uint32_t i = 0; i < T; ++i) {
-            if ((rc = head(s->DB.as<float>() + i * H, s->HB.as<float>() + i * H, predicted))) return rc;
-            if (i == draft.size() || predicted != draft[i]) break;
-            ++keep;
+        bool differs = false;
+        for (uint32_t i0 = 0; i0 < T && !differs; i0 += kHeadBatchMax) {
+            const uint32_t nv = std::min<uint32_t>(kHeadBatchMax, T - i0);
+            HeadArgs ha = s->head_args(false, false);
+            ha.in.x = s->DB.as<float>() + i0 * H;
+            ha.in.res = s->HB.as<float>() + i0 * H;
+            HIP_OK(launch_head_batch(ha, nv, (uint32_t)H, s->head_blocks, st), "verification head");
+            uint32_t res[2 * kHeadBatchMax] = {};
+            HIP_OK(hipMemcpyAsync(res, s->RESULT.p, (size_t)nv * 8, hipMemcpyDeviceToHost, st), "head results");
+            HIP_OK(hipStreamSynchronize(st), "verification head");
+            for (uint32_t j = 0; j < nv; ++j) {
+                if (res[2 * j + 1]) return fail(AF_ERR_NONFINITE, "non-finite logits or invalid greedy id");
+                predicted = res[2 * j];
+                const uint32_t i = i0 + j;
+                if (i == draft.size() || predicted != draft[i]) {
+                    differs = true;
+                    break;
+                }
+                ++keep;
+            }
         }
         size_t emitted = 0;
         for (; emitted < keep; ++emitted) {

@@ -539,6 +539,240 @@ hipError_t launch_head(const HeadArgs& a, int in_kind, uint32_t grid, hipStream_
     return hipGetLastError();
 }
 
+// ---- the head over several hidden states (speculative verification) ----------------------------
+//
+// q6_head_kernel's record loop with NV input vectors: vector v is a.in with x and res advanced by
+// v vstride floats (the batched layers' rows), the same norms, no residual output and no logits.
+// The table is read once: each record's codes are unpacked once and fed to one MFMA per vector
+// and k-block.  Vector v's greedy id and non-finite flag go to a.result[2 v], a.result[2 v + 1].
+// LDS: xs [K] f32 (each vector's input stage in turn), then per vector its digit planes
+// [K / 16][4][16] and table [K / 16].  a.partial holds NV entries per workgroup.
+template <int NV>
+__global__ __launch_bounds__(512) void q6_head_batch_kernel(HeadArgs a, uint32_t vstride) {
+    extern __shared__ __align__(16) uint8_t hl[];
+    __shared__ double red[16];
+    __shared__ float wv[8][NV];
+    __shared__ uint32_t wi[8][NV], wb[8][NV];
+    __shared__ bool last;
+    __shared__ uint4 zero_blk[2];
+
+    const uint32_t K = a.w.units * 64, sb = K / 256, rows = a.w.rows, ntiles = (rows + 15) / 16;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    const uint32_t nw = gridDim.x * (blockDim.x / 64), gw = blockIdx.x * (blockDim.x / 64) + wave;
+    float* xs = reinterpret_cast<float*>(hl);
+    uint8_t* const img0 = hl + (size_t)K * 4;  // vector v: digits at img0 + v 5K, table 4K after them
+    if (tid < 2) zero_blk[tid] = make_uint4(0u, 0u, 0u, 0u);
+
+    const uint32_t my_tiles = gw < ntiles ? (ntiles - gw + nw - 1) / nw : 0;
+    const uint32_t total = my_tiles * sb;
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.w.t), 0, (int)(ntiles * sb * kQ6Rec), 0x00020000);
+    HeadRing hr;
+    uint32_t ft = gw, fs = 0;
+    auto fill = [&](int u) {
+        const uint32_t rec = ft < ntiles ? ft * sb + fs : 0u;
+        head_fill(hr, u, rs, rec, lane);
+        if (++fs == sb) {
+            fs = 0;
+            ft += nw;
+        }
+    };
+#pragma unroll
+    for (int u = 0; u < kHeadRing; ++u) fill(u);  // weights first: their latency overlaps the input stages
+
+#pragma unroll 1
+    for (int v = 0; v < NV; ++v) {
+        InputStage in = a.in;
+        in.x += (size_t)v * vstride;
+        in.res += (size_t)v * vstride;
+        in.x_out = nullptr;
+        input_stage<IN_RESID>(in, xs, K, red);
+        uint8_t* dig = img0 + (size_t)v * 5 * K;
+        float4* tab = reinterpret_cast<float4*>(dig + (size_t)K * 4);
+        if (tid < K / 16) {  // thread i takes group i (as q6_head_kernel)
+            float v0[8], v1[8], m = 0.0f, sum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                v0[k] = xs[16 * tid + k];
+                v1[k] = xs[16 * tid + 8 + k];
+                m = fmaxf(m, fmaxf(fabsf(v0[k]), fabsf(v1[k])));
+                sum += v0[k] + v1[k];
+            }
+            uint32_t w0[4][2], w1[4][2];
+            digit_words(v0, m, w0);
+            digit_words(v1, m, w1);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                reinterpret_cast<uint4*>(dig)[tid * 4 + t] = make_uint4(w0[t][0], w0[t][1], w1[t][0], w1[t][1]);
+            const float sc = m > 0.0f ? ldexpf(1.0f, ilogbf(m) - 5) : 0.0f;
+            tab[tid] = make_float4(ldexpf(sc, -14), ldexpf(sc, -21), -32.0f * sum, 0.0f);
+        }
+        __syncthreads();  // the image is complete, and xs free for the next vector
+    }
+
+    const uint32_t g = lane >> 4, r = lane & 15;
+    const bool aon = (r >> 2) == g;
+    const uint32_t am = aon ? 256u : 0u;
+    uint32_t a0[NV], t0[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        const uint8_t* dig = img0 + (size_t)v * 5 * K;
+        a0[v] = aon ? lds_addr(dig) + r * 16 : lds_addr(zero_blk);
+        t0[v] = lds_addr(dig + (size_t)K * 4) + g * 16;
+    }
+    float bv[NV], acc[NV];
+    uint32_t bi[NV], bad[NV];
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+        bv[v] = -INFINITY;
+        acc[v] = 0.0f;
+        bi[v] = 0xFFFFFFFFu;
+        bad[v] = 0;
+    }
+    uint32_t ct = gw, cs = 0;
+    auto record = [&](int u) {
+        float sbacc[NV];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) sbacc[v] = 0.0f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            const uint32_t wl0 = hr.code[u][(3 * kb) / 4][(3 * kb) % 4];
+            const uint32_t wl1 = hr.code[u][(3 * kb + 1) / 4][(3 * kb + 1) % 4];
+            const uint32_t wh = hr.code[u][(3 * kb + 2) / 4][(3 * kb + 2) % 4];
+            const v4i bq = q6_unpack(wl0, wl1, wh);
+            const uint32_t blk = cs * 4 + kb;
+            const float ssc = (float)(int8_t)(hr.sc[u] >> (8 * kb));
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const v4i av = lds_at<v4i>(a0[v] + blk * am);
+                const v4i d = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bq, v4i{0, 0, 0, 0}, 0, 0, 0);
+                const v4f tb = lds_at<v4f>(t0[v] + blk * 64);
+                const int I = (d[0] << 14) + (d[1] << 7) + d[2];
+                float in = fmaf((float)I, tb.x, tb.z);
+                in = fmaf((float)d[3], tb.y, in);
+                sbacc[v] = fmaf(ssc, in, sbacc[v]);
+            }
+        }
+        const float dr = h2f((uint16_t)hr.d[u]);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) acc[v] = fmaf(dr, sbacc[v], acc[v]);
+        fill(u);
+        if (++cs == sb) {
+            const uint32_t row = ct * 16 + r;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                const float val = row_total(acc[v]);
+                acc[v] = 0.0f;
+                if (lane < 16 && row < rows) {
+                    if (!isfinite(val)) bad[v] = 1;
+                    else if (better(val, row, bv[v], bi[v])) {
+                        bv[v] = val;
+                        bi[v] = row;
+                    }
+                }
+            }
+            cs = 0;
+            ct += nw;
+        }
+    };
+    for (uint32_t i = total / kHeadRing; i; --i) {
+#pragma unroll
+        for (int u = 0; u < kHeadRing; ++u) record(u);
+    }
+    const uint32_t rem = total % kHeadRing;
+#pragma unroll
+    for (int u = 0; u < kHeadRing - 1; ++u)
+        if ((uint32_t)u < rem) record(u);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // the ring's last requests (past the end) before exit
+
+    // per vector: wave, then workgroup, then grid (greatest value, smallest id on ties, any flag)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float ov = __shfl_xor(bv[v], o);
+            const uint32_t oi = __shfl_xor(bi[v], o);
+            if (better(ov, oi, bv[v], bi[v])) {
+                bv[v] = ov;
+                bi[v] = oi;
+            }
+            bad[v] |= __shfl_xor(bad[v], o);
+        }
+        if (lane == 0) {
+            wv[wave][v] = bv[v];
+            wi[wave][v] = bi[v];
+            wb[wave][v] = bad[v];
+        }
+    }
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(a.partial, 0, 0x7FFFFFFF, 0x00020000);
+    if (tid < (uint32_t)NV) {
+        const uint32_t v = tid;
+        float b = wv[0][v];
+        uint32_t id = wi[0][v], flag = wb[0][v];
+        for (uint32_t w = 1; w < blockDim.x / 64; ++w) {
+            if (better(wv[w][v], wi[w][v], b, id)) {
+                b = wv[w][v];
+                id = wi[w][v];
+            }
+            flag |= wb[w][v];
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(v4u{__float_as_uint(b), id, flag, 0u}, prs, (blockIdx.x * NV + v) * 16, 0,
+                                               kPartSC1);
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t ticket = __hip_atomic_fetch_add(a.counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        last = ticket == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last) return;
+    // the last workgroup: wave v < NV merges vector v's partials over the grid
+    if (wave < (uint32_t)NV) {
+        const uint32_t v = wave;
+        float b = -INFINITY;
+        uint32_t id = 0xFFFFFFFFu, flag = 0;
+        for (uint32_t blk = lane; blk < gridDim.x; blk += 64) {
+            const v4u p = __builtin_amdgcn_raw_buffer_load_b128(prs, (blk * NV + v) * 16, 0, kPartSC1);
+            const float pv = __uint_as_float(p.x);
+            if (better(pv, p.y, b, id)) {
+                b = pv;
+                id = p.y;
+            }
+            flag |= p.z;
+        }
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const float ov = __shfl_xor(b, o);
+            const uint32_t oi = __shfl_xor(id, o);
+            if (better(ov, oi, b, id)) {
+                b = ov;
+                id = oi;
+            }
+            flag |= __shfl_xor(flag, o);
+        }
+        if (lane == 0) {
+            a.result[2 * v] = id;
+            a.result[2 * v + 1] = flag || id >= rows;
+        }
+    }
+    if (tid == 0) __hip_atomic_store(a.counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+hipError_t launch_head_batch(const HeadArgs& a, uint32_t nv, uint32_t vstride, uint32_t grid, hipStream_t s) {
+    if (nv == 0 || nv > kHeadBatchMax || !a.result) return hipErrorInvalidValue;
+    const size_t K = (size_t)a.w.units * 64, lds = K * 4 + nv * (K * 4 + K);  // xs, then per vector planes + table
+    switch (nv) {
+        case 1: hipLaunchKernelGGL(q6_head_batch_kernel<1>, dim3(grid), dim3(512), lds, s, a, vstride); break;
+        case 2: hipLaunchKernelGGL(q6_head_batch_kernel<2>, dim3(grid), dim3(512), lds, s, a, vstride); break;
+        case 3: hipLaunchKernelGGL(q6_head_batch_kernel<3>, dim3(grid), dim3(512), lds, s, a, vstride); break;
+        case 4: hipLaunchKernelGGL(q6_head_batch_kernel<4>, dim3(grid), dim3(512), lds, s, a, vstride); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // ---- GQA decode attention ---------------------------------------------------------------------
 //
 // A flat grid of D-thread blocks over (slot, chunk), slot = token * kv_heads * query groups + KV
