@@ -235,6 +235,21 @@ def test_attention_masking_window_and_gqa_mapping_attention_rs_482(ctx, window, 
     oracle.compare(small_reference(case), out)
 
 
+@pytest.mark.parametrize("ctx,window,qh,kvh", [(31, None, 16, 8), (32, None, 16, 8), (33, None, 16, 8),
+                                              (64, None, 16, 8), (65, None, 16, 8), (481, None, 16, 8),
+                                              (497, None, 16, 8), (511, None, 16, 8), (512, None, 16, 8),
+                                              (513, None, 16, 8), (700, 500, 16, 8), (97, None, 8, 8),
+                                              (512, None, 8, 8), (97, None, 8, 2), (512, None, 8, 2)])
+def test_attention_chunk_and_short_form_boundaries(ctx, window, qh, kvh):
+    """Visible-position counts around the chunk length (32 positions) and the short form's limit
+    (at most 512 positions in at most 16 chunks, kernels.hip:launch_attention_dg: 512 takes it, 513
+    the long form), a window whose 500 visible positions take the short form after the ring has
+    wrapped, and 1, 2 and 4 query heads per KV head (attention.rs:52-111)."""
+    case = small_case(ctx, window, qh, kvh, tag="sf")
+    out, _, _ = attention_case(case)
+    oracle.compare(small_reference(case), out)
+
+
 def test_attention_large_scores_and_value_norm():
     case = small_case(300, None, 4, 2, qscale=8.0, v_norm=True, tag="big")
     out, _, _ = attention_case(case)
