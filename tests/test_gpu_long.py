@@ -37,7 +37,8 @@ def boundary_positions(n, window):
     return sorted(p for p in marks if 0 <= p < n)
 
 
-def trace_and_check(model, n, env=None, name="long"):
+def trace_and_check(model, n, env=None, name="long", step=None):
+    """step: whether the persistent step kernel is expected to run (default: without env)."""
     ids = [int(i) for i in synth.prompt_ids(n, model.vocabulary, name=name + ".ids")]
     kv_rows = model.layers[0].kv_heads * model.layers[0].head_width
     saved = {}
@@ -57,7 +58,7 @@ def trace_and_check(model, n, env=None, name="long"):
         # which path ran: the persistent step kernel reports "layers" launches, the per-operation
         # kernels their own kinds
         _, timings = s.profile(ids, 2)  # the first id comes from the traced state, the second from a step
-        assert (timings["layers"][0] > 0) == (env is None), timings["layers"]
+        assert (timings["layers"][0] > 0) == (env is None if step is None else step), timings["layers"]
     positions = boundary_positions(n, model.layers[0].window)
     print(f"{name}: n={n}, checking positions {positions}", flush=True)
     ratio, ulps, differ = oracle.check_layer_stack(model, ids, outputs, kv, threads=THREADS, positions=positions)
@@ -74,6 +75,15 @@ def trace_and_check(model, n, env=None, name="long"):
 def test_step_kernel_long_trace_teacher_forced(q_heads, kv_heads, window, n):
     model = long_model(q_heads, kv_heads, window, name=f"long{q_heads}x{kv_heads}")
     trace_and_check(model, n, name=f"step-{q_heads}x{kv_heads}")
+
+
+def test_step_kernel_memory_side_exchange_teacher_forced():
+    """The BASELINE geometry on the step kernel without its XCD-local exchange (AF_STEP_XCD_LOCAL=0,
+    read at session open: the kernel that runs when a launch's workgroups do not reach the XCDs in
+    turn), so the qkv rows, the chunk partials and the merge tickets go through the memory side;
+    multi-chunk merges and the ring's wrap at 256, teacher-forced."""
+    model = long_model(16, 8, 256, name="longmem")
+    trace_and_check(model, 600, env={"AF_STEP_XCD_LOCAL": "0"}, name="step-mem", step=True)
 
 
 def test_step_kernel_trace_past_8192_positions_teacher_forced():
