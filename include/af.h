@@ -237,9 +237,10 @@ typedef struct af_session af_session;
  * head with greedy selection) and the prefill step (the layers alone) as HIP graphs, replayed
  * once per token (crates/cuda-backend/src/stack.rs:1100-1145 captures its layers the same way).
  * Layers outside the persistent step kernel's limits (Gemma 4's 512-wide global layers) run on
- * the per-operation kernels inside the same graph, between one step-kernel launch per run of the
- * other layers.  With AF_DISABLE_GRAPHS set in the environment the steps are launched directly
- * instead. */
+ * the per-operation kernels, between one step-kernel launch per run of the other layers; such a
+ * session launches its steps directly (no graph: the same rate, measured).  A model with no layer
+ * the step kernel takes runs on the per-operation kernels alone, captured as graphs.  With
+ * AF_DISABLE_GRAPHS set in the environment every session launches its steps directly. */
 int af_session_open(const af_layer_weights* layers, uint32_t n_layers, const af_output_head* head,
                     uint32_t capacity, af_session** out);
 /* GenerationSession::generate / generate_stream (stack.rs:1171-1386): prompt must extend the
