@@ -303,7 +303,13 @@ struct StepLayer {
     uint16_t *kcache, *vcache;  // fp16 [kv_heads][ring][256]
     float input_eps, q_eps, k_eps, v_eps, post_attn_eps, ffn_eps, post_ffn_eps, layer_scale, scale;
     uint32_t q_heads, kv_heads, qn, kn, v_off, ring, window, v_norm;
+    uint32_t chunks_max;  // attention chunks per KV head at most (StepArgs::cmax, or kStepWindowChunks)
 };
+
+// A windowed layer whose window fits this many staged chunks (StepArgs::stage_clen tokens each)
+// splits its visible range into at most this many: past a few hundred positions half the grid
+// then has no attention item and prefetches the gate/up records meanwhile.
+constexpr uint32_t kStepWindowChunks = 16;
 
 struct StepArgs {
     const StepLayer* layers;

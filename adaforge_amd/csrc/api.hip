@@ -1660,6 +1660,8 @@ int setup_step(af_session& s) {
         t.ring = L.ring;
         t.window = L.window;
         t.v_norm = L.v_norm ? 1u : 0u;
+        t.chunks_max =
+            L.window && L.window <= kStepWindowChunks * s.step_stage_clen ? std::min(cm, kStepWindowChunks) : cm;
     }
     if ((rc = dev_upload(s.STEP_LAYERS, table.data(), table.size() * sizeof(StepLayer), "layer table"))) return rc;
     // the o-proj input image is handed over as tagged pieces: 16 bytes per 8-byte image word

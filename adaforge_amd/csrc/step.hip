@@ -1241,7 +1241,8 @@ __device__ __forceinline__ Gemv describe(const StepArgs& a, uint32_t l, uint32_t
 }
 
 // Attention work of a layer at position pos: chunks of at least kAttnMinChunk tokens, at most
-// grid / kv_heads per KV head; item i runs on workgroup grid - 1 - i.
+// StepLayer::chunks_max per KV head (cmax: the chunk partials' stride per KV head); item i runs on
+// workgroup grid - 1 - i.
 struct AttnGeo {
     uint32_t start, chunks, clen, cmax, items;
 };
@@ -1251,7 +1252,7 @@ __device__ __forceinline__ AttnGeo attn_geo(CLayer& L, uint32_t pos, uint32_t cm
     const uint32_t nvis = L.window ? min(pos + 1, L.window) : pos + 1;
     g.start = pos + 1 - nvis;
     g.cmax = cmax;
-    uint32_t chunks = min(g.cmax, (nvis + kAttnMinChunk - 1) / kAttnMinChunk);
+    uint32_t chunks = min(L.chunks_max, (nvis + kAttnMinChunk - 1) / kAttnMinChunk);
     g.clen = (nvis + chunks - 1) / chunks;
     g.chunks = (nvis + g.clen - 1) / g.clen;
     g.items = L.kv_heads * g.chunks;
