@@ -4,8 +4,8 @@
 (crates/application/src/lib.rs:28-187) and `HipGenerationSession` the
 `GenerationSession` port (lib.rs:1092-1126), with the reference's names,
 argument meanings and error behaviour (errors raise AfError, the
-DiagnosticError of lib.rs:17-25).  The Rust FFI crate a maintainer adds binds
-the same entry points.
+DiagnosticError of lib.rs:17-25).  A Rust FFI crate on the reference's side
+binds the same entry points, declared in include/af.h.
 
 The reference backend compares GPU results against the domain crate's CPU
 references inside check_matvec/check_rms_norm.  Here those references are

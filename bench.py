@@ -517,7 +517,7 @@ def main():
         return
     if a.gpus != 1:
         print(f"bench.py measures one GPU: the batch-1 decode path runs on a single MI355X "
-              f"(--gpus {a.gpus} is not supported; DESIGN.md describes how the path would shard)", file=sys.stderr)
+              f"(--gpus {a.gpus} is not supported: one process, one GPU)", file=sys.stderr)
         sys.exit(2)
     if a.steps < 1 or a.warmup < 1:
         sys.exit("--steps and --warmup must be >= 1")
