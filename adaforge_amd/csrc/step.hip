@@ -1406,7 +1406,9 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 attention_item<GQ, XL>(L, a, pos, h, c, ag.chunks, ag.cmax, ag.clen, ag.start, tag0 + l, lds, &att_flag,
                                        &poll_bad, g);
             else if (wave != 0)
-                prefetch_records(r, pf_sink, lane);  // waited for in the o-proj stage (poll_image)
+                prefetch_records(r, pf_sink, lane);
+            // the barrier's workgroup fence waits for every LDS write of the workgroup, so the
+            // prefetch's DMAs (into pf_sink) complete here, before the o-proj stage
             __syncthreads();
             if (__builtin_amdgcn_readfirstlane(poll_bad)) {
                 failed = true;
