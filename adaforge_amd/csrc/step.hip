@@ -426,7 +426,8 @@ __device__ __forceinline__ void signal_done(uint32_t* done) {
 }
 
 // Consumes this wave's records of a GEMV phase (fe = the workgroup's flattened super-tiles), leaves
-// its partials in part and signals `done`.  img: the phase's digit image in LDS.
+// its partials in part and signals `done`.  img: the phase's digit image in LDS.  The ring arrives
+// with its next record in slot 0 (the caller rotated it at the end of the previous phase).
 // * When the ring holds every record of the phase, they are consumed first and the slots are
 //   refilled after the signal: a refill cannot issue while the memory system is saturated, and
 //   that wait then delays neither the records nor the phase's epilogue.
@@ -437,7 +438,6 @@ __device__ __forceinline__ void consume_phase(Ring& r, uint32_t nst, uint32_t T,
                                               const LaneK& lk, uint32_t* done) {
     if (wave - 1 >= fe) return;
     wait_vm();  // every record in flight was requested before this phase began
-    ring_rotate(r);
     const __amdgpu_buffer_rsrc_t rs = ring_rsrc(r);
     r.soff = __builtin_amdgcn_readfirstlane(r.soff);
     const uint32_t total = (fe - (wave - 1) + 6) / 7;
@@ -1442,6 +1442,10 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 // included) before the next phase's first LDS read
                 if (pre_now || kind == P_QKV) norms_pre_part<GQ, XL>(a, ph + 1, n_phases, pos, lds, wave, lane);
                 wait_vm();
+                // the ring's next record into slot 0 now, while the wave waits for the next phase's
+                // inputs, rather than at that phase's start, where the moves would delay its first fold
+                ring_rotate(r);
+                r.slot = 0;
                 if (wave == 1 && kind == P_QKV && ph + 1 < n_phases) {  // next: this layer's attention
                     CLayer& L = layer_at(a, l);
                     const AttnGeo ag = attn_geo(L, pos, a.cmax);
