@@ -369,10 +369,12 @@ struct Cursor {
 
 __device__ __forceinline__ Cursor cursor_start(uint32_t nst, uint32_t T, uint32_t wave) {
     Cursor c;
-    const uint32_t f = wave - 1, seg = f / nst, dseg = 7 / nst;
+    const uint32_t f = wave - 1;
+    // f < 7: with 8 or more super-tiles per run (every phase of the models here) no division
+    const uint32_t seg = nst >= 8 ? 0u : f / nst, dseg = nst >= 8 ? 0u : 7 / nst;
     const uint32_t pstep = T == 1 ? kMaxT * 8 * 16 : 8 * 16;  // one (k, ts) further; T is 1 or 4
     c.nst = nst;
-    c.dst = 7 % nst;
+    c.dst = nst >= 8 ? 7u : 7 % nst;
     c.pstep0 = dseg * pstep;
     c.pstep1 = (dseg + 1) * pstep;
     c.end0 = dseg != 0;
@@ -1267,7 +1269,7 @@ __device__ __forceinline__ bool attn_item(const AttnGeo& ag, uint32_t& h, uint32
     if constexpr (XL) {
         const uint32_t b = blockIdx.x;
         h = b % kXcds;
-        c = gridDim.x / kXcds - 1 - b / kXcds;
+        c = 256u / kXcds - 1 - b / kXcds;  // the XCD-local layout's grid
         return c < ag.chunks && h * ag.chunks < ag.items;
     } else {
         const uint32_t item = gridDim.x - 1 - blockIdx.x;
@@ -1353,6 +1355,8 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
 
     if (a.state[ST_STOP]) return;  // uniform: written only before the launch
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+    // the XCD-local layout runs on exactly 256 workgroups (setup_step): a constant then
+    const uint32_t grid = XL ? 256u : gridDim.x;
     const uint32_t pos = a.state[ST_POS];
     const uint32_t tag0 = a.state[ST_EPOCH] * a.tag_stride + 1u + a.tag_base;  // never 0, a cleared pair's tag
     Grid g{a.bar, 0u, 0u, &ok_flag, a.clock};
@@ -1434,7 +1438,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
             // Each role's code up to its last global access of the phase is one branch, so the
             // compiler's wait model never mixes wave 0's copies into the streaming waves'.
             if (wave != 0) {
-                const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
+                const uint32_t fe = step_units(d.sh.units, blockIdx.x, grid) * d.sh.T * nst;
                 consume_phase(r, nst, d.sh.T, __builtin_amdgcn_readfirstlane(fe), lds,
                               reinterpret_cast<const v4i*>(zero_blk), part, wave, lane, lk, &done_cnt);
                 // waited for here, so that no LDS copy is pending at the loop's back edge: the
@@ -1462,7 +1466,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 }
                 stamp(g, M_PRE);
                 // the streaming waves with records (wave - 1 < fe) have left their partials in part
-                const uint32_t fe = step_units(d.sh.units, blockIdx.x, gridDim.x) * d.sh.T * nst;
+                const uint32_t fe = step_units(d.sh.units, blockIdx.x, grid) * d.sh.T * nst;
                 // a residual prologue's row factor (1 for an input given as a digit image), while the
                 // streaming waves consume: the wave sums it adds are in red since the digits barrier
                 const double rn = d.in_kind < S_DIGITS ? norm_factor(red, d.K, d.in.eps_n) : 1.0;
@@ -1472,14 +1476,14 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                 done_cnt = 0;  // next incremented after the next phase's stage barrier
                 stamp(g, M_STREAMED);
                 if (!pre_now) phase_pre<GQ, XL>(a, ph + 1, n_phases, pos, lds, lane);
-                const uint32_t mu = step_units(d.sh.units, blockIdx.x, gridDim.x);
+                const uint32_t mu = step_units(d.sh.units, blockIdx.x, grid);
                 if (d.y || d.yt) {
                     if (tid < 16 * mu) {
                         const uint32_t k = tid >> 4, rr = tid & 15;
-                        uint32_t tile = blockIdx.x + k * gridDim.x;
+                        uint32_t tile = blockIdx.x + k * grid;
                         if (XL && kind == P_QKV) {
                             CLayer& L = layer_at(a, l);
-                            tile = step_qkv_tile(blockIdx.x, k, gridDim.x, 1u, L.qn / 16, L.kn / 16);
+                            tile = step_qkv_tile(blockIdx.x, k, grid, 1u, L.qn / 16, L.kn / 16);
                         }
                         const uint32_t row = tile * 16 + rr;
                         const float y = (float)(rn * (double)part_sum(part, k, 0, rr));
@@ -1505,7 +1509,7 @@ __global__ __launch_bounds__(512) void decode_step_kernel(StepArgs a) {
                         float v[8];
 #pragma unroll
                         for (int e = 0; e < 8; ++e) v[e] = act_l[k][8 * p + e];
-                        quad_digits_store(v, a.act_img, d.act_nst, blockIdx.x + k * gridDim.x, p);
+                        quad_digits_store(v, a.act_img, d.act_nst, blockIdx.x + k * grid, p);
                     }
                 }
                 wait_vm();
