@@ -526,16 +526,40 @@ __device__ __forceinline__ bool poll_tagged(const uint32_t* src, uint32_t K, uin
 }
 
 // A digit image handed over without a grid barrier: its 8-byte word i (bytes lo, hi) is the
-// 16-byte piece (lo, tag, hi, tag) at 16 i of the tagged image.  Wave w copies the pieces of copy
-// chunks j = w, w + 8, .. (64 pieces each) into LDS staging stg + 1024 j, re-copies the chunks'
-// pieces whose tags are not yet current, and writes a current piece's word to the image in LDS.
-// Returns false (in the whole wave) if its pieces did not become current within the spin limit.
+// 16-byte piece (lo, tag, hi, tag) at 16 i of the tagged image.  Wave w polls the pieces of chunks
+// j = w, w + 8, .. (64 pieces each, piece j 64 + lane in lane `lane`), re-reads the pieces whose
+// tags are not yet current, and writes a current piece's word to the image in LDS.  Up to 6 chunks
+// per wave the pieces are loaded into registers; a larger image goes through LDS staging
+// stg + 1024 j (one DMA per chunk), which costs an LDS round trip per poll.  Returns false (in the
+// whole wave) if its pieces did not become current within the spin limit.
 __device__ __forceinline__ bool poll_image(const uint32_t* src, uint32_t bytes, uint32_t tag, uint8_t* img, uint8_t* stg,
                                            uint32_t wave, uint32_t lane) {
     const uint32_t n = bytes / 8, nj = (n + 63) / 64;
     uint32_t need = 0;
     for (uint32_t i = 0, j = wave; j < nj; ++i, j += 8)
         if (j * 64 + lane < n) need |= 1u << i;
+    if (nj <= 8 * 6) {
+        const __amdgpu_buffer_rsrc_t rs = rsrc(src);
+        for (uint32_t spins = 0;; ++spins) {
+            v4u v[6];
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                v[i] = v4u{0u, 0u, 0u, 0u};
+                if (need >> i & 1)
+                    v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, ((wave + 8 * i) * 64 + lane) * 16, 0, kSC1);
+            }
+#pragma unroll
+            for (int i = 0; i < 6; ++i) {
+                if ((need >> i & 1) && v[i].y == tag && v[i].w == tag) {
+                    *reinterpret_cast<v2u*>(img + ((wave + 8 * i) * 64 + lane) * 8) = v2u{v[i].x, v[i].z};
+                    need &= ~(1u << i);
+                }
+            }
+            if (__builtin_amdgcn_ballot_w64(need != 0) == 0) return true;
+            if (spins >= kPollLimit) return false;
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
     for (uint32_t spins = 0;; ++spins) {
         for (uint32_t i = 0, j = wave; j < nj; ++i, j += 8)
             if (need >> i & 1)
