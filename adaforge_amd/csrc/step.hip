@@ -1654,7 +1654,8 @@ size_t step_lds_bytes(uint32_t hidden, uint32_t inter, uint32_t q_dim, uint32_t 
 // would end in the barriers' spin limit, reported as a failed step, not in a hang.  The
 // cooperative launch API gives the same residency and costs about 12 us more per launch.
 hipError_t launch_step(const StepArgs& a, uint32_t group, uint32_t grid, size_t lds, hipStream_t s) {
-    if (a.xcd_local && group != 2) return hipErrorInvalidValue;
+    // the XCD-local instance is compiled for its 256-workgroup grid (setup_step checks both)
+    if (a.xcd_local && (group != 2 || grid != 256)) return hipErrorInvalidValue;
     switch (group) {
         case 1: hipLaunchKernelGGL((decode_step_kernel<1, false>), dim3(grid), dim3(kThreads), lds, s, a); break;
         case 2:
