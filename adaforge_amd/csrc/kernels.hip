@@ -281,7 +281,7 @@ __device__ __forceinline__ bool better(float v, uint32_t i, float bv, uint32_t b
 // record.  Input x_j ~ s (q0 + q1 2^-7 + q2 2^-14 + q3 2^-21) per 16-element group (s = 2^(e - 5),
 // e = ilogb of the group's max |x|): exact for |x_j| >= 2^(e - 3), otherwise within 2^(e - 27).
 
-constexpr int kHeadRing = 6;  // records in flight per wave
+constexpr int kHeadRing = 4;  // records in flight per wave (4, 6 and 8 within 1.3 % of one another)
 
 // A wave's head state: its ring of records and its position in its tile sequence.
 struct HeadRing {

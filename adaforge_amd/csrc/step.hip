@@ -271,7 +271,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t ring_rsrc(const Ring& r) {
 // Cache, so the wave's own ring loads of it later return at cache latency, while HBM would
 // otherwise idle; moving every byte to the CU instead (1 KB per instruction) cost 32 times the
 // cache-to-CU traffic and 8 times the instructions for the same gain.
-constexpr uint32_t kPrefetchRecords = 32;
+constexpr uint32_t kPrefetchRecords = 30;
 constexpr uint32_t kPrefetchLine = 128;
 static_assert((kRing + kPrefetchRecords) * kStepRecord <= kStepStreamPad, "stream padding below the prefetch");
 
